@@ -1,0 +1,87 @@
+// Shared host/device helpers for the EXL3 grouped prefill library (gfx950 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string>
+
+#include "../../include/exl3_grouped.h"
+
+namespace exl3 {
+
+// ------------------------------------------------------------------------------------------- host errors
+// One message per calling thread; entry points return EXL3_OK / EXL3_ERR_ARG / EXL3_ERR_HIP and leave the
+// text in here, where exl3_last_error() reads it.
+std::string& last_error();
+
+inline int fail(const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    last_error() = buf;
+    return EXL3_ERR_ARG;
+}
+
+inline int hip_status(const char* what)
+{
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+    {
+        last_error() = std::string(what) + ": " + hipGetErrorString(e);
+        return EXL3_ERR_HIP;
+    }
+    return EXL3_OK;
+}
+
+#define EXL3_CHECK(cond, ...) do { if (!(cond)) return ::exl3::fail(__VA_ARGS__); } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ------------------------------------------------------------------------------------------- device helpers
+constexpr float HAD_SCALE = 0.088388347648f;     // 1/sqrt(128)
+constexpr int MAX_EXPERTS = 1024;
+
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+// Lane exchange within 32-lane groups: value of lane (lane ^ M).
+template <int M>
+__device__ __forceinline__ float xor_lane(float v)
+{
+    const int i = __float_as_int(v);
+    int r;
+    if constexpr (M == 1)
+        r = __builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false);       // quad_perm [1,0,3,2]
+    else if constexpr (M == 2)
+        r = __builtin_amdgcn_update_dpp(0, i, 0x4E, 0xF, 0xF, false);       // quad_perm [2,3,0,1]
+    else
+        r = __builtin_amdgcn_ds_swizzle(i, 0x1F | (M << 10));              // bitmask mode: xor M
+    return __int_as_float(r);
+}
+
+// One Walsh-Hadamard butterfly stage across lanes: v' = v + partner on the lower lane, partner - v on the upper.
+template <int M>
+__device__ __forceinline__ float lane_butterfly(float v, int lane)
+{
+    const float p = xor_lane<M>(v);
+    return (lane & M) ? (p - v) : (v + p);
+}
+
+// XCD-aware workgroup order: workgroups are handed to the 8 XCDs round robin by dispatch id, so dispatch id
+// i runs on XCD i % 8. Map it to (group, slot) such that every slot of one group lands on the same XCD
+// (they share an activation tile through that XCD's L2) and groups interleave over XCDs.
+// Requires the grid to be padded to a multiple of 8 groups.
+__device__ __forceinline__ void xcd_group_slot(int id, int slots, int& group, int& slot)
+{
+    const int xcd = id & 7;
+    const int j = id >> 3;
+    slot = j % slots;
+    group = (j / slots) * 8 + xcd;
+}
+
+}  // namespace exl3

@@ -1,0 +1,162 @@
+// Row Hadamard passes of the grouped prefill:
+//   row_had (kernel/exl3_grouped_prefill.cu:101-115): dst[r] = fp16(H128(src[tok_r or r] * suh[e_r]) / sqrt(128))
+//   act_had (kernel/exl3_grouped_prefill.cu:118-141): act[r] = fp16(H128(fp16(silu(min(g,L)) * clamp(u,+-L)) * suh_down[e_r]) / sqrt(128))
+// Both are HBM-bound. A lane owns 8 consecutive columns (one 16-byte load and store) of a 128-column block,
+// 16 lanes own a block: 3 butterfly stages run in registers, 4 across lanes (DPP / ds_swizzle), fp32 inside.
+// A wave covers 4 (row, block) pairs per step; workgroups stride over all pairs.
+#include "exl3_common.h"
+
+namespace exl3 {
+namespace {
+
+constexpr int HAD_THREADS = 256;
+constexpr int PAIRS_PER_WG = HAD_THREADS / 16;
+
+__device__ __forceinline__ void unpack8(const uint4 v, float (&x)[8])
+{
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) { x[2 * i] = h2f(w[i] & 0xFFFF); x[2 * i + 1] = h2f(w[i] >> 16); }
+}
+
+__device__ __forceinline__ uint4 pack8(const float (&x)[8])
+{
+    uint32_t w[4];
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = (uint32_t) f2h(x[2 * i]) | ((uint32_t) f2h(x[2 * i + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// H128 over 8 values per lane x 16 lanes (index = 8 (lane & 15) + i), scaled by 1/sqrt(128).
+__device__ __forceinline__ void had128_lane8(float (&x)[8], int lane)
+{
+    #pragma unroll
+    for (int len = 1; len < 8; len <<= 1)
+        #pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (!(i & len)) { const float a = x[i], b = x[i + len]; x[i] = a + b; x[i + len] = a - b; }
+    #pragma unroll
+    for (int i = 0; i < 8; ++i)
+    {
+        float v = x[i];
+        v = lane_butterfly<1>(v, lane);
+        v = lane_butterfly<2>(v, lane);
+        v = lane_butterfly<4>(v, lane);
+        v = lane_butterfly<8>(v, lane);
+        x[i] = v * HAD_SCALE;
+    }
+}
+
+template <bool GATHER>
+__global__ __launch_bounds__(HAD_THREADS)
+void row_had_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, const int64_t* __restrict__ token_sorted,
+                    const int32_t* __restrict__ expert_of_row, const uint16_t* __restrict__ suh, int64_t suh_stride,
+                    int64_t rows, int K)
+{
+    const int blocks = K / 128;
+    const int64_t n_pairs = rows * blocks;
+    const int lane = threadIdx.x & 63;
+    const int sub = threadIdx.x >> 4;                        // pair slot in the workgroup
+    const int col = 8 * (lane & 15);
+    for (int64_t pr = (int64_t) blockIdx.x * PAIRS_PER_WG + sub; pr - sub < n_pairs;
+         pr += (int64_t) gridDim.x * PAIRS_PER_WG)
+    {
+        const bool ok = pr < n_pairs;                        // lanes past the end still join the shuffles
+        const int64_t prc = ok ? pr : n_pairs - 1;
+        const int64_t r = prc / blocks;
+        const int blk = (int) (prc - r * blocks);
+        const int64_t srow = GATHER ? token_sorted[r] : r;
+        const int e = expert_of_row[r];
+        const uint4 xv = *reinterpret_cast<const uint4*>(src + srow * K + blk * 128 + col);
+        const uint4 sv = *reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + blk * 128 + col);
+        float x[8], s[8];
+        unpack8(xv, x);
+        unpack8(sv, s);
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] *= s[i];
+        had128_lane8(x, lane);
+        if (ok) *reinterpret_cast<uint4*>(dst + r * K + blk * 128 + col) = pack8(x);
+    }
+}
+
+__global__ __launch_bounds__(HAD_THREADS)
+void act_had_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ act, const int32_t* __restrict__ expert_of_row,
+                    const uint16_t* __restrict__ suh, int64_t suh_stride, int64_t rows, int I, float limit)
+{
+    const int blocks = I / 128;
+    const int64_t n_pairs = rows * blocks;
+    const int lane = threadIdx.x & 63;
+    const int sub = threadIdx.x >> 4;
+    const int col = 8 * (lane & 15);
+    for (int64_t pr = (int64_t) blockIdx.x * PAIRS_PER_WG + sub; pr - sub < n_pairs;
+         pr += (int64_t) gridDim.x * PAIRS_PER_WG)
+    {
+        const bool ok = pr < n_pairs;
+        const int64_t prc = ok ? pr : n_pairs - 1;
+        const int64_t r = prc / blocks;
+        const int blk = (int) (prc - r * blocks);
+        const int e = expert_of_row[r];
+        const uint16_t* g = gu + r * (2 * (int64_t) I) + blk * 128 + col;
+        const uint4 gv = *reinterpret_cast<const uint4*>(g);
+        const uint4 uv = *reinterpret_cast<const uint4*>(g + I);
+        const uint4 sv = *reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + blk * 128 + col);
+        float x[8], u[8], s[8];
+        unpack8(gv, x);
+        unpack8(uv, u);
+        unpack8(sv, s);
+        #pragma unroll
+        for (int i = 0; i < 8; ++i)
+        {
+            const float gc = fminf(x[i], limit);
+            const float uc = fminf(fmaxf(u[i], -limit), limit);
+            const float a = gc / (1.0f + __expf(-gc)) * uc;
+            x[i] = h2f(f2h(a)) * s[i];                        // fp16 rounding point of the reference
+        }
+        had128_lane8(x, lane);
+        if (ok) *reinterpret_cast<uint4*>(act + r * I + blk * 128 + col) = pack8(x);
+    }
+}
+
+unsigned had_grid(int64_t n_pairs)
+{
+    const int64_t wgs = (n_pairs + PAIRS_PER_WG - 1) / PAIRS_PER_WG;
+    return (unsigned) (wgs < 16384 ? wgs : 16384);
+}
+
+}  // namespace
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" int exl3_row_had(const uint16_t* src, uint16_t* dst, const int64_t* token_sorted, const int32_t* expert_of_row,
+                            const uint16_t* suh, int64_t suh_stride, int64_t suh_len, int64_t rows, int K, int gather,
+                            void* stream)
+{
+    EXL3_CHECK(K > 0 && K % 128 == 0 && suh_len == K, "K must be a multiple of 128 and match suh");
+    EXL3_CHECK(rows >= 0, "bad row count");
+    if (rows == 0) return EXL3_OK;
+    EXL3_CHECK(src && dst && expert_of_row && suh && (!gather || token_sorted), "null pointer");
+    EXL3_CHECK(((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(suh)) & 15) == 0
+               && suh_stride % 8 == 0, "src/dst/suh must be 16-byte aligned");
+    const unsigned grid = had_grid(rows * (K / 128));
+    hipStream_t s = as_stream(stream);
+    if (gather)
+        row_had_kernel<true><<<grid, HAD_THREADS, 0, s>>>(src, dst, token_sorted, expert_of_row, suh, suh_stride, rows, K);
+    else
+        row_had_kernel<false><<<grid, HAD_THREADS, 0, s>>>(src, dst, nullptr, expert_of_row, suh, suh_stride, rows, K);
+    return hip_status("row_had");
+}
+
+extern "C" int exl3_act_had(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
+                            const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, void* stream)
+{
+    EXL3_CHECK(I > 0 && gu_width == 2 * (int64_t) I && I % 128 == 0, "gate|up width must be 2I, I multiple of 128");
+    EXL3_CHECK(rows >= 0, "bad row count");
+    if (rows == 0) return EXL3_OK;
+    EXL3_CHECK(gu && act && expert_of_row && suh_down, "null pointer");
+    EXL3_CHECK(((reinterpret_cast<uintptr_t>(gu) | reinterpret_cast<uintptr_t>(act) | reinterpret_cast<uintptr_t>(suh_down)) & 15) == 0
+               && suh_stride % 8 == 0, "gu/act/suh must be 16-byte aligned");
+    act_had_kernel<<<had_grid(rows * (I / 128)), HAD_THREADS, 0, as_stream(stream)>>>(gu, act, expert_of_row, suh_down,
+                                                                                      suh_stride, rows, I, limit);
+    return hip_status("act_had");
+}

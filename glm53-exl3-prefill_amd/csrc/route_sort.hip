@@ -1,0 +1,282 @@
+// Route sort and block table.
+//
+// sort_routes replaces the torch glue of grouped_prefill (kernel/exl3_grouped_runtime.py:59-68: stable
+// argsort, repeat_interleave, gathers, scatter_add_, cumsum) with a stable counting sort in three launches:
+//   1. hist:    one workgroup per CHUNK of routes counts experts in LDS -> hist[chunk][e]
+//   2. offsets: one workgroup turns hist into counts[e], expert_row0[e] and per-chunk write cursors
+//   3. scatter: each chunk re-walks its routes in index order; ranks among equal ids inside a wave come from
+//      a ballot match over the id bits, across the chunk's waves from per-wave counts in LDS, so the write
+//      order is exactly the stable order.
+// build_blocks restates kernel/exl3_grouped_prefill.cu:63-96 with a parallel scan instead of the serial one.
+#include "exl3_common.h"
+
+namespace exl3 {
+namespace {
+
+constexpr int SORT_THREADS = 256;
+constexpr int SORT_WAVES = SORT_THREADS / 64;
+constexpr int ROUTES_PER_THREAD = 8;
+constexpr int CHUNK = SORT_THREADS * ROUTES_PER_THREAD;    // routes per workgroup in passes 1 and 3
+
+template <typename T>
+__device__ __forceinline__ int load_id(const void* ids, int64_t i)
+{
+    const int64_t v = (int64_t) reinterpret_cast<const T*>(ids)[i];
+    return (int) v == v ? (int) v : -1;
+}
+
+__device__ __forceinline__ int route_id(const void* ids, int ids_dtype, int64_t i, int n_experts)
+{
+    const int e = (ids_dtype == EXL3_DTYPE_I64) ? load_id<int64_t>(ids, i) : load_id<int32_t>(ids, i);
+    return (e >= 0 && e < n_experts) ? e : -1;
+}
+
+__device__ __forceinline__ uint16_t route_weight_f16(const void* w, int dtype, int64_t i)
+{
+    float f;
+    if (dtype == EXL3_DTYPE_F32) f = reinterpret_cast<const float*>(w)[i];
+    else if (dtype == EXL3_DTYPE_F16) return reinterpret_cast<const uint16_t*>(w)[i];
+    else f = __uint_as_float((uint32_t) reinterpret_cast<const uint16_t*>(w)[i] << 16);   // bf16
+    return f2h(f);
+}
+
+__global__ __launch_bounds__(SORT_THREADS)
+void sort_hist_kernel(const void* __restrict__ ids, int ids_dtype, int64_t R, int n_experts,
+                      int32_t* __restrict__ hist, int32_t* __restrict__ bad_per_chunk)
+{
+    __shared__ int32_t s_hist[MAX_EXPERTS];
+    const int t = threadIdx.x;
+    for (int e = t; e < n_experts; e += SORT_THREADS) s_hist[e] = 0;
+    __syncthreads();
+    const int64_t base = (int64_t) blockIdx.x * CHUNK;
+    int bad = 0;
+    for (int k = 0; k < ROUTES_PER_THREAD; ++k)
+    {
+        const int64_t i = base + k * SORT_THREADS + t;
+        if (i < R)
+        {
+            const int e = route_id(ids, ids_dtype, i, n_experts);
+            if (e >= 0) atomicAdd(&s_hist[e], 1);
+            else ++bad;
+        }
+    }
+    __syncthreads();
+    for (int e = t; e < n_experts; e += SORT_THREADS) hist[(int64_t) blockIdx.x * n_experts + e] = s_hist[e];
+    __shared__ int32_t s_bad;
+    if (t == 0) s_bad = 0;
+    __syncthreads();
+    if (bad) atomicAdd(&s_bad, bad);
+    __syncthreads();
+    if (t == 0) bad_per_chunk[blockIdx.x] = s_bad;
+}
+
+// Single workgroup of 1024 threads; thread e owns expert e.
+__global__ __launch_bounds__(1024)
+void sort_offsets_kernel(int32_t* __restrict__ hist, const int32_t* __restrict__ bad_per_chunk, int n_chunks,
+                         int n_experts, int32_t* __restrict__ counts, int32_t* __restrict__ expert_row0,
+                         int32_t* __restrict__ dropped)
+{
+    __shared__ int32_t s_scan[1024];
+    const int e = threadIdx.x;
+    if (e == 0)
+    {
+        int d = 0;
+        for (int b = 0; b < n_chunks; ++b) d += bad_per_chunk[b];
+        *dropped = d;
+    }
+    int c = 0;
+    if (e < n_experts)
+        for (int b = 0; b < n_chunks; ++b) c += hist[(int64_t) b * n_experts + e];
+    s_scan[e] = (e < n_experts) ? c : 0;
+    __syncthreads();
+    // Hillis-Steele inclusive scan over 1024 entries
+    for (int d = 1; d < 1024; d <<= 1)
+    {
+        const int v = (e >= d) ? s_scan[e - d] : 0;
+        __syncthreads();
+        s_scan[e] += v;
+        __syncthreads();
+    }
+    if (e < n_experts)
+    {
+        const int row0 = s_scan[e] - c;
+        counts[e] = c;
+        expert_row0[e] = row0;
+        int cur = row0;
+        for (int b = 0; b < n_chunks; ++b)
+        {
+            const int h = hist[(int64_t) b * n_experts + e];
+            hist[(int64_t) b * n_experts + e] = cur;      // becomes chunk b's first row for expert e
+            cur += h;
+        }
+    }
+}
+
+// Bitmask of the lanes of this wave whose key equals ours (only among lanes with valid keys).
+__device__ __forceinline__ uint64_t match_lanes(int key, bool valid)
+{
+    uint64_t peers = __ballot(valid);
+    #pragma unroll
+    for (int bit = 0; bit < 10; ++bit)            // keys < 1024
+    {
+        const bool b = (key >> bit) & 1;
+        const uint64_t m = __ballot(b);
+        peers &= b ? m : ~m;
+    }
+    return peers;
+}
+
+__global__ __launch_bounds__(SORT_THREADS)
+void sort_scatter_kernel(const void* __restrict__ ids, int ids_dtype, const void* __restrict__ weights, int w_dtype,
+                         int64_t R, int topk, int n_experts, const int32_t* __restrict__ cursor0,
+                         int64_t* __restrict__ token_sorted, uint16_t* __restrict__ weight_sorted,
+                         int32_t* __restrict__ expert_of_row)
+{
+    __shared__ int32_t s_cursor[MAX_EXPERTS];
+    __shared__ int32_t s_wave_cnt[SORT_WAVES][MAX_EXPERTS];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    for (int e = t; e < n_experts; e += SORT_THREADS)
+    {
+        s_cursor[e] = cursor0[(int64_t) blockIdx.x * n_experts + e];
+        for (int w = 0; w < SORT_WAVES; ++w) s_wave_cnt[w][e] = 0;
+    }
+    __syncthreads();
+    const int64_t base = (int64_t) blockIdx.x * CHUNK;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int k = 0; k < ROUTES_PER_THREAD; ++k)
+    {
+        const int64_t i = base + k * SORT_THREADS + t;
+        const int e = (i < R) ? route_id(ids, ids_dtype, i, n_experts) : -1;
+        const bool valid = e >= 0;
+        const uint64_t peers = match_lanes(valid ? e : 0, valid);
+        const int rank = __popcll(peers & below);
+        const bool leader = valid && rank == 0;
+        if (leader) s_wave_cnt[wave][e] = __popcll(peers);
+        __syncthreads();
+        if (valid)
+        {
+            int row = s_cursor[e] + rank;
+            for (int w = 0; w < wave; ++w) row += s_wave_cnt[w][e];
+            token_sorted[row] = i / topk;
+            weight_sorted[row] = route_weight_f16(weights, w_dtype, i);
+            expert_of_row[row] = e;
+        }
+        __syncthreads();
+        if (leader)
+        {
+            atomicAdd(&s_cursor[e], __popcll(peers));
+            s_wave_cnt[wave][e] = 0;
+        }
+        __syncthreads();
+    }
+}
+
+// Rows past sum(counts) (only present when routes were dropped): token 0, weight 0, expert 0.
+__global__ void sort_fill_tail_kernel(const int32_t* __restrict__ counts, const int32_t* __restrict__ expert_row0,
+                                      int n_experts, int64_t R, int64_t* __restrict__ token_sorted,
+                                      uint16_t* __restrict__ weight_sorted, int32_t* __restrict__ expert_of_row)
+{
+    const int64_t n_rows = (int64_t) expert_row0[n_experts - 1] + counts[n_experts - 1];
+    for (int64_t r = n_rows + (int64_t) blockIdx.x * blockDim.x + threadIdx.x; r < R; r += (int64_t) gridDim.x * blockDim.x)
+    {
+        token_sorted[r] = 0;
+        weight_sorted[r] = 0;
+        expert_of_row[r] = 0;
+    }
+}
+
+__global__ __launch_bounds__(1024)
+void build_blocks_kernel(const int32_t* __restrict__ counts, int n_experts, int max_blocks,
+                         int32_t* __restrict__ block_expert, int32_t* __restrict__ block_row0,
+                         int32_t* __restrict__ meta)
+{
+    __shared__ int32_t s_rows[1024];
+    __shared__ int32_t s_blks[1024];
+    const int e = threadIdx.x;
+    const int c = (e < n_experts) ? counts[e] : 0;
+    const int nb = (c + 127) / 128;
+    s_rows[e] = c;
+    s_blks[e] = nb;
+    __syncthreads();
+    for (int d = 1; d < 1024; d <<= 1)
+    {
+        const int vr = (e >= d) ? s_rows[e - d] : 0;
+        const int vb = (e >= d) ? s_blks[e - d] : 0;
+        __syncthreads();
+        s_rows[e] += vr;
+        s_blks[e] += vb;
+        __syncthreads();
+    }
+    const int row0 = s_rows[e] - c;
+    const int blk0 = s_blks[e] - nb;
+    if (e < n_experts)
+        for (int i = 0; i < nb; ++i)
+        {
+            const int b = blk0 + i;
+            if (b < max_blocks) { block_expert[b] = e; block_row0[b] = row0 + i * 128; }
+        }
+    const int n_blocks = s_blks[1023];
+    if (e == 0) { meta[0] = n_blocks; meta[1] = s_rows[1023]; }
+    for (int b = n_blocks + e; b < max_blocks; b += 1024) block_expert[b] = -1;
+}
+
+}  // namespace
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" size_t exl3_sort_routes_workspace_bytes(int64_t tokens, int topk, int n_experts)
+{
+    if (tokens < 0 || topk <= 0 || n_experts <= 0) return 0;
+    const int64_t R = tokens * topk;
+    const int64_t n_chunks = (R + CHUNK - 1) / CHUNK;
+    return (size_t) (256 + 4 * n_chunks * n_experts + 4 * n_chunks);
+}
+
+extern "C" int exl3_sort_routes(const void* topk_ids, int ids_dtype, const void* topk_weights, int weights_dtype,
+                                int64_t tokens, int topk, int n_experts,
+                                int64_t* token_sorted, uint16_t* weight_sorted, int32_t* expert_of_row,
+                                int32_t* counts, int32_t* expert_row0,
+                                void* workspace, size_t workspace_bytes, void* stream)
+{
+    EXL3_CHECK(ids_dtype == EXL3_DTYPE_I64 || ids_dtype == EXL3_DTYPE_I32, "topk_ids must be int64 or int32");
+    EXL3_CHECK(weights_dtype == EXL3_DTYPE_F32 || weights_dtype == EXL3_DTYPE_F16 || weights_dtype == EXL3_DTYPE_BF16,
+               "topk_weights must be float32, float16 or bfloat16");
+    EXL3_CHECK(tokens >= 0 && topk > 0, "bad routing shape");
+    EXL3_CHECK(n_experts > 0 && n_experts <= MAX_EXPERTS, "too many experts");
+    const int64_t R = tokens * topk;
+    EXL3_CHECK(R < (int64_t) 1 << 31, "too many routes");
+    const size_t need = exl3_sort_routes_workspace_bytes(tokens, topk, n_experts);
+    EXL3_CHECK(workspace != nullptr && workspace_bytes >= need, "sort workspace too small (%zu < %zu bytes)",
+               workspace_bytes, need);
+    EXL3_CHECK(counts && expert_row0, "null output pointer");
+    EXL3_CHECK(R == 0 || (topk_ids && topk_weights && token_sorted && weight_sorted && expert_of_row),
+               "null pointer");
+    hipStream_t s = as_stream(stream);
+    int32_t* dropped = reinterpret_cast<int32_t*>(workspace);
+    int32_t* hist = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + 256);
+    const int n_chunks = (int) ((R + CHUNK - 1) / CHUNK);
+    int32_t* bad = hist + (int64_t) n_chunks * n_experts;
+    if (n_chunks > 0)
+        sort_hist_kernel<<<n_chunks, SORT_THREADS, 0, s>>>(topk_ids, ids_dtype, R, n_experts, hist, bad);
+    sort_offsets_kernel<<<1, 1024, 0, s>>>(hist, bad, n_chunks, n_experts, counts, expert_row0, dropped);
+    if (n_chunks > 0)
+    {
+        sort_scatter_kernel<<<n_chunks, SORT_THREADS, 0, s>>>(topk_ids, ids_dtype, topk_weights, weights_dtype, R, topk,
+                                                              n_experts, hist, token_sorted, weight_sorted, expert_of_row);
+        sort_fill_tail_kernel<<<64, 256, 0, s>>>(counts, expert_row0, n_experts, R, token_sorted, weight_sorted,
+                                                 expert_of_row);
+    }
+    return hip_status("sort_routes");
+}
+
+extern "C" int exl3_build_blocks(const int32_t* counts, int n_experts, int max_blocks,
+                                 int32_t* block_expert, int32_t* block_row0, int32_t* meta, void* stream)
+{
+    EXL3_CHECK(n_experts >= 0 && n_experts <= MAX_EXPERTS, "too many experts");
+    EXL3_CHECK(max_blocks >= 0, "bad max_blocks");
+    EXL3_CHECK(counts && meta && (max_blocks == 0 || (block_expert && block_row0)), "null pointer");
+    build_blocks_kernel<<<1, 1024, 0, as_stream(stream)>>>(counts, n_experts, max_blocks, block_expert, block_row0,
+                                                           meta);
+    return hip_status("build_blocks");
+}

@@ -1,0 +1,114 @@
+// Trellis tile decode for gfx950.
+//
+// A 16x16 tile is 256 positions; position p's 16-bit state is the window of stream bits
+// [(p+1)K - 16, (p+1)K) (mod 256K) of the tile's little-endian dword stream, its first bit as bit 0.
+// decode(state): x = state * 0xCBAC1FED mod 2^32; y = (x & 0x8FFF8FFF) ^ 0x3B603B60;
+//                w = fp16(y.lo16) + fp16(y.hi16)  (one fp16 add).
+// A lane decodes one chunk: the 8 positions p = 8c + j (c = chunk 0..31, j = 0..7), which sit at tile rows
+// k = 2(c & 3) + (j & 1) + 8((j >> 1) & 1) and columns n = (c >> 2) + 8(j >> 2).
+//
+// gfx950 cost per weight: the 32-bit multiply by a 16-bit state is split into a 16x16 low-half multiply whose
+// result lands in the upper word (SDWA) plus a 16x16+32 multiply-add that picks the state's half by op_sel,
+// so no state ever needs shifting out of its dword; v_bitop3 does mask-and-xor in one op, and two SDWA fp16
+// adds write the packed result pair. About 4.4 VALU ops per weight at 4 bits.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace exl3 {
+
+constexpr uint32_t MCG_MUL_LO = 0x1FEDu;       // low 16 bits of 0xCBAC1FED
+constexpr uint32_t MCG_MUL_HI = 0xCBACu;       // high 16 bits
+constexpr uint32_t MCG_XOR = 0x3B603B60u;
+constexpr uint32_t MCG_MASK = 0x8FFF8FFFu;
+
+// x = s * 0xCBAC1FED (mod 2^32) where s = low (HI = 0) or high (HI = 1) 16 bits of r.
+template <int HI>
+__device__ __forceinline__ uint32_t mcg_mul(uint32_t r)
+{
+    uint32_t t, x;
+    const uint32_t chi = MCG_MUL_HI, clo = MCG_MUL_LO;
+    if constexpr (HI == 0)
+        asm("v_mul_lo_u16_sdwa %0, %2, %3 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD\n\t"
+            "v_mad_u32_u16 %1, %2, %4, %0"
+            : "=&v"(t), "=v"(x) : "v"(r), "v"(chi), "v"(clo));
+    else
+        asm("v_mul_lo_u16_sdwa %0, %2, %3 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:DWORD\n\t"
+            "v_mad_u32_u16 %1, %2, %4, %0 op_sel:[1,0,0,0]"
+            : "=&v"(t), "=v"(x) : "v"(r), "v"(chi), "v"(clo));
+    return x;
+}
+
+__device__ __forceinline__ uint32_t mcg_mask(uint32_t x) { return (x & MCG_MASK) ^ MCG_XOR; }
+
+// Packed fp16 pair {fp16(ya.lo + ya.hi), fp16(yb.lo + yb.hi)} (first in the low half).
+__device__ __forceinline__ uint32_t add_halves_pair(uint32_t ya, uint32_t yb)
+{
+    uint32_t w;
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+        : "=&v"(w) : "v"(ya), "v"(yb));
+    return w;
+}
+
+// Decoded chunk, as four packed fp16 pairs ordered for a [n][k] (k-contiguous) destination:
+//   out[0] = (k0, k0+1) at column n0, out[1] = (k0+8, k0+9) at n0, out[2] = (k0, k0+1) at n0+8,
+//   out[3] = (k0+8, k0+9) at n0+8, with k0 = 2(c & 3), n0 = c >> 2.
+struct Chunk4 { uint32_t w[4]; };
+
+// Per-lane constants locating chunk c's bits: the two dwords (lo, hi) holding them and the bit offset of the
+// window of position 8c inside the 64-bit value hi:lo.
+struct ChunkLoc { int dlo, dhi, off; };
+
+template <int BITS>
+__device__ __forceinline__ ChunkLoc chunk_loc(int c)
+{
+    constexpr int NDW = 8 * BITS;                          // dwords per tile
+    const int b0 = 8 * c * BITS + BITS - 16;               // first stream bit of position 8c's window
+    const int d0 = (b0 >= 0) ? (b0 >> 5) : -1;            // floor(b0 / 32), b0 >= -15
+    ChunkLoc L;
+    L.off = b0 - 32 * d0;
+    L.dlo = (d0 + NDW) % NDW;
+    L.dhi = (d0 + 1) % NDW;
+    return L;
+}
+
+// Decode the chunk whose stream bits sit in hi:lo starting at bit `off` (BITS in {1,2,3,4}).
+template <int BITS>
+__device__ __forceinline__ Chunk4 decode_chunk(uint32_t lo, uint32_t hi, int off)
+{
+    uint32_t y[8];
+    if constexpr (BITS == 4)
+    {
+        // off == 20 for every chunk: states j and j+4 are the low/high halves of one shifted dword
+        const uint32_t r0 = hi;                                      // states 3, 7
+        const uint32_t r1 = __builtin_amdgcn_alignbit(hi, lo, 20);   // states 0, 4
+        const uint32_t r2 = __builtin_amdgcn_alignbit(hi, lo, 24);   // states 1, 5
+        const uint32_t r3 = __builtin_amdgcn_alignbit(hi, lo, 28);   // states 2, 6
+        y[0] = mcg_mask(mcg_mul<0>(r1)); y[4] = mcg_mask(mcg_mul<1>(r1));
+        y[1] = mcg_mask(mcg_mul<0>(r2)); y[5] = mcg_mask(mcg_mul<1>(r2));
+        y[2] = mcg_mask(mcg_mul<0>(r3)); y[6] = mcg_mask(mcg_mul<1>(r3));
+        y[3] = mcg_mask(mcg_mul<0>(r0)); y[7] = mcg_mask(mcg_mul<1>(r0));
+    }
+    else
+    {
+        const uint64_t q = ((uint64_t) hi << 32) | lo;
+        #pragma unroll
+        for (int j = 0; j < 8; ++j)
+            y[j] = mcg_mask(mcg_mul<0>((uint32_t) (q >> (off + j * BITS))));
+    }
+    Chunk4 r;
+    r.w[0] = add_halves_pair(y[0], y[1]);
+    r.w[1] = add_halves_pair(y[2], y[3]);
+    r.w[2] = add_halves_pair(y[4], y[5]);
+    r.w[3] = add_halves_pair(y[6], y[7]);
+    return r;
+}
+
+// Decode two independent states (low and high half of r) -> packed fp16 pair.
+__device__ __forceinline__ uint32_t decode_state_pair(uint32_t r)
+{
+    return add_halves_pair(mcg_mask(mcg_mul<0>(r)), mcg_mask(mcg_mul<1>(r)));
+}
+
+}  // namespace exl3

@@ -1,0 +1,515 @@
+// Weight-stationary trellis GEMM for gfx950: the grouped gate|up / down stages of the EXL3 MoE prefill
+// (kernel/exl3_grouped_prefill.cu:148-279) and the single-expert fat GEMM (kernel/exl3_fat_gemm_v2.cu:72-234).
+//
+// Workgroup = 2 waves, tile = 128 rows x 128 output columns (one H128 block), K stage = 32.
+//   * Each stage's 16 trellis tiles (32 x 128 weights) are decoded ONCE per workgroup straight from
+//     global -> VGPR raw words into a k-contiguous [n][k] fp16 tile in LDS (padded rows, conflict-free),
+//     then reused by both waves for all 128 rows.
+//   * Each wave owns 64 rows x 128 columns and runs v_mfma_f32_32x32x16_f16 with the DECODED WEIGHTS as the
+//     first operand and the activations as the second, so the accumulator holds out^T: a lane owns one row
+//     (token) and 64 of the 128 output columns of the tile. The output Hadamard then runs 6 of its 7
+//     butterfly stages inside the lane's registers and one across the wave halves (v_permlane32_swap).
+//   * Activations and raw trellis words are prefetched one stage ahead into VGPRs (no LDS round trip for
+//     the activations); one barrier per stage guards the double-buffered decoded tile.
+//   * Workgroups are laid out XCD-aware: the column tiles of one row block share an XCD (and its L2).
+#include "exl3_common.h"
+#include "trellis_decode.h"
+
+namespace exl3 {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+constexpr int GEMM_WAVES = 2;
+constexpr int GEMM_THREADS = 64 * GEMM_WAVES;
+constexpr int TILE_M = 64 * GEMM_WAVES;             // 128 rows
+constexpr int TILE_N = 128;
+constexpr int TILE_K = 32;
+constexpr int LDS_ROW = TILE_K + 8;                 // halves per n-row of the decoded tile (80 B, conflict-free)
+constexpr int LDS_TILE = TILE_N * LDS_ROW;          // halves per decoded stage
+
+enum { MODE_STORE_F16 = 0, MODE_SCATTER_F32 = 1, MODE_STORE_F32 = 2 };
+
+struct GemmParams
+{
+    const uint16_t* a;             // [a_rows, size_k] fp16
+    int64_t a_rows;
+    int size_k;
+    const uint16_t* packed0;       // trellis of tensor 0 (gate / single tensor)
+    const uint16_t* packed1;       // trellis of tensor 1 (up), may be null
+    int64_t expert_stride_words;   // uint16 words between experts
+    int tiles_n;                   // 16-col trellis tiles per tensor
+    const uint16_t* svh0;
+    const uint16_t* svh1;
+    int64_t svh_stride;
+    const int32_t* block_expert;   // grouped schedule
+    const int32_t* block_row0;
+    const int32_t* counts;
+    const int32_t* expert_row0;
+    int n_groups;                  // row blocks (grouped: max_blocks; dense: ceil(m / 128))
+    int n_slots;                   // 128-col tiles over all tensors
+    int n_tiles_each;              // 128-col tiles per tensor
+    int64_t m;                     // dense rows
+    const int64_t* token;          // scatter destination row per sorted row
+    const uint16_t* route_weight;  // fp16 per sorted row
+    void* out;
+    int64_t out_ld;                // elements per output row
+};
+
+// In-place Walsh-Hadamard transform of 64 values (Sylvester order over the index bits).
+__device__ __forceinline__ void fwht64(float (&x)[64])
+{
+    #pragma unroll
+    for (int len = 1; len < 64; len <<= 1)
+        #pragma unroll
+        for (int i = 0; i < 64; ++i)
+            if (!(i & len))
+            {
+                const float a = x[i], b = x[i + len];
+                x[i] = a + b;
+                x[i + len] = a - b;
+            }
+}
+
+// Butterfly between lane l and lane l + 32 for two registers at once: lanes 0-31 get p_lo + p_hi, lanes 32-63
+// get p_lo - p_hi (same for q).
+__device__ __forceinline__ void half_wave_butterfly(float& p, float& q)
+{
+    auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(p), __float_as_uint(q), false, false);
+    const float a = __uint_as_float(s1[0]), b = __uint_as_float(s1[1]);
+    const float s = a + b, d = a - b;
+    auto s2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(d), false, false);
+    p = __uint_as_float(s2[0]);
+    q = __uint_as_float(s2[1]);
+}
+
+template <int BITS, int MODE, bool DENSE>
+__global__ __launch_bounds__(GEMM_THREADS, 2)
+void trellis_gemm_kernel(const GemmParams p)
+{
+    __shared__ __align__(16) uint16_t lds_b[2][LDS_TILE];
+
+    int group, slot;
+    xcd_group_slot((int) blockIdx.x, p.n_slots, group, slot);
+    int e, row0, rows_valid;
+    if constexpr (DENSE)
+    {
+        if (group >= p.n_groups) return;
+        e = 0;
+        row0 = group * TILE_M;
+        rows_valid = (int) min((int64_t) TILE_M, p.m - row0);
+    }
+    else
+    {
+        if (group >= p.n_groups) return;
+        e = p.block_expert[group];
+        if (e < 0) return;
+        row0 = p.block_row0[group];
+        rows_valid = min(TILE_M, p.expert_row0[e] + p.counts[e] - row0);
+    }
+    if (rows_valid <= 0) return;
+
+    const int which = slot >= p.n_tiles_each ? 1 : 0;
+    const int nt = slot - which * p.n_tiles_each;
+    const uint32_t* packed = reinterpret_cast<const uint32_t*>((which ? p.packed1 : p.packed0) +
+                                                               (int64_t) e * p.expert_stride_words);
+    const uint16_t* svh = (which ? p.svh1 : p.svh0) + (int64_t) e * p.svh_stride + nt * TILE_N;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+    const int num_kb = p.size_k / TILE_K;
+
+    // ---- decode role: lane -> trellis tile (kt, nt8) of the stage, chunks 4j .. 4j+3 (tile columns j, j+8)
+    const int ti = tid >> 3, j = tid & 7;
+    const int kt = ti >> 3, nt8 = ti & 7;
+    constexpr int NDW = 8 * BITS;                         // dwords per tile
+    int dw_off[BITS + 1];
+    #pragma unroll
+    for (int i = 0; i <= BITS; ++i) dw_off[i] = (BITS * j - 1 + i + NDW) % NDW;
+    const int64_t tile_stride_stage = (int64_t) 2 * p.tiles_n * NDW;      // dwords per K stage
+    const uint32_t* raw_base = packed + ((int64_t) kt * p.tiles_n + nt * 8 + nt8) * NDW;
+    const int wcol0 = (nt8 * 16 + j) * LDS_ROW + kt * 16;                  // column j of the tile
+    const int wcol1 = wcol0 + 8 * LDS_ROW;                                 // column j + 8
+
+    // ---- MFMA role: wave rows [64 wave, 64 wave + 64)
+    const int wave_row0 = 64 * wave;
+    const bool wave_active = wave_row0 < rows_valid;
+    const uint16_t* a_ptr[2];
+    #pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+    {
+        const int r = min(wave_row0 + 32 * mb + l32, rows_valid - 1);
+        a_ptr[mb] = p.a + (int64_t) (row0 + r) * p.size_k + 16 * h;
+    }
+    const int wread = l32 * LDS_ROW + 16 * h;
+
+    auto load_raw = [&](int kb, uint32_t (&r)[BITS + 1]) {
+        const uint32_t* base = raw_base + (int64_t) kb * tile_stride_stage;
+        #pragma unroll
+        for (int i = 0; i <= BITS; ++i) r[i] = base[dw_off[i]];
+    };
+    auto load_a = [&](int kb, half8_t (&a)[2][2]) {
+        #pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+        {
+            const half8_t* src = reinterpret_cast<const half8_t*>(a_ptr[mb] + kb * TILE_K);
+            a[mb][0] = src[0];
+            a[mb][1] = src[1];
+        }
+    };
+    auto decode_store = [&](const uint32_t (&r)[BITS + 1], uint16_t* lds) {
+        Chunk4 c[4];
+        #pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const int b0 = 8 * i * BITS + BITS - 16;           // window start of chunk 4j+i relative to dword bj
+            const int rel = (b0 >= 0 ? b0 / 32 : -1) + 1;
+            const int off = b0 - 32 * (rel - 1);
+            c[i] = decode_chunk<BITS>(r[rel], r[rel + 1], off);
+        }
+        const uint4 v0 = {c[0].w[0], c[1].w[0], c[2].w[0], c[3].w[0]};
+        const uint4 v1 = {c[0].w[1], c[1].w[1], c[2].w[1], c[3].w[1]};
+        const uint4 v2 = {c[0].w[2], c[1].w[2], c[2].w[2], c[3].w[2]};
+        const uint4 v3 = {c[0].w[3], c[1].w[3], c[2].w[3], c[3].w[3]};
+        *reinterpret_cast<uint4*>(lds + wcol0) = v0;
+        *reinterpret_cast<uint4*>(lds + wcol0 + 8) = v1;
+        *reinterpret_cast<uint4*>(lds + wcol1) = v2;
+        *reinterpret_cast<uint4*>(lds + wcol1 + 8) = v3;
+    };
+
+    float16_t acc[2][4];
+    #pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+        #pragma unroll
+        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = {};
+
+    // Unconditional even for a wave without valid rows (its rows are clamped, results discarded): keeping
+    // the MFMAs in the same basic block as the decode lets the scheduler interleave the two.
+    auto mfma_stage = [&](const half8_t (&a)[2][2], const uint16_t* lds) {
+        #pragma unroll
+        for (int t = 0; t < 2; ++t)
+        {
+            half8_t w[4];
+            #pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+                w[nb] = *reinterpret_cast<const half8_t*>(lds + nb * 32 * LDS_ROW + wread + 8 * t);
+            #pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+                #pragma unroll
+                for (int nb = 0; nb < 4; ++nb)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[nb], a[mb][t], acc[mb][nb], 0, 0, 0);
+        }
+    };
+
+    // ---- main loop, unrolled by two so both register buffers have static names. num_kb is even (K % 64 == 0).
+    // Loads and decodes are unconditional (stage index clamped at the end) so every path keeps the same number
+    // of loads in flight and the waits stay partial: a stage's raw words and activations are waited for only
+    // when they are consumed, one stage after they were issued.
+    uint32_t raw_a[BITS + 1], raw_b[BITS + 1];
+    half8_t act_a[2][2], act_b[2][2];
+    const int last = num_kb - 1;
+    load_raw(0, raw_a);
+    load_a(0, act_a);
+    load_raw(1, raw_b);
+    load_a(1, act_b);
+    decode_store(raw_a, lds_b[0]);
+    for (int kb = 0; kb < num_kb; kb += 2)
+    {
+        __syncthreads();
+        decode_store(raw_b, lds_b[1]);                  // stage kb + 1
+        load_raw(min(kb + 2, last), raw_a);
+        mfma_stage(act_a, lds_b[0]);                    // stage kb
+        load_a(min(kb + 2, last), act_a);
+        __syncthreads();
+        decode_store(raw_a, lds_b[0]);                  // stage kb + 2 (discarded after the last stage)
+        load_raw(min(kb + 3, last), raw_b);
+        mfma_stage(act_b, lds_b[1]);                    // stage kb + 1
+        load_a(min(kb + 3, last), act_b);
+    }
+
+    // ---- epilogue: per 32-row block, H128 over the 128 columns of each row, scale by svh, store / scatter
+    if (!wave_active) return;
+    const int out_col0 = which * p.n_tiles_each * TILE_N + nt * TILE_N;
+    #pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+    {
+        const int r_local = wave_row0 + 32 * mb + l32;        // this lane's row within the tile
+        if (wave_row0 + 32 * mb >= rows_valid) break;           // uniform over the wave
+        // x[nb * 16 + r] holds column 32 nb + 8 (r >> 2) + 4 h + (r & 3)
+        float x[64];
+        #pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+            #pragma unroll
+            for (int r = 0; r < 16; ++r) x[nb * 16 + r] = acc[mb][nb][r];
+        fwht64(x);
+        #pragma unroll
+        for (int i = 0; i < 64; i += 2) half_wave_butterfly(x[i], x[i + 1]);
+
+        const bool row_ok = r_local < rows_valid;
+        const int64_t srow = (int64_t) row0 + r_local;
+        float rw = 0.0f;
+        int64_t orow = srow;
+        if constexpr (MODE == MODE_SCATTER_F32)
+        {
+            if (row_ok) { orow = p.token[srow]; rw = h2f(p.route_weight[srow]); }
+        }
+        #pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+            #pragma unroll
+            for (int g = 0; g < 4; ++g)
+            {
+                const int col = 32 * nb + 8 * g + 4 * h;          // first of 4 consecutive columns
+                const uint2 sv = *reinterpret_cast<const uint2*>(svh + col);
+                float s[4] = {h2f(sv.x & 0xFFFF), h2f(sv.x >> 16), h2f(sv.y & 0xFFFF), h2f(sv.y >> 16)};
+                float v[4];
+                #pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = x[nb * 16 + 4 * g + q] * HAD_SCALE * s[q];
+                if (!row_ok) continue;
+                if constexpr (MODE == MODE_STORE_F16)
+                {
+                    uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + orow * p.out_ld + out_col0 + col;
+                    uint2 pk;
+                    pk.x = (uint32_t) f2h(v[0]) | ((uint32_t) f2h(v[1]) << 16);
+                    pk.y = (uint32_t) f2h(v[2]) | ((uint32_t) f2h(v[3]) << 16);
+                    *reinterpret_cast<uint2*>(o) = pk;
+                }
+                else if constexpr (MODE == MODE_STORE_F32)
+                {
+                    float* o = reinterpret_cast<float*>(p.out) + orow * p.out_ld + out_col0 + col;
+                    *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+                }
+                else
+                {
+                    float* o = reinterpret_cast<float*>(p.out) + orow * p.out_ld + out_col0 + col;
+                    #pragma unroll
+                    for (int q = 0; q < 4; ++q) unsafeAtomicAdd(o + q, v[q] * rw);
+                }
+            }
+    }
+}
+
+// ------------------------------------------------------------------------------------------- reconstruct
+// packed [tiles_k, tiles_n, 16 bits] -> out fp16 [16 tiles_k, 16 tiles_n]; 8 lanes per tile as in the GEMM.
+template <int BITS>
+__global__ __launch_bounds__(256)
+void reconstruct_kernel(uint16_t* __restrict__ out, const uint32_t* __restrict__ packed, int tiles_k, int tiles_n)
+{
+    constexpr int NDW = 8 * BITS;
+    const int64_t gid = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    const int64_t tile = gid >> 3;
+    if (tile >= (int64_t) tiles_k * tiles_n) return;
+    const int j = (int) (gid & 7);
+    const uint32_t* t = packed + tile * NDW;
+    uint32_t r[BITS + 1];
+    #pragma unroll
+    for (int i = 0; i <= BITS; ++i) r[i] = t[(BITS * j - 1 + i + NDW) % NDW];
+    const int tk = (int) (tile / tiles_n), tn = (int) (tile % tiles_n);
+    const int64_t ncols = (int64_t) tiles_n * 16;
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const int b0 = 8 * i * BITS + BITS - 16;
+        const int rel = (b0 >= 0 ? b0 / 32 : -1) + 1;
+        const int off = b0 - 32 * (rel - 1);
+        const Chunk4 c = decode_chunk<BITS>(r[rel], r[rel + 1], off);
+        // chunk 4j+i: k0 = 2i, columns j and j+8
+        #pragma unroll
+        for (int q = 0; q < 4; ++q)
+        {
+            const int k = 2 * i + 8 * (q & 1);
+            const int n = j + 8 * (q >> 1);
+            uint16_t* o = out + (int64_t) (tk * 16 + k) * ncols + tn * 16 + n;
+            o[0] = (uint16_t) (c.w[q] & 0xFFFF);
+            o[ncols] = (uint16_t) (c.w[q] >> 16);
+        }
+    }
+}
+
+__global__ void decode_states_kernel(const uint32_t* __restrict__ states, uint32_t* __restrict__ out, int64_t n2)
+{
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n2) out[i] = decode_state_pair(states[i]);
+}
+
+template <int BITS, int MODE, bool DENSE>
+int launch_gemm(const GemmParams& p, hipStream_t s)
+{
+    const int groups8 = (p.n_groups + 7) / 8 * 8;
+    const int64_t grid = (int64_t) groups8 * p.n_slots;
+    if (grid == 0) return EXL3_OK;
+    if (grid > 0x7FFFFFFF) return fail("grid too large");
+    trellis_gemm_kernel<BITS, MODE, DENSE><<<(unsigned) grid, GEMM_THREADS, 0, s>>>(p);
+    return EXL3_OK;
+}
+
+template <int MODE, bool DENSE>
+int launch_bits(int bits, const GemmParams& p, hipStream_t s)
+{
+    switch (bits)
+    {
+        case 2: return launch_gemm<2, MODE, DENSE>(p, s);
+        case 3: return launch_gemm<3, MODE, DENSE>(p, s);
+        case 4: return launch_gemm<4, MODE, DENSE>(p, s);
+        default: return fail("unsupported bits %d (2, 3 or 4)", bits);
+    }
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+}  // namespace
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
+                                 const uint16_t* packed_gate, const uint16_t* packed_up, int64_t expert_stride_words,
+                                 int tiles_k, int tiles_n, int bits,
+                                 const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                                 const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
+                                 const int32_t* counts, const int32_t* expert_row0, int n_experts,
+                                 const int64_t* token_sorted, const uint16_t* route_weight,
+                                 void* out, int64_t out_rows, int mode, void* stream)
+{
+    EXL3_CHECK(bits >= 2 && bits <= 4, "unsupported bits %d (2, 3 or 4)", bits);
+    EXL3_CHECK(size_k == tiles_k * 16 && size_k % 64 == 0 && size_k > 0, "K mismatch");
+    const int size_n_each = tiles_n * 16;
+    EXL3_CHECK(size_n_each % TILE_N == 0 && size_n_each > 0, "N must be a multiple of 128");
+    EXL3_CHECK(n_experts > 0 && n_experts <= MAX_EXPERTS, "too many experts");
+    EXL3_CHECK(max_blocks >= 0 && a_rows >= 0, "bad sizes");
+    EXL3_CHECK((packed_up == nullptr) == (svh_up == nullptr), "gate/up strides must match");
+    EXL3_CHECK(expert_stride_words >= (int64_t) tiles_k * tiles_n * 16 * bits || n_experts == 1,
+               "packed [E, tiles_k, tiles_n, 16*bits] with contiguous inner dims (expert stride may be larger: [E,2,...] views)");
+    EXL3_CHECK(svh_stride >= size_n_each || n_experts == 1, "svh N mismatch");
+    EXL3_CHECK(a && packed_gate && svh_gate && block_expert && block_row0 && counts && expert_row0 && out,
+               "null pointer");
+    EXL3_CHECK(aligned16(a) && (size_k * 2) % 16 == 0, "a must be 16-byte aligned");
+    EXL3_CHECK(((reinterpret_cast<uintptr_t>(packed_gate) | reinterpret_cast<uintptr_t>(packed_up)) & 3) == 0 &&
+               expert_stride_words % 2 == 0, "trellis tensors must be 4-byte aligned");
+    EXL3_CHECK(((reinterpret_cast<uintptr_t>(svh_gate) | reinterpret_cast<uintptr_t>(svh_up)) & 7) == 0 &&
+               svh_stride % 4 == 0, "svh must be 8-byte aligned");
+    const int n_tensors = packed_up ? 2 : 1;
+    GemmParams p{};
+    p.a = a; p.a_rows = a_rows; p.size_k = size_k;
+    p.packed0 = packed_gate; p.packed1 = packed_up; p.expert_stride_words = expert_stride_words;
+    p.tiles_n = tiles_n; p.svh0 = svh_gate; p.svh1 = svh_up; p.svh_stride = svh_stride;
+    p.block_expert = block_expert; p.block_row0 = block_row0; p.counts = counts; p.expert_row0 = expert_row0;
+    p.n_groups = max_blocks; p.n_tiles_each = size_n_each / TILE_N; p.n_slots = n_tensors * p.n_tiles_each;
+    p.token = token_sorted; p.route_weight = route_weight; p.out = out;
+    hipStream_t s = as_stream(stream);
+    int rc;
+    if (mode == EXL3_GEMM_STORE_F16)
+    {
+        p.out_ld = (int64_t) n_tensors * size_n_each;
+        EXL3_CHECK(out_rows >= a_rows, "mode 0: out fp16 [rows, n_tensors*N]");
+        EXL3_CHECK((reinterpret_cast<uintptr_t>(out) & 7) == 0, "out must be 8-byte aligned");
+        rc = launch_bits<MODE_STORE_F16, false>(bits, p, s);
+    }
+    else if (mode == EXL3_GEMM_SCATTER_F32)
+    {
+        EXL3_CHECK(n_tensors == 1, "mode 1: out fp32 [T, N], single tensor");
+        EXL3_CHECK(token_sorted && route_weight, "routing dtypes");
+        p.out_ld = size_n_each;
+        rc = launch_bits<MODE_SCATTER_F32, false>(bits, p, s);
+    }
+    else
+        return fail("mode must be 0 (fp16 store) or 1 (fp32 atomic scatter)");
+    if (rc != EXL3_OK) return rc;
+    return hip_status("grouped_gemm");
+}
+
+namespace {
+
+int fat_common(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed, int tiles_k, int tiles_n,
+               int packed_words, const float* out, const uint16_t* svh, int64_t svh_len, int bits, int mcg, int mul1,
+               int variant)
+{
+    EXL3_CHECK(a && packed && out && svh, "tensors must be CUDA");
+    EXL3_CHECK(bits >= 2 && bits <= 4 && mcg && !mul1, "only K2/K3/K4 MCG tensors");
+    EXL3_CHECK(size_k == tiles_k * 16, "a K dimension does not match packed tensor");
+    EXL3_CHECK(svh_len == (int64_t) tiles_n * 16, "svh N dimension does not match packed tensor");
+    EXL3_CHECK(svh_len % TILE_N == 0, "N must be divisible by 128");
+    EXL3_CHECK(packed_words == 16 * bits, "packed block width must be 16*K int16 words");
+    EXL3_CHECK(size_k % 64 == 0, "K must be divisible by 64");
+    EXL3_CHECK(variant >= 0 && variant <= 3, "unknown variant");
+    EXL3_CHECK(m >= 0 && m < ((int64_t) 1 << 31), "bad row count");
+    EXL3_CHECK(aligned16(a) && aligned16(out) && (reinterpret_cast<uintptr_t>(svh) & 7) == 0 &&
+               (reinterpret_cast<uintptr_t>(packed) & 3) == 0, "tensors must be contiguous and aligned");
+    return EXL3_OK;
+}
+
+}  // namespace
+
+extern "C" int exl3_fat_gemm(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed, int tiles_k, int tiles_n,
+                             int packed_words, float* out, int64_t out_rows, const uint16_t* svh, int64_t svh_len,
+                             int bits, int mcg, int mul1, int variant, void* stream)
+{
+    int rc = fat_common(a, m, size_k, packed, tiles_k, tiles_n, packed_words, out, svh, svh_len, bits, mcg, mul1, variant);
+    if (rc) return rc;
+    EXL3_CHECK(out_rows == m, "out shape must be [M, N]");
+    GemmParams p{};
+    p.a = a; p.a_rows = m; p.size_k = size_k; p.packed0 = packed; p.tiles_n = tiles_n;
+    p.svh0 = svh; p.n_groups = (int) ((m + TILE_M - 1) / TILE_M); p.n_tiles_each = (int) (svh_len / TILE_N);
+    p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = svh_len;
+    rc = launch_bits<MODE_STORE_F32, true>(bits, p, as_stream(stream));
+    if (rc) return rc;
+    return hip_status("fat_gemm_v2");
+}
+
+extern "C" int exl3_fat_gemm_scatter(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed, int tiles_k,
+                                     int tiles_n, int packed_words, float* out, int64_t out_rows, const uint16_t* svh,
+                                     int64_t svh_len, const int64_t* token_idx, const uint16_t* route_weight,
+                                     int bits, int mcg, int mul1, int variant, void* stream)
+{
+    int rc = fat_common(a, m, size_k, packed, tiles_k, tiles_n, packed_words, out, svh, svh_len, bits, mcg, mul1, variant);
+    if (rc) return rc;
+    EXL3_CHECK(token_idx && route_weight, "routing tensors");
+    EXL3_CHECK(out_rows >= 0, "bad out rows");
+    GemmParams p{};
+    p.a = a; p.a_rows = m; p.size_k = size_k; p.packed0 = packed; p.tiles_n = tiles_n;
+    p.svh0 = svh; p.n_groups = (int) ((m + TILE_M - 1) / TILE_M); p.n_tiles_each = (int) (svh_len / TILE_N);
+    p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = svh_len;
+    p.token = token_idx; p.route_weight = route_weight;
+    rc = launch_bits<MODE_SCATTER_F32, true>(bits, p, as_stream(stream));
+    if (rc) return rc;
+    return hip_status("fat_gemm_v2_scatter");
+}
+
+extern "C" int64_t exl3_smem_bytes(int64_t variant)
+{
+    if (variant < 0 || variant > 3) return -1;
+    return (int64_t) sizeof(uint16_t) * 2 * LDS_TILE;
+}
+
+extern "C" int exl3_reconstruct(uint16_t* out, const uint16_t* packed, int tiles_k, int tiles_n, int bits, int mcg,
+                                int mul1, void* stream)
+{
+    EXL3_CHECK(bits >= 2 && bits <= 4 && mcg && !mul1, "only K2/K3/K4 MCG tensors");
+    EXL3_CHECK(tiles_k >= 0 && tiles_n >= 0, "bad shape");
+    EXL3_CHECK(out && packed, "null pointer");
+    EXL3_CHECK((reinterpret_cast<uintptr_t>(packed) & 3) == 0, "packed must be 4-byte aligned");
+    const int64_t lanes = (int64_t) tiles_k * tiles_n * 8;
+    if (lanes == 0) return EXL3_OK;
+    const unsigned grid = (unsigned) ((lanes + 255) / 256);
+    hipStream_t s = as_stream(stream);
+    const uint32_t* pk = reinterpret_cast<const uint32_t*>(packed);
+    switch (bits)
+    {
+        case 2: reconstruct_kernel<2><<<grid, 256, 0, s>>>(out, pk, tiles_k, tiles_n); break;
+        case 3: reconstruct_kernel<3><<<grid, 256, 0, s>>>(out, pk, tiles_k, tiles_n); break;
+        default: reconstruct_kernel<4><<<grid, 256, 0, s>>>(out, pk, tiles_k, tiles_n); break;
+    }
+    return hip_status("reconstruct");
+}
+
+extern "C" int exl3_decode_states(const uint16_t* states, uint16_t* out, int64_t n, void* stream)
+{
+    EXL3_CHECK(n >= 0 && n % 2 == 0, "n must be even");
+    EXL3_CHECK(n == 0 || (states && out), "null pointer");
+    EXL3_CHECK(((reinterpret_cast<uintptr_t>(states) | reinterpret_cast<uintptr_t>(out)) & 3) == 0,
+               "states/out must be 4-byte aligned");
+    const int64_t n2 = n / 2;
+    if (n2 == 0) return EXL3_OK;
+    decode_states_kernel<<<(unsigned) ((n2 + 255) / 256), 256, 0, as_stream(stream)>>>(
+        reinterpret_cast<const uint32_t*>(states), reinterpret_cast<uint32_t*>(out), n2);
+    return hip_status("decode_states");
+}

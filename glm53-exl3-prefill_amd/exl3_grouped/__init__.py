@@ -1,0 +1,9 @@
+"""MI355X (gfx950) EXL3 grouped routed-expert MoE prefill: torch-facing ops over the libexl3_grouped.so C ABI."""
+from .ops import (act_had, build_blocks, decode_states, fat_gemm_v2, fat_gemm_v2_scatter, grouped_gemm,  # noqa: F401
+                  reconstruct, row_had, smem_bytes, sort_routes, sort_routes_workspace_bytes)
+from . import _lib  # noqa: F401
+
+
+def library_path() -> str:
+    """Path of the loaded (or to-be-loaded) native library."""
+    return _lib.path()

@@ -1,0 +1,282 @@
+"""Torch-facing operators with the reference extension's names, argument order and error behaviour.
+
+Reference ops (paths relative to the reference repository):
+  build_blocks, row_had, act_had, grouped_gemm   kernel/exl3_grouped_prefill.cu:283-386 (pybind module)
+  fat_gemm_v2, fat_gemm_v2_scatter, smem_bytes   kernel/exl3_fat_gemm_v2.cu:298-333
+  reconstruct                                     exllamav3 ext.reconstruct, called at kernel/test_fat_v2.py:91-94
+New ops (no reference counterpart): sort_routes (the torch glue of kernel/exl3_grouped_runtime.py:59-68 as a
+GPU counting sort) and decode_states (pins the device trellis decoder).
+
+Each op checks dtypes / shapes / strides on the host first (a bad call raises RuntimeError, like the
+reference's TORCH_CHECK, before anything touches a GPU), then enqueues HIP kernels on the current stream of
+the tensors' device through the C ABI. Nothing here allocates device memory except sort_routes' optional
+workspace.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_DT = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16,
+       torch.int32: _lib.DTYPE_I32, torch.int64: _lib.DTYPE_I64}
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _require_cuda(*ts) -> torch.device:
+    for t in ts:
+        if t is not None:
+            _check(t.is_cuda, "tensors must be CUDA")
+    dev = next(t for t in ts if t is not None).device
+    for t in ts:
+        if t is not None:
+            _check(t.device == dev, "tensors must be on the same device")
+    return dev
+
+
+class _On:
+    """Device guard + current stream handle for one op call."""
+
+    def __init__(self, dev: torch.device):
+        self.dev = dev
+
+    def __enter__(self):
+        self.guard = torch.cuda.device(self.dev)
+        self.guard.__enter__()
+        return ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+
+    def __exit__(self, *exc):
+        self.guard.__exit__(*exc)
+        return False
+
+
+# ------------------------------------------------------------------------------------------- routing
+def sort_routes_workspace_bytes(tokens: int, topk: int, n_experts: int) -> int:
+    return int(_lib.load().exl3_sort_routes_workspace_bytes(tokens, topk, n_experts))
+
+
+def sort_routes(topk_ids: torch.Tensor, topk_weights: torch.Tensor, n_experts: int, token_sorted: torch.Tensor,
+                weight_sorted: torch.Tensor, expert_of_row: torch.Tensor, counts: torch.Tensor,
+                expert_row0: torch.Tensor, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Stable sort of routes by expert (replaces kernel/exl3_grouped_runtime.py:59-68). Returns the workspace;
+    its first int32 holds the number of dropped routes (ids outside [0, n_experts))."""
+    _check(topk_ids.dim() == 2 and topk_weights.shape == topk_ids.shape, "topk_ids / topk_weights must be [T, topk]")
+    _check(topk_ids.dtype in (torch.int64, torch.int32), "topk_ids must be int64 or int32")
+    _check(topk_weights.dtype in (torch.float32, torch.float16, torch.bfloat16),
+           "topk_weights must be float32, float16 or bfloat16")
+    _check(topk_ids.is_contiguous() and topk_weights.is_contiguous(), "routing tensors must be contiguous")
+    T, k = topk_ids.shape
+    R = T * k
+    _check(token_sorted.dtype == torch.int64 and weight_sorted.dtype == torch.float16 and
+           expert_of_row.dtype == torch.int32, "sorted outputs: int64 tokens, fp16 weights, int32 experts")
+    _check(token_sorted.numel() == R and weight_sorted.numel() == R and expert_of_row.numel() == R,
+           "sorted outputs must have T*topk elements")
+    _check(counts.dtype == torch.int32 and expert_row0.dtype == torch.int32 and counts.numel() == n_experts and
+           expert_row0.numel() == n_experts, "counts / expert_row0 must be int32 [E]")
+    _check(0 < n_experts <= 1024, "too many experts")
+    need = sort_routes_workspace_bytes(T, k, n_experts)
+    dev = _require_cuda(topk_ids, topk_weights, token_sorted, weight_sorted, expert_of_row, counts, expert_row0)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    _check(workspace.numel() * workspace.element_size() >= need, "sort workspace too small")
+    with _On(dev) as s:
+        _lib.call("exl3_sort_routes", _p(topk_ids), _DT[topk_ids.dtype], _p(topk_weights), _DT[topk_weights.dtype],
+                  T, k, n_experts, _p(token_sorted), _p(weight_sorted), _p(expert_of_row), _p(counts),
+                  _p(expert_row0), _p(workspace), workspace.numel() * workspace.element_size(), s)
+    return workspace
+
+
+def build_blocks(counts: torch.Tensor, block_expert: torch.Tensor, block_row0: torch.Tensor, meta: torch.Tensor) -> None:
+    """kernel/exl3_grouped_prefill.cu:285-294."""
+    _check(counts.dtype == torch.int32 and block_expert.dtype == torch.int32 and block_row0.dtype == torch.int32
+           and meta.dtype == torch.int32, "int32 tensors")
+    _check(counts.numel() <= 1024, "too many experts")
+    _check(block_row0.numel() >= block_expert.numel() and meta.numel() >= 2, "block table shapes")
+    _check(counts.is_contiguous() and block_expert.is_contiguous() and block_row0.is_contiguous()
+           and meta.is_contiguous(), "contiguous tensors")
+    dev = _require_cuda(counts, block_expert, block_row0, meta)
+    with _On(dev) as s:
+        _lib.call("exl3_build_blocks", _p(counts), counts.numel(), block_expert.numel(), _p(block_expert),
+                  _p(block_row0), _p(meta), s)
+
+
+# ------------------------------------------------------------------------------------------- Hadamard passes
+def row_had(src: torch.Tensor, dst: torch.Tensor, token_sorted: Optional[torch.Tensor], expert_of_row: torch.Tensor,
+            suh: torch.Tensor, gather: bool) -> None:
+    """kernel/exl3_grouped_prefill.cu:297-311."""
+    rows, K = dst.shape
+    _check(K % 128 == 0 and suh.size(-1) == K, "K must be a multiple of 128 and match suh")
+    _check(src.dtype == torch.float16 and dst.dtype == torch.float16 and suh.dtype == torch.float16,
+           "fp16 tensors")
+    _check(src.dim() == 2 and src.size(1) == K and src.is_contiguous() and dst.is_contiguous(),
+           "src / dst must be contiguous [*, K]")
+    _check(suh.dim() == 2 and suh.stride(1) == 1, "suh must be [E, K] with unit inner stride")
+    _check(expert_of_row.dtype == torch.int32 and expert_of_row.numel() >= rows, "expert_of_row int32 [rows]")
+    if gather:
+        _check(token_sorted is not None and token_sorted.dtype == torch.int64 and token_sorted.numel() >= rows,
+               "token_sorted int64 [rows]")
+    else:
+        _check(src.size(0) >= rows, "src has too few rows")
+    dev = _require_cuda(src, dst, expert_of_row, suh, token_sorted if gather else None)
+    with _On(dev) as s:
+        _lib.call("exl3_row_had", _p(src), _p(dst), _p(token_sorted) if gather else None, _p(expert_of_row),
+                  _p(suh), suh.stride(0), suh.size(-1), rows, K, 1 if gather else 0, s)
+
+
+def act_had(gu: torch.Tensor, act: torch.Tensor, expert_of_row: torch.Tensor, suh_down: torch.Tensor,
+            limit: float) -> None:
+    """kernel/exl3_grouped_prefill.cu:313-322."""
+    rows, I = act.shape
+    _check(gu.size(1) == 2 * I and I % 128 == 0, "gate|up width must be 2I, I multiple of 128")
+    _check(gu.dtype == torch.float16 and act.dtype == torch.float16 and suh_down.dtype == torch.float16,
+           "fp16 tensors")
+    _check(gu.is_contiguous() and act.is_contiguous() and gu.size(0) >= rows, "gu / act must be contiguous")
+    _check(suh_down.dim() == 2 and suh_down.size(1) == I and suh_down.stride(1) == 1, "suh_down must be [E, I]")
+    _check(expert_of_row.dtype == torch.int32 and expert_of_row.numel() >= rows, "expert_of_row int32 [rows]")
+    dev = _require_cuda(gu, act, expert_of_row, suh_down)
+    with _On(dev) as s:
+        _lib.call("exl3_act_had", _p(gu), gu.size(1), _p(act), _p(expert_of_row), _p(suh_down), suh_down.stride(0),
+                  rows, I, float(limit), s)
+
+
+# ------------------------------------------------------------------------------------------- grouped GEMM
+def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional[torch.Tensor],
+                 svh_gate: torch.Tensor, svh_up: Optional[torch.Tensor], block_expert: torch.Tensor,
+                 block_row0: torch.Tensor, counts: torch.Tensor, expert_row0: torch.Tensor,
+                 token_sorted: Optional[torch.Tensor], route_weight: Optional[torch.Tensor], out: torch.Tensor,
+                 mode: int) -> None:
+    """kernel/exl3_grouped_prefill.cu:326-378. mode 0: fp16 store; mode 1: fp32 atomic scatter."""
+    _check(a.dtype == torch.float16 and a.is_contiguous(), "a fp16 contiguous")
+    _check(packed_gate.dim() == 4 and packed_gate.dtype in (torch.int16, torch.uint16) and
+           packed_gate.stride(3) == 1 and packed_gate.stride(2) == packed_gate.size(3) and
+           packed_gate.stride(1) == packed_gate.size(2) * packed_gate.size(3),
+           "packed [E, tiles_k, tiles_n, 64] with contiguous inner dims (expert stride may be larger: [E,2,...] views)")
+    words = packed_gate.size(3)
+    _check(words in (32, 48, 64), "packed tile width must be 16*bits words, bits in {2, 3, 4}")
+    bits = words // 16
+    size_k, tiles_k, tiles_n = a.size(1), packed_gate.size(1), packed_gate.size(2)
+    _check(size_k == tiles_k * 16 and size_k % 64 == 0, "K mismatch")
+    size_n_each = tiles_n * 16
+    _check(size_n_each % 128 == 0, "N must be a multiple of 128")
+    n_tensors = 2 if packed_up is not None else 1
+    expert_stride = packed_gate.stride(0)
+    _check(svh_gate.dtype == torch.float16 and svh_gate.dim() == 2 and svh_gate.stride(1) == 1, "svh fp16 [E, N]")
+    svh_stride = svh_gate.stride(0)
+    _check(svh_gate.size(-1) == size_n_each, "svh N mismatch")
+    if packed_up is not None:
+        _check(packed_up.shape == packed_gate.shape and packed_up.stride() == packed_gate.stride() and
+               svh_up is not None and svh_up.stride() == svh_gate.stride() and svh_up.shape == svh_gate.shape,
+               "gate/up strides must match")
+    E = counts.numel()
+    _check(packed_gate.size(0) >= E and svh_gate.size(0) >= E, "fewer experts in the weights than in counts")
+    _check(block_expert.dtype == torch.int32 and block_row0.dtype == torch.int32 and counts.dtype == torch.int32
+           and expert_row0.dtype == torch.int32, "int32 block table")
+    max_blocks = block_expert.numel()
+    if mode == 0:
+        _check(out.dtype == torch.float16 and out.dim() == 2 and out.size(1) == n_tensors * size_n_each and
+               out.is_contiguous() and out.size(0) >= a.size(0), "mode 0: out fp16 [rows, n_tensors*N]")
+    elif mode == 1:
+        _check(out.dtype == torch.float32 and out.dim() == 2 and out.size(1) == size_n_each and n_tensors == 1 and
+               out.is_contiguous(), "mode 1: out fp32 [T, N], single tensor")
+        _check(token_sorted is not None and route_weight is not None and token_sorted.dtype == torch.int64 and
+               route_weight.dtype == torch.float16, "routing dtypes")
+    else:
+        raise RuntimeError("mode must be 0 or 1")
+    dev = _require_cuda(a, packed_gate, packed_up, svh_gate, svh_up, block_expert, block_row0, counts,
+                        expert_row0, out, token_sorted if mode == 1 else None, route_weight if mode == 1 else None)
+    with _On(dev) as s:
+        _lib.call("exl3_grouped_gemm", _p(a), a.size(0), size_k, _p(packed_gate), _p(packed_up), expert_stride,
+                  tiles_k, tiles_n, bits, _p(svh_gate), _p(svh_up), svh_stride, _p(block_expert), _p(block_row0),
+                  max_blocks, _p(counts), _p(expert_row0), E, _p(token_sorted) if mode == 1 else None,
+                  _p(route_weight) if mode == 1 else None, _p(out), out.size(0), mode, s)
+
+
+# ------------------------------------------------------------------------------------------- per-expert entry
+def _fat_check(a, packed, out, svh, K, mcg, mul1):
+    """kernel/exl3_fat_gemm_v2.cu:236-252 (bits 2 and 3 accepted in addition to 4)."""
+    _check(a.is_contiguous() and packed.is_contiguous() and out.is_contiguous() and svh.is_contiguous(),
+           "tensors must be contiguous")
+    _check(a.dtype == torch.float16, "a must be float16")
+    _check(packed.dtype in (torch.int16, torch.uint16), "packed must be int16")
+    _check(out.dtype == torch.float32, "out must be float32")
+    _check(svh.dtype == torch.float16, "svh must be float16")
+    _check(a.dim() == 2 and packed.dim() == 3 and out.dim() == 2 and svh.dim() == 1, "rank mismatch")
+    _check(int(K) in (2, 3, 4) and bool(mcg) and not bool(mul1), "only K2/K3/K4 MCG tensors")
+    _check(a.size(1) == packed.size(0) * 16, "a K dimension does not match packed tensor")
+    _check(svh.numel() == packed.size(1) * 16, "svh N dimension does not match packed tensor")
+    _check(svh.numel() % 128 == 0, "N must be divisible by 128")
+    _check(packed.size(2) == 16 * int(K), "packed block width must be 16*K int16 words")
+    _check(a.size(1) % 64 == 0, "K must be divisible by 64")
+
+
+def fat_gemm_v2(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, svh: torch.Tensor, K: int, mcg: bool,
+                mul1: bool, variant: int = 1) -> None:
+    """kernel/exl3_fat_gemm_v2.cu:298-303: out[M, N] = H128(a @ W') / sqrt(128) * svh (fp32)."""
+    _fat_check(a, packed, out, svh, K, mcg, mul1)
+    _check(out.size(0) == a.size(0) and out.size(1) == svh.numel(), "out shape must be [M, N]")
+    _check(0 <= int(variant) <= 3, "unknown variant")
+    dev = _require_cuda(a, packed, out, svh)
+    with _On(dev) as s:
+        _lib.call("exl3_fat_gemm", _p(a), a.size(0), a.size(1), _p(packed), packed.size(0), packed.size(1),
+                  packed.size(2), _p(out), out.size(0), _p(svh), svh.numel(), int(K), int(bool(mcg)),
+                  int(bool(mul1)), int(variant), s)
+
+
+def fat_gemm_v2_scatter(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, svh: torch.Tensor,
+                        token_idx: torch.Tensor, route_weight: torch.Tensor, K: int, mcg: bool, mul1: bool,
+                        variant: int = 1) -> None:
+    """kernel/exl3_fat_gemm_v2.cu:305-314: out[token_idx[m]] += fp32(route_weight[m]) * y[m] (device atomics)."""
+    _fat_check(a, packed, out, svh, K, mcg, mul1)
+    _check(out.size(1) == svh.numel(), "out N dimension mismatch")
+    _check(token_idx.is_contiguous() and route_weight.is_contiguous(), "routing tensors")
+    _check(token_idx.dtype == torch.int64 and route_weight.dtype == torch.float16, "routing dtypes")
+    _check(token_idx.numel() == a.size(0) and route_weight.numel() == a.size(0),
+           "routing tensors must have M elements")
+    _check(0 <= int(variant) <= 3, "unknown variant")
+    dev = _require_cuda(a, packed, out, svh, token_idx, route_weight)
+    with _On(dev) as s:
+        _lib.call("exl3_fat_gemm_scatter", _p(a), a.size(0), a.size(1), _p(packed), packed.size(0), packed.size(1),
+                  packed.size(2), _p(out), out.size(0), _p(svh), svh.numel(), _p(token_idx), _p(route_weight),
+                  int(K), int(bool(mcg)), int(bool(mul1)), int(variant), s)
+
+
+def smem_bytes(variant: int) -> int:
+    """kernel/exl3_fat_gemm_v2.cu:316-326: LDS bytes per workgroup of `variant`, -1 if unknown."""
+    return int(_lib.load().exl3_smem_bytes(int(variant)))
+
+
+# ------------------------------------------------------------------------------------------- trellis utilities
+def reconstruct(w: torch.Tensor, packed: torch.Tensor, K: int, mcg: bool, mul1: bool) -> None:
+    """exllamav3 ext.reconstruct(w, packed, K, mcg, mul1): W' fp16 [16 tiles_k, 16 tiles_n]."""
+    _check(packed.dim() == 3 and packed.is_contiguous() and packed.dtype in (torch.int16, torch.uint16),
+           "packed must be contiguous int16 [tiles_k, tiles_n, 16*K]")
+    _check(int(K) in (2, 3, 4) and bool(mcg) and not bool(mul1), "only K2/K3/K4 MCG tensors")
+    _check(packed.size(2) == 16 * int(K), "packed block width must be 16*K int16 words")
+    _check(w.dtype == torch.float16 and w.is_contiguous() and w.shape == (packed.size(0) * 16, packed.size(1) * 16),
+           "w must be contiguous fp16 [16 tiles_k, 16 tiles_n]")
+    dev = _require_cuda(w, packed)
+    with _On(dev) as s:
+        _lib.call("exl3_reconstruct", _p(w), _p(packed), packed.size(0), packed.size(1), int(K), int(bool(mcg)),
+                  int(bool(mul1)), s)
+
+
+def decode_states(states: torch.Tensor, out: torch.Tensor) -> None:
+    """out[i] = fp16 decode(states[i]) with the GEMM's device decoder (states int16/uint16, even count)."""
+    _check(states.dtype in (torch.int16, torch.uint16) and out.dtype in (torch.float16, torch.int16, torch.uint16),
+           "16-bit tensors")
+    _check(states.is_contiguous() and out.is_contiguous() and states.numel() == out.numel() and
+           states.numel() % 2 == 0, "contiguous, equal, even sizes")
+    dev = _require_cuda(states, out)
+    with _On(dev) as s:
+        _lib.call("exl3_decode_states", _p(states), _p(out), states.numel(), s)

@@ -1,0 +1,126 @@
+"""Serving integration for the grouped EXL3 MoE prefill on MI355X (same contract as the reference's
+kernel/exl3_grouped_runtime.py, whose functions and behaviour this module mirrors).
+
+Installed into vLLM's exl3 overlay module by patch_exl3_grouped.py when EXL3_GROUPED_PREFILL != "0".
+Prefill calls (tokens > the fused kernel's row cap) go through one launch per stage over all experts;
+decode calls (tokens <= cap), expert-parallel calls (layer.expert_map set) and layers without w13_trellis keep
+the original path untouched (kernel/exl3_grouped_runtime.py:93-98).
+
+Env:
+  EXL3_GROUPED_PREFILL=1     enable (read by the hook)
+  EXL3_GROUPED_LIB=<path>    prebuilt libexl3_grouped.so (default: exl3_grouped/libexl3_grouped.so beside this file)
+"""
+import logging
+import os
+import sys
+import time
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+if _HERE not in sys.path:
+    sys.path.insert(0, _HERE)
+
+logger = logging.getLogger("vllm.exl3.grouped")
+_ext = None
+_logged = False
+
+
+def _load_ext():
+    """Load the native library once (kernel/exl3_grouped_runtime.py:20-47 JIT-compiles instead; here the
+    library is built ahead of time for gfx950). Raises if it is missing."""
+    global _ext
+    if _ext is not None:
+        return _ext
+    t0 = time.time()
+    import exl3_grouped
+    exl3_grouped._lib.load()
+    _ext = exl3_grouped
+    logger.info("EXL3 grouped prefill library loaded in %.2fs from %s", time.time() - t0, exl3_grouped.library_path())
+    return _ext
+
+
+def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, layer, limit: float,
+                    stage_events: list | None = None) -> torch.Tensor:
+    """x2d [T, K] (any float dtype), ids [T, topk] (int64 or int32), weights [T, topk] -> out [T, K] fp32.
+    Restates kernel/exl3_grouped_runtime.py:50-83 with the route sort on the GPU (sort_routes).
+    stage_events: if a list is given, a timing event recorded on the current stream after each stage is appended
+    as (stage name, event), after a leading ("start", event)."""
+    gp = _load_ext()
+
+    def mark(name):
+        if stage_events is not None:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            stage_events.append((name, ev))
+
+    mark("start")
+    dev = x2d.device
+    T, K = x2d.shape
+    topk = ids.shape[1]
+    R = T * topk
+    E = int(layer.w13_trellis.shape[0])
+    I = int(layer._exl3_intermediate_local)
+    x16 = x2d.to(torch.float16).contiguous()
+    ids = ids.contiguous()
+    weights = weights.contiguous()
+    token_sorted = torch.empty(R, dtype=torch.int64, device=dev)
+    weight_sorted = torch.empty(R, dtype=torch.float16, device=dev)
+    expert_of_row = torch.empty(R, dtype=torch.int32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    expert_row0 = torch.empty(E, dtype=torch.int32, device=dev)
+    gp.sort_routes(ids, weights, E, token_sorted, weight_sorted, expert_of_row, counts, expert_row0)
+    mark("sort_routes")
+    max_blocks = R // 128 + E
+    block_expert = torch.empty(max_blocks, dtype=torch.int32, device=dev)
+    block_row0 = torch.empty_like(block_expert)
+    meta = torch.zeros(2, dtype=torch.int32, device=dev)
+    gp.build_blocks(counts, block_expert, block_row0, meta)
+    mark("build_blocks")
+    h13 = torch.empty(R, K, dtype=torch.float16, device=dev)
+    gp.row_had(x16, h13, token_sorted, expert_of_row, layer.w13_suh[:, 0], True)
+    mark("row_had")
+    gu = torch.empty(R, 2 * I, dtype=torch.float16, device=dev)
+    gp.grouped_gemm(h13, layer.w13_trellis[:, 0], layer.w13_trellis[:, 1], layer.w13_svh[:, 0], layer.w13_svh[:, 1],
+                    block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 0)
+    mark("gemm_gate_up")
+    act = torch.empty(R, I, dtype=torch.float16, device=dev)
+    gp.act_had(gu, act, expert_of_row, layer.w2_suh, float(limit))
+    mark("act_had")
+    out = torch.zeros(T, K, dtype=torch.float32, device=dev)
+    mark("zero_out")
+    gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
+                    block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, out, 1)
+    mark("gemm_down_scatter")
+    return out
+
+
+def install(ov):
+    """Wrap ov.apply_exl3_experts: prefill-sized calls use the grouped path; everything else is untouched
+    (kernel/exl3_grouped_runtime.py:86-112)."""
+    global _logged
+    original = ov.apply_exl3_experts
+
+    def apply_exl3_experts_grouped(x, topk_ids, topk_weights, layer, *, limit=ov.SWIGLU_LIMIT_DEFAULT, fused=None):
+        global _logged
+        tokens = x.shape[-2]
+        temps = getattr(layer, "_exl3_fused_temps", None)
+        cap = int(temps[0].shape[1]) if temps else 0
+        expert_map = getattr(layer, "expert_map", None)
+        if tokens <= cap or expert_map is not None or not hasattr(layer, "w13_trellis"):
+            return original(x, topk_ids, topk_weights, layer, limit=limit, fused=fused)
+        x2d = x.reshape(tokens, x.shape[-1])
+        ids = topk_ids.reshape(tokens, -1).to(torch.long)
+        weights = topk_weights.reshape(tokens, -1)
+        out = grouped_prefill(x2d, ids, weights, layer, float(limit))
+        layer._exl3_last_apply = "grouped"
+        if not _logged:
+            logger.info("EXL3 grouped prefill engaged (tokens=%d > cap=%d, experts=%d)", tokens, cap,
+                        int(layer.w13_trellis.shape[0]))
+            _logged = True
+        return out.to(dtype=x.dtype)
+
+    ov.apply_exl3_experts = apply_exl3_experts_grouped
+    # the MoE method's apply() looks the function up at call time from the module globals, so the wrap sticks
+    _load_ext()  # load at boot rather than on the first prefill
+    logger.info("EXL3 grouped prefill installed (EXL3_GROUPED_PREFILL=1)")

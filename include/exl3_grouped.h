@@ -1,0 +1,160 @@
+/*
+ * exl3_grouped.h -- C ABI of the MI355X (gfx950) EXL3 grouped routed-expert MoE prefill library.
+ *
+ * Every pointer argument is a device pointer (caller-allocated; the library never allocates or frees
+ * device memory). fp16 tensors are passed as uint16_t* (IEEE binary16 bit patterns). `stream` is a
+ * hipStream_t (NULL = the default stream); work is enqueued there with no host synchronisation. Work runs on
+ * the calling thread's current HIP device.
+ *
+ * Every entry point validates its arguments before touching the GPU and returns
+ *   EXL3_OK (0), EXL3_ERR_ARG (1: bad argument, nothing launched) or EXL3_ERR_HIP (2: launch failed);
+ * the message for the last non-zero status of the calling thread is exl3_last_error().
+ *
+ * Reference file:line citations are relative to the reference repository
+ * (siddharth1825/glm53-exl3-prefill); "pybind op" means the torch-extension op the entry point replaces.
+ *
+ * Trellis tensors: [tiles_k, tiles_n, 16*bits] int16 per matrix (bits in {2,3,4}); a tile holds the 16x16
+ * weights W'[16 tk + k][16 tn + n] as 256 bits-wide symbols with a tail-biting 16-bit state window and the
+ * MCG codebook (the bit-level spec is written out in oracle/exl3_oracle.c and DESIGN.md).
+ */
+#ifndef EXL3_GROUPED_H
+#define EXL3_GROUPED_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EXL3_OK 0
+#define EXL3_ERR_ARG 1
+#define EXL3_ERR_HIP 2
+
+#define EXL3_DTYPE_F32 0
+#define EXL3_DTYPE_F16 1
+#define EXL3_DTYPE_BF16 2
+#define EXL3_DTYPE_I32 3
+#define EXL3_DTYPE_I64 4
+
+#define EXL3_GEMM_STORE_F16 0      /* grouped_gemm mode 0: fp16 store into [rows, n_tensors*N] */
+#define EXL3_GEMM_SCATTER_F32 1    /* grouped_gemm mode 1: fp32 atomic add into out[token_sorted[r]] * w[r] */
+
+/* Message for the calling thread's last failing call ("" if none). */
+const char* exl3_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int exl3_abi_version(void);
+
+/*
+ * Route sort: the torch glue of grouped_prefill (kernel/exl3_grouped_runtime.py:59-68) as GPU kernels.
+ * Stable sort of the flat route list i = t*topk + j by expert id:
+ *   token_sorted[r] = i/topk, weight_sorted[r] = fp16(topk_weights[i]), expert_of_row[r] = topk_ids[i],
+ *   counts[e] = #routes of e, expert_row0[e] = exclusive prefix sum of counts.
+ * ids_dtype: EXL3_DTYPE_I64 or EXL3_DTYPE_I32; weights_dtype: EXL3_DTYPE_F32, _F16 or _BF16.
+ * Routes whose id is outside [0, n_experts) are dropped; the rows they would have filled (the tail past
+ * sum(counts)) are written as token 0, weight 0, expert 0, and the number of dropped routes is added to the
+ * int32 at workspace offset 0 (read it after the stream completes to detect bad routing).
+ * workspace: device scratch of exl3_sort_routes_workspace_bytes(...) bytes; its contents need no initialising.
+ */
+size_t exl3_sort_routes_workspace_bytes(int64_t tokens, int topk, int n_experts);
+int exl3_sort_routes(const void* topk_ids, int ids_dtype, const void* topk_weights, int weights_dtype,
+                     int64_t tokens, int topk, int n_experts,
+                     int64_t* token_sorted, uint16_t* weight_sorted, int32_t* expert_of_row,
+                     int32_t* counts, int32_t* expert_row0,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Block table (pybind op build_blocks, kernel/exl3_grouped_prefill.cu:63-96 and :285-294).
+ * counts int32 [n_experts] -> for each 128-row block b of each expert (experts in order):
+ *   block_expert[b] = e, block_row0[b] = expert_row0[e] + 128*i; entries b >= n_blocks get block_expert = -1
+ *   (block_row0 is not written there); meta = {n_blocks, n_rows}. n_experts <= 1024 ("too many experts").
+ */
+int exl3_build_blocks(const int32_t* counts, int n_experts, int max_blocks,
+                      int32_t* block_expert, int32_t* block_row0, int32_t* meta, void* stream);
+
+/*
+ * Input Hadamard (pybind op row_had, kernel/exl3_grouped_prefill.cu:101-115 and :296-311):
+ *   dst[r, :] = fp16( H128( src[gather ? token_sorted[r] : r, :] * suh[expert_of_row[r], :] ) / sqrt(128) )
+ * per 128-column block, fp32 inside. src fp16 [*, K] contiguous, dst fp16 [rows, K] contiguous,
+ * suh fp16 rows of length K at stride suh_stride elements (e.g. w13_suh[:, 0] has stride 2K).
+ * K % 128 == 0 and suh_len == K ("K must be a multiple of 128 and match suh").
+ */
+int exl3_row_had(const uint16_t* src, uint16_t* dst, const int64_t* token_sorted, const int32_t* expert_of_row,
+                 const uint16_t* suh, int64_t suh_stride, int64_t suh_len, int64_t rows, int K, int gather,
+                 void* stream);
+
+/*
+ * Clamped SwiGLU + down Hadamard (pybind op act_had, kernel/exl3_grouped_prefill.cu:118-141 and :313-322):
+ *   a = fp16( silu(min(g, limit)) * clamp(u, -limit, limit) ), g = gu[r, :I], u = gu[r, I:]  (fp32 math)
+ *   act[r, :] = fp16( H128( a * suh_down[expert_of_row[r], :] ) / sqrt(128) )
+ * gu fp16 [rows, gu_width] contiguous with gu_width == 2*I, act fp16 [rows, I], I % 128 == 0.
+ */
+int exl3_act_had(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
+                 const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, void* stream);
+
+/*
+ * Grouped weight-stationary trellis GEMM over all experts (pybind op grouped_gemm,
+ * kernel/exl3_grouped_prefill.cu:148-279 and :324-378).
+ *   a: fp16 [a_rows, size_k] contiguous (rows sorted by expert).
+ *   packed_gate / packed_up: trellis of expert e at packed + e*expert_stride_words, laid out
+ *     [tiles_k, tiles_n, 16*bits] int16 contiguous; packed_up == NULL for the single-tensor (down) stage.
+ *     size_k == 16*tiles_k, size_k % 32 == 0, N_each = 16*tiles_n with N_each % 128 == 0.
+ *   svh_gate / svh_up: fp16 rows of N_each at stride svh_stride (svh_up NULL iff packed_up NULL).
+ *   block table (build_blocks) with max_blocks entries; counts / expert_row0 int32 [n_experts].
+ *   mode EXL3_GEMM_STORE_F16: out fp16 [a_rows, n_tensors*N_each],
+ *        out[r, which*N_each + n] = fp16( H128_n(a[r] @ W'_e,which) / sqrt(128) * svh_e,which[n] )
+ *   mode EXL3_GEMM_SCATTER_F32 (single tensor only): out fp32 [out_rows, N_each], caller-zeroed,
+ *        out[token_sorted[r], n] += fp32(route_weight[r]) * ( H128_n(a[r] @ W'_e) / sqrt(128) * svh_e[n] )
+ *        with device-scope fp32 atomics (order of additions is not deterministic).
+ * gate/up tensors must share expert strides (as [E, 2, ...] views do).
+ */
+int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
+                      const uint16_t* packed_gate, const uint16_t* packed_up, int64_t expert_stride_words,
+                      int tiles_k, int tiles_n, int bits,
+                      const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                      const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
+                      const int32_t* counts, const int32_t* expert_row0, int n_experts,
+                      const int64_t* token_sorted, const uint16_t* route_weight,
+                      void* out, int64_t out_rows, int mode, void* stream);
+
+/*
+ * Per-expert weight-stationary trellis GEMM, the exl3_fat_gemm drop-in (pybind ops fat_gemm_v2 /
+ * fat_gemm_v2_scatter / smem_bytes, kernel/exl3_fat_gemm_v2.cu:236-333; PR77 signature
+ * exl3_fat_gemm(a, packed, out, svh, K, mcg, mul1), kernel/test_fat_v2.py:122,134).
+ *   a fp16 [m, size_k]; packed [size_k/16, n/16, 16*bits] int16; svh fp16 [n]; out fp32.
+ *   store:   out[m, n]  = H128_n(a @ W') / sqrt(128) * svh          (out [m, n])
+ *   scatter: out[token_idx[i], :] += fp32(route_weight[i]) * (same)  (out [out_rows, n], device atomics)
+ * bits must be 2, 3 or 4 with mcg != 0 and mul1 == 0 (the reference accepts only bits 4: "only K4 MCG tensors");
+ * size_k % 64 == 0, n % 128 == 0. variant in [0, 3] selects a tile schedule (the reference's four
+ * smem/pipeline variants); exl3_smem_bytes(variant) returns its LDS bytes per workgroup, or -1 if unknown.
+ */
+int exl3_fat_gemm(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed, int tiles_k, int tiles_n,
+                  int packed_words, float* out, int64_t out_rows, const uint16_t* svh, int64_t svh_len,
+                  int bits, int mcg, int mul1, int variant, void* stream);
+int exl3_fat_gemm_scatter(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed, int tiles_k,
+                          int tiles_n, int packed_words, float* out, int64_t out_rows, const uint16_t* svh,
+                          int64_t svh_len, const int64_t* token_idx, const uint16_t* route_weight,
+                          int bits, int mcg, int mul1, int variant, void* stream);
+int64_t exl3_smem_bytes(int64_t variant);
+
+/*
+ * Trellis reconstruct (exllamav3 ext.reconstruct(w, packed, K, mcg, mul1), called by the reference's tests
+ * at kernel/test_fat_v2.py:91-94 and harness/proto_fp8.py:70): packed [tiles_k, tiles_n, 16*bits] ->
+ * out fp16 [16*tiles_k, 16*tiles_n] row-major (W' in logical [k][n] order).
+ */
+int exl3_reconstruct(uint16_t* out, const uint16_t* packed, int tiles_k, int tiles_n, int bits, int mcg,
+                     int mul1, void* stream);
+
+/*
+ * Decode arbitrary 16-bit trellis states with the GEMM's own device decoder: out[i] = fp16 bits of
+ * decode(states[i]). No counterpart in the reference; it exists so the decoder can be pinned bit-exactly
+ * over all 65536 states. n must be even.
+ */
+int exl3_decode_states(const uint16_t* states, uint16_t* out, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXL3_GROUPED_H */

@@ -1,0 +1,153 @@
+"""C ABI checks that need no GPU: the library loads, exports every entry point include/exl3_grouped.h declares,
+and rejects bad arguments with EXL3_ERR_ARG and a message before launching anything (the reference's
+TORCH_CHECK contract, kernel/exl3_grouped_prefill.cu:288-372, kernel/exl3_fat_gemm_v2.cu:236-252)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import exl3_grouped as gp
+from exl3_grouped import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "exl3_grouped.h")
+FAKE = ctypes.c_void_p(0x1000)        # never dereferenced: every case below fails validation first
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(exl3_\w+)\s*\(", text)))
+
+
+def test_header_declares_what_the_binding_binds():
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.exl3_abi_version() == _lib.ABI_VERSION
+
+
+def rc_and_msg(name, *args):
+    rc = getattr(_lib.load(), name)(*args)
+    return rc, _lib.last_error()
+
+
+def test_build_blocks_rejects_too_many_experts():
+    rc, msg = rc_and_msg("exl3_build_blocks", FAKE, 1025, 10, FAKE, FAKE, FAKE, None)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "too many experts"
+
+
+def test_row_had_rejects_bad_k():
+    rc, msg = rc_and_msg("exl3_row_had", FAKE, FAKE, FAKE, FAKE, FAKE, 100, 100, 4, 100, 1, None)
+    assert rc == _lib.EXL3_ERR_ARG and "multiple of 128" in msg
+    rc, msg = rc_and_msg("exl3_row_had", FAKE, FAKE, FAKE, FAKE, FAKE, 256, 128, 4, 256, 1, None)
+    assert rc == _lib.EXL3_ERR_ARG and "match suh" in msg
+
+
+def test_act_had_rejects_bad_width():
+    rc, msg = rc_and_msg("exl3_act_had", FAKE, 300, FAKE, FAKE, FAKE, 128, 4, 128, ctypes.c_float(10.0), None)
+    assert rc == _lib.EXL3_ERR_ARG and "2I" in msg
+
+
+def _gemm(**kw):
+    a = dict(a=FAKE, a_rows=256, size_k=512, pg=FAKE, pu=None, es=32 * 16 * 64, tk=32, tn=16, bits=4, sg=FAKE,
+             su=None, ss=256, be=FAKE, br=FAKE, mb=10, counts=FAKE, row0=FAKE, E=8, tok=FAKE, rw=FAKE, out=FAKE,
+             out_rows=64, mode=1)
+    a.update(kw)
+    return rc_and_msg("exl3_grouped_gemm", *a.values(), None)
+
+
+def test_grouped_gemm_contract():
+    assert _gemm(bits=5)[0] == _lib.EXL3_ERR_ARG
+    assert "K mismatch" in _gemm(size_k=500)[1]
+    assert "K mismatch" in _gemm(size_k=480, tk=30)[1]                 # K % 64
+    assert "multiple of 128" in _gemm(tn=12)[1]
+    assert "too many experts" in _gemm(E=2000)[1]
+    assert "single tensor" in _gemm(pu=FAKE, su=FAKE)[1]
+    assert "gate/up strides must match" in _gemm(pu=FAKE, su=None)[1]
+    assert "mode" in _gemm(mode=3)[1]
+
+
+def test_fat_gemm_contract():
+    args = dict(a=FAKE, m=300, k=4096, pk=FAKE, tk=256, tn=96, words=64, out=FAKE, out_rows=300, svh=FAKE,
+                svh_len=1536, bits=4, mcg=1, mul1=0, variant=1)
+
+    def call(**kw):
+        a = dict(args)
+        a.update(kw)
+        return rc_and_msg("exl3_fat_gemm", *a.values(), None)
+
+    assert "MCG" in call(mcg=0)[1] and "MCG" in call(mul1=1)[1] and "MCG" in call(bits=5)[1]
+    assert "does not match packed" in call(k=4000)[1]
+    assert "svh N dimension" in call(svh_len=1024)[1]
+    assert "16*K" in call(words=48)[1]
+    assert "unknown variant" in call(variant=4)[1]
+    assert "out shape" in call(out_rows=299)[1]
+    assert _lib.load().exl3_smem_bytes(9) == -1 and _lib.load().exl3_smem_bytes(0) > 0
+
+
+def test_sort_routes_contract():
+    lib = _lib.load()
+    need = lib.exl3_sort_routes_workspace_bytes(100, 8, 288)
+    assert need > 0
+    rc, msg = rc_and_msg("exl3_sort_routes", FAKE, _lib.DTYPE_I64, FAKE, _lib.DTYPE_F32, 100, 8, 288, FAKE, FAKE, FAKE,
+                         FAKE, FAKE, FAKE, need - 1, None)
+    assert rc == _lib.EXL3_ERR_ARG and "workspace" in msg
+    rc, msg = rc_and_msg("exl3_sort_routes", FAKE, _lib.DTYPE_F32, FAKE, _lib.DTYPE_F32, 100, 8, 288, FAKE, FAKE,
+                         FAKE, FAKE, FAKE, FAKE, need, None)
+    assert rc == _lib.EXL3_ERR_ARG and "int64 or int32" in msg
+
+
+def test_decode_and_reconstruct_contract():
+    assert "even" in rc_and_msg("exl3_decode_states", FAKE, FAKE, 3, None)[1]
+    assert "MCG" in rc_and_msg("exl3_reconstruct", FAKE, FAKE, 2, 2, 4, 1, 1, None)[1]
+
+
+# ------------------------------------------------------------------------------------------- torch shim
+def test_shim_checks_dtypes_before_device():
+    c = torch.zeros(8, dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="int32 tensors"):
+        gp.build_blocks(c, c, c, c)
+    i32 = torch.zeros(8, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="tensors must be CUDA"):
+        gp.build_blocks(i32, torch.zeros(20, dtype=torch.int32), torch.zeros(20, dtype=torch.int32),
+                        torch.zeros(2, dtype=torch.int32))
+
+
+def test_shim_fat_gemm_messages():
+    a = torch.zeros(300, 4096, dtype=torch.float16)
+    pk = torch.zeros(256, 96, 64, dtype=torch.int16)
+    out = torch.zeros(300, 1536)
+    svh = torch.zeros(1536, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="only K2/K3/K4 MCG tensors"):
+        gp.fat_gemm_v2(a, pk, out, svh, 4, False, False, 1)
+    with pytest.raises(RuntimeError, match="a must be float16"):
+        gp.fat_gemm_v2(a.float(), pk, out, svh, 4, True, False, 1)
+    with pytest.raises(RuntimeError, match="unknown variant"):
+        gp.fat_gemm_v2(a, pk, out, svh, 4, True, False, 7)
+    with pytest.raises(RuntimeError, match="tensors must be CUDA"):
+        gp.fat_gemm_v2(a, pk, out, svh, 4, True, False, 1)
+    assert gp.smem_bytes(5) == -1
+
+
+def test_shim_grouped_gemm_messages():
+    a = torch.zeros(256, 512, dtype=torch.float16)
+    w13 = torch.zeros(8, 2, 32, 16, 64, dtype=torch.int16)
+    svh = torch.zeros(8, 2, 256, dtype=torch.float16)
+    i32 = torch.zeros(20, dtype=torch.int32)
+    gu = torch.zeros(256, 512, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="a fp16 contiguous"):
+        gp.grouped_gemm(a.float(), w13[:, 0], w13[:, 1], svh[:, 0], svh[:, 1], i32, i32, i32[:8], i32[:8], None,
+                        None, gu, 0)
+    with pytest.raises(RuntimeError, match="mode 0"):
+        gp.grouped_gemm(a, w13[:, 0], w13[:, 1], svh[:, 0], svh[:, 1], i32, i32, i32[:8], i32[:8], None, None,
+                        gu[:, :256], 0)
+    with pytest.raises(RuntimeError, match="tensors must be CUDA"):
+        gp.grouped_gemm(a, w13[:, 0], w13[:, 1], svh[:, 0], svh[:, 1], i32, i32, i32[:8], i32[:8], None, None,
+                        gu, 0)

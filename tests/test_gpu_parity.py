@@ -1,0 +1,306 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle on the same seeded inputs.
+
+Bars: bit-exact for integer / byte work (decode, reconstruct, route sort, block table); for floating point the
+north-star tolerance rel L2 <= 1e-3 against the oracle (tighter bars are asserted where the arithmetic allows:
+fp16 stage outputs may differ from the float64 oracle by one fp16 rounding step, fp32 GEMM outputs by fp32
+accumulation order). At the headline size, where the full CPU loop is too slow for a test, parity is checked on
+sampled tokens plus size-independent properties (linearity in the route weights, token-permutation
+equivariance).
+"""
+import numpy as np
+import pytest
+import torch
+
+import exl3_grouped as gp
+import exl3_grouped_runtime as rt
+import exl3_oracle as O
+from exl3_grouped import synth
+
+pytestmark = pytest.mark.gpu
+LIMIT = 10.0
+
+
+def to_np_layer(L):
+    return O.Layer(L.w13_trellis, L.w13_suh, L.w13_svh, L.w2_trellis, L.w2_suh, L.w2_svh)
+
+
+def t16(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def within_f16_steps(got, ref, steps=1, frac=0.999):
+    """Fraction of elements within `steps` fp16 spacings of the reference (fp16 outputs)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    spacing = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    ok = np.abs(got - ref) <= steps * spacing + 1e-7
+    return ok.mean() >= frac
+
+
+# ------------------------------------------------------------------------------------------- decode
+def test_decode_states_all_65536_bit_exact(dev):
+    states = torch.arange(65536, dtype=torch.int32).to(torch.int16).to(dev)
+    out = torch.empty(65536, dtype=torch.int16, device=dev)
+    gp.decode_states(states, out)
+    got = out.cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, O.decode_lut())
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_reconstruct_bit_exact(dev, bits):
+    rng = np.random.default_rng(100 + bits)
+    for tk, tn in [(1, 1), (3, 8), (64, 48)]:
+        pk = rng.integers(0, 65536, (tk, tn, 16 * bits), dtype=np.uint16).view(np.int16)
+        w = torch.empty(tk * 16, tn * 16, dtype=torch.float16, device=dev)
+        gp.reconstruct(w, t16(pk, dev), bits, True, False)
+        assert np.array_equal(w.cpu().numpy().view(np.uint16), O.reconstruct(pk).view(np.uint16)), (tk, tn)
+
+
+# ------------------------------------------------------------------------------------------- routing
+ROUTINGS = [("softmax", 128, 8, 2), ("softmax", 1024, 288, 8), ("zipf", 8192, 288, 8), ("thin", 7168, 288, 8),
+            ("skewed", 2048, 288, 8), ("softmax", 1, 288, 8), ("softmax", 3000, 1024, 6)]
+
+
+def gpu_sort(ids_t, w_t, E):
+    dev = ids_t.device
+    R = ids_t.numel()
+    ts = torch.empty(R, dtype=torch.int64, device=dev)
+    ws = torch.empty(R, dtype=torch.float16, device=dev)
+    eor = torch.empty(R, dtype=torch.int32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    row0 = torch.empty(E, dtype=torch.int32, device=dev)
+    work = gp.sort_routes(ids_t, w_t, E, ts, ws, eor, counts, row0)
+    dropped = int(work[:4].view(torch.int32).item())
+    return ts.cpu().numpy(), ws.cpu().numpy(), eor.cpu().numpy(), counts.cpu().numpy(), row0.cpu().numpy(), dropped
+
+
+@pytest.mark.parametrize("kind,T,E,k", ROUTINGS)
+def test_sort_routes_bit_exact(dev, kind, T, E, k):
+    ids, w = synth.make_routing(kind, T, E, k, seed=T)
+    ref = O.sort_routes(ids, w, E)
+    for ids_dt in (torch.int64, torch.int32):
+        got = gpu_sort(torch.from_numpy(ids).to(ids_dt).to(dev), torch.from_numpy(w).to(dev), E)
+        assert got[5] == 0
+        for g, r in zip(got[:5], ref):
+            assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(r).view(np.uint8))
+
+
+@pytest.mark.parametrize("wdt", [torch.float16, torch.bfloat16])
+def test_sort_routes_weight_dtypes(dev, wdt):
+    ids, w = synth.make_routing("softmax", 500, 64, 8, seed=5)
+    wt = torch.from_numpy(w).to(wdt)
+    ref = O.sort_routes(ids, wt.float().numpy(), 64)
+    got = gpu_sort(torch.from_numpy(ids).to(dev), wt.to(dev), 64)
+    assert np.array_equal(got[1].view(np.uint16), ref[1].view(np.uint16))
+
+
+def test_sort_routes_empty_and_dropped(dev):
+    got = gpu_sort(torch.zeros(0, 8, dtype=torch.int64, device=dev), torch.zeros(0, 8, device=dev), 16)
+    assert got[3].tolist() == [0] * 16 and got[4].tolist() == [0] * 16 and got[5] == 0
+    ids = np.array([[0, 3], [20, 1], [-1, 3]], np.int64)
+    w = np.full((3, 2), 0.5, np.float32)
+    ts, ws, eor, counts, row0, dropped = gpu_sort(torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev), 4)
+    assert dropped == 2 and counts.tolist() == [1, 1, 0, 2] and row0.tolist() == [0, 1, 2, 2]
+    assert ts[:4].tolist() == [0, 1, 0, 2] and eor[:4].tolist() == [0, 1, 3, 3]
+    assert ts[4:].tolist() == [0, 0] and eor[4:].tolist() == [0, 0] and ws[4:].tolist() == [0, 0]
+
+
+@pytest.mark.parametrize("kind,T,E,k", ROUTINGS)
+def test_build_blocks_bit_exact(dev, kind, T, E, k):
+    ids, w = synth.make_routing(kind, T, E, k, seed=T + 1)
+    counts = np.bincount(ids.ravel(), minlength=E).astype(np.int32)
+    R = ids.size
+    for max_blocks in (R // 128 + E, max(1, R // 512)):
+        rbe, rbr, rmeta = O.build_blocks(counts, max_blocks, init=-7)
+        be = torch.full((max_blocks,), -7, dtype=torch.int32, device=dev)
+        br = torch.full((max_blocks,), -7, dtype=torch.int32, device=dev)
+        meta = torch.zeros(2, dtype=torch.int32, device=dev)
+        gp.build_blocks(t16(counts, dev), be, br, meta)
+        assert np.array_equal(be.cpu().numpy(), rbe) and np.array_equal(br.cpu().numpy(), rbr)
+        assert np.array_equal(meta.cpu().numpy(), rmeta)
+
+
+# ------------------------------------------------------------------------------------------- Hadamard passes
+@pytest.mark.parametrize("gather", [True, False])
+def test_row_had(dev, gather):
+    rng = np.random.default_rng(7)
+    T, H, E, R = 300, 4096, 20, 1200
+    x = rng.standard_normal((T if gather else R, H)).astype(np.float16)
+    tok = rng.integers(0, T, R).astype(np.int64)
+    eor = np.sort(rng.integers(0, E, R)).astype(np.int32)
+    suh2 = synth._signs(rng, (E, 2, H))
+    dst = torch.empty(R, H, dtype=torch.float16, device=dev)
+    suh_t = t16(suh2, dev)
+    gp.row_had(t16(x, dev), dst, t16(tok, dev) if gather else None, t16(eor, dev), suh_t[:, 0], gather)
+    ref = O.row_had(x, tok if gather else None, eor, suh2[:, 0], gather)
+    got = dst.cpu().numpy()
+    assert O.rel_l2(got, ref) < 1e-4 and within_f16_steps(got, ref)
+
+
+@pytest.mark.parametrize("scale", [1.0, 12.0])
+def test_act_had(dev, scale):
+    rng = np.random.default_rng(8)
+    R, I, E = 2000, 768, 30
+    gu = (rng.standard_normal((R, 2 * I)) * scale).astype(np.float16)     # scale 12 drives the clamp
+    eor = np.sort(rng.integers(0, E, R)).astype(np.int32)
+    suh = synth._signs(rng, (E, I))
+    act = torch.empty(R, I, dtype=torch.float16, device=dev)
+    gp.act_had(t16(gu, dev), act, t16(eor, dev), t16(suh, dev), LIMIT)
+    ref = O.act_had(gu, eor, suh, LIMIT)
+    got = act.cpu().numpy()
+    # fp16 rounding of the SwiGLU output can land one step apart (fast exp vs libm exp) before the Hadamard
+    assert O.rel_l2(got, ref) < 1e-3 and within_f16_steps(got, ref, steps=2, frac=0.99)
+
+
+# ------------------------------------------------------------------------------------------- grouped GEMM
+def stage_inputs(name, seed, T=None, bits=None, svh_scale=1.0):
+    L, x, ids, w, cfg = synth.make_config(name, seed=seed, T=T, bits=bits, svh_scale=svh_scale)
+    layer = to_np_layer(L)
+    ts, ws, eor, counts, row0 = O.sort_routes(ids, w, cfg["E"])
+    return L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0)
+
+
+def gpu_blocks(counts, R, E, dev):
+    mb = R // 128 + E
+    be = torch.empty(mb, dtype=torch.int32, device=dev)
+    br = torch.empty(mb, dtype=torch.int32, device=dev)
+    meta = torch.zeros(2, dtype=torch.int32, device=dev)
+    gp.build_blocks(t16(counts, dev), be, br, meta)
+    return be, br
+
+
+@pytest.mark.parametrize("name,T", [("tiny", None), ("layer1k", None), ("headline", 256)])
+def test_grouped_gemm_gate_up(dev, name, T):
+    L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, 1, T=T)
+    R = ids.size
+    h13 = O.row_had(x.astype(np.float16), ts, eor, L.w13_suh[:, 0], True)
+    cache = O.WeightCache(layer)
+    ref = O.grouped_gemm_mode0(h13, cache, counts, row0)
+    TL = synth.to_device(L, dev)
+    be, br = gpu_blocks(counts, R, cfg["E"], dev)
+    gu = torch.empty(R, 2 * cfg["I"], dtype=torch.float16, device=dev)
+    gp.grouped_gemm(t16(h13, dev), TL.w13_trellis[:, 0], TL.w13_trellis[:, 1], TL.w13_svh[:, 0], TL.w13_svh[:, 1],
+                    be, br, t16(counts, dev), t16(row0, dev), None, None, gu, 0)
+    got = gu.cpu().numpy()
+    assert O.rel_l2(got, ref) < 1e-4 and within_f16_steps(got, ref)
+
+
+@pytest.mark.parametrize("name,T", [("tiny", None), ("layer1k", None), ("thin", 512)])
+def test_grouped_gemm_down_scatter(dev, name, T):
+    L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, 2, T=T)
+    R = ids.size
+    rng = np.random.default_rng(9)
+    act = (rng.standard_normal((R, cfg["I"])) * 3).astype(np.float16)
+    cache = O.WeightCache(layer)
+    ref = O.grouped_gemm_mode1(act, cache, counts, row0, ts, ws, cfg["T"])
+    TL = synth.to_device(L, dev)
+    be, br = gpu_blocks(counts, R, cfg["E"], dev)
+    out = torch.zeros(cfg["T"], cfg["H"], dtype=torch.float32, device=dev)
+    gp.grouped_gemm(t16(act, dev), TL.w2_trellis, None, TL.w2_svh, None, be, br, t16(counts, dev), t16(row0, dev),
+                    t16(ts, dev), t16(ws, dev), out, 1)
+    assert O.rel_l2(out.cpu().numpy(), ref) < 1e-5
+
+
+# ------------------------------------------------------------------------------------------- fat GEMM (config 2)
+@pytest.mark.parametrize("M", [300, 4096])
+def test_fat_gemm_config2(dev, M):
+    a, packed, svh = synth.make_fat(0, M=M)
+    ref = O.fat_gemm(a, packed, svh, dtype=np.float32)
+    outs = []
+    for v in range(4):
+        out = torch.empty(M, 1536, dtype=torch.float32, device=dev)
+        gp.fat_gemm_v2(t16(a, dev), t16(packed, dev), out, t16(svh, dev), 4, True, False, v)
+        outs.append(out.cpu().numpy())
+    assert O.rel_l2(outs[0], ref) < 1e-5
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])                                # variants are bit-identical
+
+
+def test_fat_gemm_scatter(dev):
+    M, T = 300, 4096
+    a, packed, svh = synth.make_fat(1, M=M, K=1024, N=4096)
+    rng = np.random.default_rng(11)
+    tok = rng.permutation(T)[:M].astype(np.int64)
+    rw = (rng.random(M) * 0.5 + 0.25).astype(np.float16)
+    out0 = np.zeros((T, 4096), np.float32)
+    ref = O.fat_gemm_scatter(a, packed, svh, tok, rw, out0, dtype=np.float32)
+    out = torch.zeros(T, 4096, dtype=torch.float32, device=dev)
+    gp.fat_gemm_v2_scatter(t16(a, dev), t16(packed, dev), out, t16(svh, dev), t16(tok, dev), t16(rw, dev), 4, True,
+                           False, 1)
+    assert O.rel_l2(out.cpu().numpy(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+def test_fat_gemm_low_bits(dev, bits):
+    a, packed, svh = synth.make_fat(2, M=200, K=1024, N=768, bits=bits)
+    ref = O.fat_gemm(a, packed, svh)
+    out = torch.empty(200, 768, dtype=torch.float32, device=dev)
+    gp.fat_gemm_v2(t16(a, dev), t16(packed, dev), out, t16(svh, dev), bits, True, False, 1)
+    assert O.rel_l2(out.cpu().numpy(), ref) < 1e-5
+
+
+# ------------------------------------------------------------------------------------------- full layer
+class Fake:
+    pass
+
+
+def run_layer(L, x, ids, w, dev):
+    TL = synth.to_device(L, dev)
+    out = rt.grouped_prefill(t16(x, dev), t16(ids, dev), t16(w, dev), TL, LIMIT)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("name,svh_scale", [("tiny", 1.0), ("tiny", 1 / 64), ("layer1k", 1.0), ("layer1k", 1 / 64)])
+def test_layer_vs_expert_loop(dev, name, svh_scale):
+    L, x, ids, w, cfg = synth.make_config(name, seed=4, svh_scale=svh_scale)
+    got = run_layer(L, x, ids, w, dev).cpu().numpy()
+    layer = to_np_layer(L)
+    ref = O.expert_loop(x, ids, w, layer, LIMIT)
+    assert O.rel_l2(got, ref) < 1e-3
+    staged = O.grouped_prefill(x, ids, w, layer, LIMIT)
+    assert O.rel_l2(got, staged) < 1e-4
+
+
+def sampled_loop(L, x, ids, w, tokens):
+    layer = to_np_layer(L)
+    return O.expert_loop(x[tokens], ids[tokens], w[tokens], layer, LIMIT)
+
+
+def test_headline_sampled_tokens_and_properties(dev):
+    L, x, ids, w, cfg = synth.make_config("headline", seed=0)
+    out = run_layer(L, x, ids, w, dev)
+    tokens = np.random.default_rng(0).choice(cfg["T"], 24, replace=False)
+    ref = sampled_loop(L, x, ids, w, tokens)
+    assert O.rel_l2(out.cpu().numpy()[tokens], ref) < 1e-3
+    # linearity in the route weights (x2 is exact in fp16)
+    out2 = run_layer(L, x, ids, 2 * w, dev)
+    assert (out2 - 2 * out).norm().item() <= 1e-6 * out.norm().item()
+    # token permutation equivariance
+    perm = np.random.default_rng(1).permutation(cfg["T"])
+    outp = run_layer(L, x[perm], ids[perm], w[perm], dev)
+    assert (outp - out[torch.from_numpy(perm).to(dev)]).norm().item() <= 1e-6 * out.norm().item()
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_thin_config_all_bits(dev, bits):
+    L, x, ids, w, cfg = synth.make_config("thin", seed=0, bits=bits)
+    out = run_layer(L, x, ids, w, dev).cpu().numpy()
+    tokens = np.random.default_rng(bits).choice(cfg["T"], 16, replace=False)
+    assert O.rel_l2(out[tokens], sampled_loop(L, x, ids, w, tokens)) < 1e-3
+
+
+def test_install_engages_grouped_path(dev):
+    L, x, ids, w, cfg = synth.make_config("tiny", seed=5)
+    ov = Fake()
+    ov.SWIGLU_LIMIT_DEFAULT = LIMIT
+    ov.apply_exl3_experts = lambda *a, **k: "original"
+    rt.install(ov)
+    TL = synth.to_device(L, dev)
+    TL._exl3_fused_temps = [torch.zeros(1, 64)]
+    xb = t16(x, dev).to(torch.bfloat16)
+    got = ov.apply_exl3_experts(xb, t16(ids, dev).to(torch.int32), t16(w, dev), TL, limit=LIMIT)
+    assert got.dtype == torch.bfloat16 and TL._exl3_last_apply == "grouped"
+    ref = rt.grouped_prefill(xb, t16(ids, dev), t16(w, dev), TL, LIMIT)
+    assert torch.allclose(got.float(), ref.to(torch.bfloat16).float())
+    assert ov.apply_exl3_experts(xb[:64], t16(ids, dev)[:64], t16(w, dev)[:64], TL) == "original"

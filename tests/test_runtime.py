@@ -1,0 +1,96 @@
+"""Host-side logic that needs no GPU: the serving wrapper's pass-through rules
+(kernel/exl3_grouped_runtime.py:91-107), the idempotent overlay hook (kernel/patch_exl3_grouped.py:6-22) and the
+synthetic generators."""
+import types
+
+import numpy as np
+import pytest
+import torch
+
+import exl3_grouped_runtime as rt
+import patch_exl3_grouped as patcher
+from exl3_grouped import synth
+
+
+class FakeLayer(torch.nn.Module):
+    pass
+
+
+def fake_overlay():
+    calls = []
+
+    def original(x, topk_ids, topk_weights, layer, *, limit=10.0, fused=None):
+        calls.append(dict(tokens=x.shape[-2], limit=limit, fused=fused))
+        return "original"
+
+    ov = types.SimpleNamespace(apply_exl3_experts=original, SWIGLU_LIMIT_DEFAULT=10.0)
+    return ov, calls
+
+
+def test_install_passes_through_decode_ep_and_non_trellis_layers():
+    ov, calls = fake_overlay()
+    rt.install(ov)
+    assert ov.apply_exl3_experts is not None and ov.apply_exl3_experts.__name__ == "apply_exl3_experts_grouped"
+    x = torch.zeros(64, 512, dtype=torch.float16)
+    ids = torch.zeros(64, 8, dtype=torch.long)
+    w = torch.zeros(64, 8)
+    # decode-sized call: tokens <= cap (cap = layer._exl3_fused_temps[0].shape[1])
+    layer = FakeLayer()
+    layer.w13_trellis = torch.zeros(4, 2, 32, 16, 64, dtype=torch.int16)
+    layer._exl3_fused_temps = [torch.zeros(1, 128)]
+    layer.expert_map = None
+    assert ov.apply_exl3_experts(x, ids, w, layer, limit=7.0, fused="f") == "original"
+    assert calls[-1] == dict(tokens=64, limit=7.0, fused="f")
+    # expert-parallel layer
+    layer2 = FakeLayer()
+    layer2.w13_trellis = layer.w13_trellis
+    layer2.expert_map = torch.arange(4)
+    assert ov.apply_exl3_experts(torch.zeros(300, 512), ids, w, layer2) == "original"
+    # layer without trellis weights
+    layer3 = FakeLayer()
+    layer3.expert_map = None
+    assert ov.apply_exl3_experts(torch.zeros(300, 512), ids, w, layer3) == "original"
+    assert len(calls) == 3
+
+
+def test_patch_hook_is_idempotent(tmp_path):
+    target = tmp_path / "exl3.py"
+    target.write_text("SWIGLU_LIMIT_DEFAULT = 10.0\n")
+    assert patcher.patch(target, "/opt/somewhere") is True
+    text = target.read_text()
+    assert patcher.MARKER in text and "EXL3_GROUPED_PREFILL" in text and "/opt/somewhere" in text
+    assert patcher.patch(target, "/opt/somewhere") is False
+    assert target.read_text() == text
+    compile(text, str(target), "exec")
+
+
+def test_generators_are_deterministic():
+    a = synth.make_config("tiny", seed=3)
+    b = synth.make_config("tiny", seed=3)
+    for u, v in zip(a[:4], b[:4]):
+        if isinstance(u, np.ndarray):
+            assert np.array_equal(u, v)
+    assert np.array_equal(a[0].w13_trellis, b[0].w13_trellis)
+    assert np.array_equal(a[0].w13_suh[:, 0], a[0].w13_suh[:, 1])       # gate/up share suh
+    c = synth.make_config("tiny", seed=4)
+    assert not np.array_equal(a[0].w13_trellis, c[0].w13_trellis)
+
+
+@pytest.mark.parametrize("kind", ["softmax", "zipf", "thin", "skewed"])
+def test_routing_shapes_and_distinct_ids(kind):
+    ids, w = synth.make_routing(kind, 512, 288, 8, seed=1)
+    assert ids.shape == (512, 8) and w.shape == (512, 8)
+    assert ids.min() >= 0 and ids.max() < 288
+    assert all(len(set(r)) == 8 for r in ids.tolist())
+    assert np.allclose(w.sum(1), 1.0, atol=1e-5) and (w > 0).all()
+
+
+def test_zipf_and_thin_skews():
+    ids, _ = synth.routing_zipf(8192, 288, 8, 1.1, 0)
+    c = np.sort(np.bincount(ids.ravel(), minlength=288))[::-1]
+    assert c[0] > 0.9 * 8192 and c[:16].sum() > 0.7 * c.sum()
+    ids, _ = synth.routing_thin(7168, 288, 8, 0)
+    c = np.bincount(ids.ravel(), minlength=288)
+    cs = np.sort(c)[::-1]
+    assert 0.5 < cs[:16].sum() / c.sum() < 0.65          # 16 hot experts take ~60%
+    assert 180 <= int((c <= 16).sum()) <= 220            # ~200 experts with <= 16 rows
