@@ -22,33 +22,42 @@ constexpr uint32_t MCG_MUL_HI = 0xCBACu;       // high 16 bits
 constexpr uint32_t MCG_XOR = 0x3B603B60u;
 constexpr uint32_t MCG_MASK = 0x8FFF8FFFu;
 
-// x = s * 0xCBAC1FED (mod 2^32) where s = low (HI = 0) or high (HI = 1) 16 bits of r.
-template <int HI>
-__device__ __forceinline__ uint32_t mcg_mul(uint32_t r)
+// gfx950 forwards a VALU result written through an SDWA destination select (a partial-register write) to the
+// next instruction stale: the consumer must be at least one instruction later. The compiler cannot place that
+// wait inside an asm statement, so every asm block below orders its instructions so that each partial write is
+// followed by an independent instruction before its first reader.
+
+// x0 = lo(ra) * 0xCBAC1FED, x1 = (HI1 ? hi : lo)(rb) * 0xCBAC1FED  (mod 2^32), both as full 32-bit products.
+template <int HI1>
+__device__ __forceinline__ void mcg_mul2(uint32_t ra, uint32_t rb, uint32_t& x0, uint32_t& x1)
 {
-    uint32_t t, x;
+    uint32_t t0, t1;
     const uint32_t chi = MCG_MUL_HI, clo = MCG_MUL_LO;
-    if constexpr (HI == 0)
-        asm("v_mul_lo_u16_sdwa %0, %2, %3 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD\n\t"
-            "v_mad_u32_u16 %1, %2, %4, %0"
-            : "=&v"(t), "=v"(x) : "v"(r), "v"(chi), "v"(clo));
+    if constexpr (HI1)
+        asm("v_mul_lo_u16_sdwa %0, %4, %6 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD\n\t"
+            "v_mul_lo_u16_sdwa %1, %5, %6 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:DWORD\n\t"
+            "v_mad_u32_u16 %2, %4, %7, %0\n\t"
+            "v_mad_u32_u16 %3, %5, %7, %1 op_sel:[1,0,0,0]"
+            : "=&v"(t0), "=&v"(t1), "=&v"(x0), "=&v"(x1) : "v"(ra), "v"(rb), "v"(chi), "v"(clo));
     else
-        asm("v_mul_lo_u16_sdwa %0, %2, %3 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:DWORD\n\t"
-            "v_mad_u32_u16 %1, %2, %4, %0 op_sel:[1,0,0,0]"
-            : "=&v"(t), "=v"(x) : "v"(r), "v"(chi), "v"(clo));
-    return x;
+        asm("v_mul_lo_u16_sdwa %0, %4, %6 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD\n\t"
+            "v_mul_lo_u16_sdwa %1, %5, %6 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD\n\t"
+            "v_mad_u32_u16 %2, %4, %7, %0\n\t"
+            "v_mad_u32_u16 %3, %5, %7, %1"
+            : "=&v"(t0), "=&v"(t1), "=&v"(x0), "=&v"(x1) : "v"(ra), "v"(rb), "v"(chi), "v"(clo));
 }
 
 __device__ __forceinline__ uint32_t mcg_mask(uint32_t x) { return (x & MCG_MASK) ^ MCG_XOR; }
 
-// Packed fp16 pair {fp16(ya.lo + ya.hi), fp16(yb.lo + yb.hi)} (first in the low half).
-__device__ __forceinline__ uint32_t add_halves_pair(uint32_t ya, uint32_t yb)
+// Two packed fp16 pairs: w0 = {fp16(ya.lo + ya.hi), fp16(yb.lo + yb.hi)}, w1 = {same for yc, yd}.
+__device__ __forceinline__ void add_halves_2pairs(uint32_t ya, uint32_t yb, uint32_t yc, uint32_t yd,
+                                                  uint32_t& w0, uint32_t& w1)
 {
-    uint32_t w;
-    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-        "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
-        : "=&v"(w) : "v"(ya), "v"(yb));
-    return w;
+    asm("v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %1, %4, %4 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %0, %3, %3 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %1, %5, %5 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+        : "=&v"(w0), "=&v"(w1) : "v"(ya), "v"(yb), "v"(yc), "v"(yd));
 }
 
 // Decoded chunk, as four packed fp16 pairs ordered for a [n][k] (k-contiguous) destination:
@@ -77,7 +86,7 @@ __device__ __forceinline__ ChunkLoc chunk_loc(int c)
 template <int BITS>
 __device__ __forceinline__ Chunk4 decode_chunk(uint32_t lo, uint32_t hi, int off)
 {
-    uint32_t y[8];
+    uint32_t x[8];
     if constexpr (BITS == 4)
     {
         // off == 20 for every chunk: states j and j+4 are the low/high halves of one shifted dword
@@ -85,30 +94,36 @@ __device__ __forceinline__ Chunk4 decode_chunk(uint32_t lo, uint32_t hi, int off
         const uint32_t r1 = __builtin_amdgcn_alignbit(hi, lo, 20);   // states 0, 4
         const uint32_t r2 = __builtin_amdgcn_alignbit(hi, lo, 24);   // states 1, 5
         const uint32_t r3 = __builtin_amdgcn_alignbit(hi, lo, 28);   // states 2, 6
-        y[0] = mcg_mask(mcg_mul<0>(r1)); y[4] = mcg_mask(mcg_mul<1>(r1));
-        y[1] = mcg_mask(mcg_mul<0>(r2)); y[5] = mcg_mask(mcg_mul<1>(r2));
-        y[2] = mcg_mask(mcg_mul<0>(r3)); y[6] = mcg_mask(mcg_mul<1>(r3));
-        y[3] = mcg_mask(mcg_mul<0>(r0)); y[7] = mcg_mask(mcg_mul<1>(r0));
+        mcg_mul2<1>(r1, r1, x[0], x[4]);
+        mcg_mul2<1>(r2, r2, x[1], x[5]);
+        mcg_mul2<1>(r3, r3, x[2], x[6]);
+        mcg_mul2<1>(r0, r0, x[3], x[7]);
     }
     else
     {
         const uint64_t q = ((uint64_t) hi << 32) | lo;
+        uint32_t r[8];
         #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            y[j] = mcg_mask(mcg_mul<0>((uint32_t) (q >> (off + j * BITS))));
+        for (int j = 0; j < 8; ++j) r[j] = (uint32_t) (q >> (off + j * BITS));
+        #pragma unroll
+        for (int j = 0; j < 8; j += 2) mcg_mul2<0>(r[j], r[j + 1], x[j], x[j + 1]);
     }
-    Chunk4 r;
-    r.w[0] = add_halves_pair(y[0], y[1]);
-    r.w[1] = add_halves_pair(y[2], y[3]);
-    r.w[2] = add_halves_pair(y[4], y[5]);
-    r.w[3] = add_halves_pair(y[6], y[7]);
-    return r;
+    uint32_t y[8];
+    #pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = mcg_mask(x[j]);
+    Chunk4 c;
+    add_halves_2pairs(y[0], y[1], y[2], y[3], c.w[0], c.w[1]);
+    add_halves_2pairs(y[4], y[5], y[6], y[7], c.w[2], c.w[3]);
+    return c;
 }
 
-// Decode two independent states (low and high half of r) -> packed fp16 pair.
-__device__ __forceinline__ uint32_t decode_state_pair(uint32_t r)
+// Decode four independent states (low and high halves of ra and rb) -> packed fp16 pairs (wa for ra, wb for rb).
+__device__ __forceinline__ void decode_state_pairs(uint32_t ra, uint32_t rb, uint32_t& wa, uint32_t& wb)
 {
-    return add_halves_pair(mcg_mask(mcg_mul<0>(r)), mcg_mask(mcg_mul<1>(r)));
+    uint32_t x0, x1, x2, x3;
+    mcg_mul2<1>(ra, ra, x0, x1);
+    mcg_mul2<1>(rb, rb, x2, x3);
+    add_halves_2pairs(mcg_mask(x0), mcg_mask(x1), mcg_mask(x2), mcg_mask(x3), wa, wb);
 }
 
 }  // namespace exl3

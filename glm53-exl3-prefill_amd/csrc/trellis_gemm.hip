@@ -165,7 +165,8 @@ void trellis_gemm_kernel(const GemmParams p)
             const int b0 = 8 * i * BITS + BITS - 16;           // window start of chunk 4j+i relative to dword bj
             const int rel = (b0 >= 0 ? b0 / 32 : -1) + 1;
             const int off = b0 - 32 * (rel - 1);
-            c[i] = decode_chunk<BITS>(r[rel], r[rel + 1], off);
+            // the lane's bits end inside r[BITS]; a window that ends there never reads its upper dword
+            c[i] = decode_chunk<BITS>(r[rel], r[rel + 1 <= BITS ? rel + 1 : BITS], off);
         }
         const uint4 v0 = {c[0].w[0], c[1].w[0], c[2].w[0], c[3].w[0]};
         const uint4 v1 = {c[0].w[1], c[1].w[1], c[2].w[1], c[3].w[1]};
@@ -311,7 +312,7 @@ void reconstruct_kernel(uint16_t* __restrict__ out, const uint32_t* __restrict__
         const int b0 = 8 * i * BITS + BITS - 16;
         const int rel = (b0 >= 0 ? b0 / 32 : -1) + 1;
         const int off = b0 - 32 * (rel - 1);
-        const Chunk4 c = decode_chunk<BITS>(r[rel], r[rel + 1], off);
+        const Chunk4 c = decode_chunk<BITS>(r[rel], r[rel + 1 <= BITS ? rel + 1 : BITS], off);
         // chunk 4j+i: k0 = 2i, columns j and j+8
         #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -325,10 +326,16 @@ void reconstruct_kernel(uint16_t* __restrict__ out, const uint32_t* __restrict__
     }
 }
 
+// Each thread decodes two dwords (four states); n2 = number of dwords.
 __global__ void decode_states_kernel(const uint32_t* __restrict__ states, uint32_t* __restrict__ out, int64_t n2)
 {
-    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n2) out[i] = decode_state_pair(states[i]);
+    const int64_t i = 2 * ((int64_t) blockIdx.x * blockDim.x + threadIdx.x);
+    if (i >= n2) return;
+    const uint32_t ra = states[i], rb = (i + 1 < n2) ? states[i + 1] : 0u;
+    uint32_t wa, wb;
+    decode_state_pairs(ra, rb, wa, wb);
+    out[i] = wa;
+    if (i + 1 < n2) out[i + 1] = wb;
 }
 
 template <int BITS, int MODE, bool DENSE>
@@ -509,7 +516,7 @@ extern "C" int exl3_decode_states(const uint16_t* states, uint16_t* out, int64_t
                "states/out must be 4-byte aligned");
     const int64_t n2 = n / 2;
     if (n2 == 0) return EXL3_OK;
-    decode_states_kernel<<<(unsigned) ((n2 + 255) / 256), 256, 0, as_stream(stream)>>>(
+    decode_states_kernel<<<(unsigned) ((n2 + 511) / 512), 256, 0, as_stream(stream)>>>(
         reinterpret_cast<const uint32_t*>(states), reinterpret_cast<uint32_t*>(out), n2);
     return hip_status("decode_states");
 }
