@@ -40,6 +40,8 @@ def parse():
     ap.add_argument("--cpu-sample-seconds", type=float, default=20.0)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--stages", action="store_true", help="print per-stage ms to stderr")
+    ap.add_argument("--scatter", choices=["atomic", "combine"], default=None,
+                    help="down-projection output method (default: the runtime's, EXL3_GROUPED_SCATTER or atomic)")
     return ap.parse_args()
 
 
@@ -73,8 +75,9 @@ def run(args, T=None, emit=True):
     R = T_ * k
     limit = 10.0
 
+    scatter = args.scatter or rt.scatter_mode()
     for _ in range(args.warmup):
-        rt.grouped_prefill(xt, it, wt, TL, limit)
+        rt.grouped_prefill(xt, it, wt, TL, limit, scatter=scatter)
     torch.cuda.synchronize()
 
     # timed region: exactly `steps` full steps, bracketed by device synchronisation
@@ -83,7 +86,7 @@ def run(args, T=None, emit=True):
     t0 = time.perf_counter()
     for _ in range(args.steps):
         ev = []
-        rt.grouped_prefill(xt, it, wt, TL, limit, stage_events=ev)
+        rt.grouped_prefill(xt, it, wt, TL, limit, stage_events=ev, scatter=scatter)
         events.append(ev)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -98,10 +101,11 @@ def run(args, T=None, emit=True):
     gate_up_flop = 4.0 * R * H * I
     down_flop = 2.0 * R * H * I
     achieved = gate_up_flop / (gemm_ms * 1e-3) / 1e12
-    both_gemm_tflops = (gate_up_flop + down_flop) / ((gemm_ms + stage_avg["gemm_down_scatter"]) * 1e-3) / 1e12
+    down_ms = stage_avg.get("gemm_down_scatter", stage_avg.get("gemm_down_routes", float("nan")))
+    both_gemm_tflops = (gate_up_flop + down_flop) / ((gemm_ms + down_ms) * 1e-3) / 1e12
     layer_tflops = (gate_up_flop + down_flop) / (ms_per_step * 1e-3) / 1e12
     if args.stages or not emit:
-        print(json.dumps({"T": T_, "bits": bits, "ms_per_step": round(ms_per_step, 4),
+        print(json.dumps({"T": T_, "bits": bits, "scatter": scatter, "ms_per_step": round(ms_per_step, 4),
                           "stage_ms": {n: round(v, 4) for n, v in stage_avg.items()},
                           "gemm_tflops_both": round(both_gemm_tflops, 1),
                           "layer_tflops": round(layer_tflops, 1)}), file=sys.stderr, flush=True)
@@ -120,7 +124,7 @@ def run(args, T=None, emit=True):
         "dtype": "f16",
         "data": "synthetic (seeded random trellis codes, signs, scales, N(0,1) activations, Zipf-skewed router)",
         "config": {"workload": workload, "experts": E, "hidden": H, "intermediate": I, "bits": bits,
-                   "tokens": T_, "topk": k, "routing": cfg["routing"], "routed_rows": R},
+                   "tokens": T_, "topk": k, "routing": cfg["routing"], "routed_rows": R, "scatter": scatter},
         "tokens_per_s": round(T_ / (ms_per_step * 1e-3), 1),
         "stage_ms": {n: round(v, 4) for n, v in stage_avg.items()},
         "gemm_tflops_gate_up_and_down": round(both_gemm_tflops, 1),

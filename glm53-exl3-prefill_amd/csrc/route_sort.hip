@@ -130,7 +130,7 @@ __global__ __launch_bounds__(SORT_THREADS)
 void sort_scatter_kernel(const void* __restrict__ ids, int ids_dtype, const void* __restrict__ weights, int w_dtype,
                          int64_t R, int topk, int n_experts, const int32_t* __restrict__ cursor0,
                          int64_t* __restrict__ token_sorted, uint16_t* __restrict__ weight_sorted,
-                         int32_t* __restrict__ expert_of_row)
+                         int32_t* __restrict__ expert_of_row, int32_t* __restrict__ route_index)
 {
     __shared__ int32_t s_cursor[MAX_EXPERTS];
     __shared__ int32_t s_wave_cnt[SORT_WAVES][MAX_EXPERTS];
@@ -160,6 +160,7 @@ void sort_scatter_kernel(const void* __restrict__ ids, int ids_dtype, const void
             token_sorted[row] = i / topk;
             weight_sorted[row] = route_weight_f16(weights, w_dtype, i);
             expert_of_row[row] = e;
+            if (route_index) route_index[row] = (int32_t) i;
         }
         __syncthreads();
         if (leader)
@@ -171,10 +172,11 @@ void sort_scatter_kernel(const void* __restrict__ ids, int ids_dtype, const void
     }
 }
 
-// Rows past sum(counts) (only present when routes were dropped): token 0, weight 0, expert 0.
+// Rows past sum(counts) (only present when routes were dropped): token 0, weight 0, expert 0, route 0.
 __global__ void sort_fill_tail_kernel(const int32_t* __restrict__ counts, const int32_t* __restrict__ expert_row0,
                                       int n_experts, int64_t R, int64_t* __restrict__ token_sorted,
-                                      uint16_t* __restrict__ weight_sorted, int32_t* __restrict__ expert_of_row)
+                                      uint16_t* __restrict__ weight_sorted, int32_t* __restrict__ expert_of_row,
+                                      int32_t* __restrict__ route_index)
 {
     const int64_t n_rows = (int64_t) expert_row0[n_experts - 1] + counts[n_experts - 1];
     for (int64_t r = n_rows + (int64_t) blockIdx.x * blockDim.x + threadIdx.x; r < R; r += (int64_t) gridDim.x * blockDim.x)
@@ -182,6 +184,7 @@ __global__ void sort_fill_tail_kernel(const int32_t* __restrict__ counts, const 
         token_sorted[r] = 0;
         weight_sorted[r] = 0;
         expert_of_row[r] = 0;
+        if (route_index) route_index[r] = 0;
     }
 }
 
@@ -236,7 +239,7 @@ extern "C" size_t exl3_sort_routes_workspace_bytes(int64_t tokens, int topk, int
 extern "C" int exl3_sort_routes(const void* topk_ids, int ids_dtype, const void* topk_weights, int weights_dtype,
                                 int64_t tokens, int topk, int n_experts,
                                 int64_t* token_sorted, uint16_t* weight_sorted, int32_t* expert_of_row,
-                                int32_t* counts, int32_t* expert_row0,
+                                int32_t* route_index, int32_t* counts, int32_t* expert_row0,
                                 void* workspace, size_t workspace_bytes, void* stream)
 {
     EXL3_CHECK(ids_dtype == EXL3_DTYPE_I64 || ids_dtype == EXL3_DTYPE_I32, "topk_ids must be int64 or int32");
@@ -263,9 +266,10 @@ extern "C" int exl3_sort_routes(const void* topk_ids, int ids_dtype, const void*
     if (n_chunks > 0)
     {
         sort_scatter_kernel<<<n_chunks, SORT_THREADS, 0, s>>>(topk_ids, ids_dtype, topk_weights, weights_dtype, R, topk,
-                                                              n_experts, hist, token_sorted, weight_sorted, expert_of_row);
+                                                              n_experts, hist, token_sorted, weight_sorted, expert_of_row,
+                                                              route_index);
         sort_fill_tail_kernel<<<64, 256, 0, s>>>(counts, expert_row0, n_experts, R, token_sorted, weight_sorted,
-                                                 expert_of_row);
+                                                 expert_of_row, route_index);
     }
     return hip_status("sort_routes");
 }

@@ -28,8 +28,13 @@ constexpr int TILE_N = 128;
 constexpr int TILE_K = 32;
 constexpr int LDS_ROW = TILE_K + 8;                 // halves per n-row of the decoded tile (80 B, conflict-free)
 constexpr int LDS_TILE = TILE_N * LDS_ROW;          // halves per decoded stage
+constexpr int SC_ROW = TILE_N + 4;                  // floats per staged output row of the scatter epilogue
+constexpr int LDS_MAIN_BYTES = 2 * LDS_TILE * 2;
+constexpr int LDS_SCATTER_BYTES = GEMM_WAVES * 32 * SC_ROW * 4;
 
-enum { MODE_STORE_F16 = 0, MODE_SCATTER_F32 = 1, MODE_STORE_F32 = 2 };
+// STORE_F16: fp16 rows (gate|up). SCATTER_F32: fp32 atomic add into out[token[r]]. STORE_F32: fp32 rows (fat GEMM).
+// STORE_ROUTE_F32: fp32 rows at out[route_index[r]] (per-route partials for the deterministic combine).
+enum { MODE_STORE_F16 = 0, MODE_SCATTER_F32 = 1, MODE_STORE_F32 = 2, MODE_STORE_ROUTE_F32 = 3 };
 
 struct GemmParams
 {
@@ -53,6 +58,7 @@ struct GemmParams
     int64_t m;                     // dense rows
     const int64_t* token;          // scatter destination row per sorted row
     const uint16_t* route_weight;  // fp16 per sorted row
+    const int32_t* route_index;    // STORE_ROUTE_F32 destination row per sorted row
     void* out;
     int64_t out_ld;                // elements per output row
 };
@@ -88,7 +94,10 @@ template <int BITS, int MODE, bool DENSE>
 __global__ __launch_bounds__(GEMM_THREADS, 2)
 void trellis_gemm_kernel(const GemmParams p)
 {
-    __shared__ __align__(16) uint16_t lds_b[2][LDS_TILE];
+    constexpr int LDS_BYTES = (MODE == MODE_SCATTER_F32 && LDS_SCATTER_BYTES > LDS_MAIN_BYTES) ? LDS_SCATTER_BYTES
+                                                                                              : LDS_MAIN_BYTES;
+    __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
+    uint16_t (*lds_b)[LDS_TILE] = reinterpret_cast<uint16_t (*)[LDS_TILE]>(lds_raw);
 
     int group, slot;
     xcd_group_slot((int) blockIdx.x, p.n_slots, group, slot);
@@ -228,7 +237,10 @@ void trellis_gemm_kernel(const GemmParams p)
         load_a(min(kb + 3, last), act_b);
     }
 
-    // ---- epilogue: per 32-row block, H128 over the 128 columns of each row, scale by svh, store / scatter
+    // ---- epilogue: per 32-row block, H128 over the 128 columns of each row, scale by svh (and the route weight),
+    // then store / scatter. The scatter stages each block through LDS so that every atomic instruction covers 64
+    // consecutive floats of one output row (two cache lines) instead of 32 rows.
+    if constexpr (MODE == MODE_SCATTER_F32) __syncthreads();     // decoded tiles are dead; LDS becomes staging
     if (!wave_active) return;
     const int out_col0 = which * p.n_tiles_each * TILE_N + nt * TILE_N;
     #pragma unroll
@@ -247,13 +259,15 @@ void trellis_gemm_kernel(const GemmParams p)
         for (int i = 0; i < 64; i += 2) half_wave_butterfly(x[i], x[i + 1]);
 
         const bool row_ok = r_local < rows_valid;
-        const int64_t srow = (int64_t) row0 + r_local;
-        float rw = 0.0f;
+        const int64_t srow = (int64_t) row0 + min(r_local, rows_valid - 1);
+        float rw = 1.0f;
         int64_t orow = srow;
-        if constexpr (MODE == MODE_SCATTER_F32)
+        if constexpr (MODE == MODE_SCATTER_F32 || MODE == MODE_STORE_ROUTE_F32)
         {
-            if (row_ok) { orow = p.token[srow]; rw = h2f(p.route_weight[srow]); }
+            rw = h2f(p.route_weight[srow]);
+            orow = (MODE == MODE_SCATTER_F32) ? p.token[srow] : (int64_t) p.route_index[srow];
         }
+        float* stage = reinterpret_cast<float*>(lds_raw) + wave * (32 * SC_ROW);
         #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
             #pragma unroll
@@ -261,10 +275,17 @@ void trellis_gemm_kernel(const GemmParams p)
             {
                 const int col = 32 * nb + 8 * g + 4 * h;          // first of 4 consecutive columns
                 const uint2 sv = *reinterpret_cast<const uint2*>(svh + col);
-                float s[4] = {h2f(sv.x & 0xFFFF), h2f(sv.x >> 16), h2f(sv.y & 0xFFFF), h2f(sv.y >> 16)};
+                const float sc = HAD_SCALE * rw;
+                const float s[4] = {h2f(sv.x & 0xFFFF) * sc, h2f(sv.x >> 16) * sc, h2f(sv.y & 0xFFFF) * sc,
+                                    h2f(sv.y >> 16) * sc};
                 float v[4];
                 #pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = x[nb * 16 + 4 * g + q] * HAD_SCALE * s[q];
+                for (int q = 0; q < 4; ++q) v[q] = x[nb * 16 + 4 * g + q] * s[q];
+                if constexpr (MODE == MODE_SCATTER_F32)
+                {
+                    *reinterpret_cast<float4*>(stage + l32 * SC_ROW + col) = make_float4(v[0], v[1], v[2], v[3]);
+                    continue;
+                }
                 if (!row_ok) continue;
                 if constexpr (MODE == MODE_STORE_F16)
                 {
@@ -274,18 +295,58 @@ void trellis_gemm_kernel(const GemmParams p)
                     pk.y = (uint32_t) f2h(v[2]) | ((uint32_t) f2h(v[3]) << 16);
                     *reinterpret_cast<uint2*>(o) = pk;
                 }
-                else if constexpr (MODE == MODE_STORE_F32)
+                else
                 {
                     float* o = reinterpret_cast<float*>(p.out) + orow * p.out_ld + out_col0 + col;
                     *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
                 }
-                else
-                {
-                    float* o = reinterpret_cast<float*>(p.out) + orow * p.out_ld + out_col0 + col;
-                    #pragma unroll
-                    for (int q = 0; q < 4; ++q) unsafeAtomicAdd(o + q, v[q] * rw);
-                }
             }
+        if constexpr (MODE == MODE_SCATTER_F32)
+        {
+            // LDS accesses of one wave complete in order: the reads below see the writes above, and the next
+            // block's writes land after these reads.
+            const int nrows = min(32, rows_valid - (wave_row0 + 32 * mb));
+            const uint32_t tok_lo = (uint32_t) orow, tok_hi = (uint32_t) ((uint64_t) orow >> 32);
+            float* outp = reinterpret_cast<float*>(p.out) + out_col0 + lane;
+            for (int t = 0; t < nrows; ++t)
+            {
+                const int64_t trow = (int64_t) (((uint64_t) __builtin_amdgcn_readlane(tok_hi, t) << 32) |
+                                                __builtin_amdgcn_readlane(tok_lo, t));
+                const float v0 = stage[t * SC_ROW + lane];
+                const float v1 = stage[t * SC_ROW + 64 + lane];
+                float* o = outp + trow * p.out_ld;
+                unsafeAtomicAdd(o, v0);
+                unsafeAtomicAdd(o + 64, v1);
+            }
+        }
+    }
+}
+
+// out[t, :] = sum_j partial[t*topk + j, :] in order j = 0 .. topk-1 (deterministic), skipping routes whose id is
+// outside [0, n_experts) (their partial rows were never written).
+__global__ __launch_bounds__(256)
+void combine_routes_kernel(const float4* __restrict__ partial, float4* __restrict__ out, const void* __restrict__ ids,
+                           int ids_dtype, int n_experts, int64_t tokens, int topk, int64_t n4)
+{
+    const int64_t total = tokens * n4;
+    for (int64_t idx = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t) gridDim.x * blockDim.x)
+    {
+        const int64_t t = idx / n4, c = idx - t * n4;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int j = 0; j < topk; ++j)
+        {
+            const int64_t i = t * topk + j;
+            if (ids)
+            {
+                const int64_t e = ids_dtype == EXL3_DTYPE_I64 ? reinterpret_cast<const int64_t*>(ids)[i]
+                                                             : reinterpret_cast<const int32_t*>(ids)[i];
+                if (e < 0 || e >= n_experts) continue;
+            }
+            const float4 v = partial[i * n4 + c];
+            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+        }
+        out[idx] = acc;
     }
 }
 
@@ -374,7 +435,7 @@ extern "C" int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
                                  const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
                                  const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
                                  const int32_t* counts, const int32_t* expert_row0, int n_experts,
-                                 const int64_t* token_sorted, const uint16_t* route_weight,
+                                 const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
                                  void* out, int64_t out_rows, int mode, void* stream)
 {
     EXL3_CHECK(bits >= 2 && bits <= 4, "unsupported bits %d (2, 3 or 4)", bits);
@@ -401,7 +462,7 @@ extern "C" int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
     p.tiles_n = tiles_n; p.svh0 = svh_gate; p.svh1 = svh_up; p.svh_stride = svh_stride;
     p.block_expert = block_expert; p.block_row0 = block_row0; p.counts = counts; p.expert_row0 = expert_row0;
     p.n_groups = max_blocks; p.n_tiles_each = size_n_each / TILE_N; p.n_slots = n_tensors * p.n_tiles_each;
-    p.token = token_sorted; p.route_weight = route_weight; p.out = out;
+    p.token = token_sorted; p.route_weight = route_weight; p.route_index = route_index; p.out = out;
     hipStream_t s = as_stream(stream);
     int rc;
     if (mode == EXL3_GEMM_STORE_F16)
@@ -418,8 +479,16 @@ extern "C" int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
         p.out_ld = size_n_each;
         rc = launch_bits<MODE_SCATTER_F32, false>(bits, p, s);
     }
+    else if (mode == EXL3_GEMM_STORE_ROUTE_F32)
+    {
+        EXL3_CHECK(n_tensors == 1, "mode 2: out fp32 [routes, N], single tensor");
+        EXL3_CHECK(route_index && route_weight, "mode 2 needs route_index and route_weight");
+        EXL3_CHECK(aligned16(out), "out must be 16-byte aligned");
+        p.out_ld = size_n_each;
+        rc = launch_bits<MODE_STORE_ROUTE_F32, false>(bits, p, s);
+    }
     else
-        return fail("mode must be 0 (fp16 store) or 1 (fp32 atomic scatter)");
+        return fail("mode must be 0 (fp16 store), 1 (fp32 atomic scatter) or 2 (fp32 per-route store)");
     if (rc != EXL3_OK) return rc;
     return hip_status("grouped_gemm");
 }
@@ -481,10 +550,26 @@ extern "C" int exl3_fat_gemm_scatter(const uint16_t* a, int64_t m, int size_k, c
     return hip_status("fat_gemm_v2_scatter");
 }
 
+extern "C" int exl3_combine_routes(const float* partial, float* out, const void* topk_ids, int ids_dtype, int n_experts,
+                                   int64_t tokens, int topk, int64_t n, void* stream)
+{
+    EXL3_CHECK(tokens >= 0 && topk > 0 && n > 0 && n % 4 == 0, "combine: bad shape");
+    EXL3_CHECK(!topk_ids || ids_dtype == EXL3_DTYPE_I64 || ids_dtype == EXL3_DTYPE_I32, "topk_ids must be int64 or int32");
+    if (tokens == 0) return EXL3_OK;
+    EXL3_CHECK(partial && out, "null pointer");
+    EXL3_CHECK(aligned16(partial) && aligned16(out), "partial/out must be 16-byte aligned");
+    const int64_t total = tokens * (n / 4);
+    const int64_t blocks = (total + 255) / 256;
+    combine_routes_kernel<<<(unsigned) (blocks < 65536 ? blocks : 65536), 256, 0, as_stream(stream)>>>(
+        reinterpret_cast<const float4*>(partial), reinterpret_cast<float4*>(out), topk_ids, ids_dtype, n_experts,
+        tokens, topk, n / 4);
+    return hip_status("combine_routes");
+}
+
 extern "C" int64_t exl3_smem_bytes(int64_t variant)
 {
     if (variant < 0 || variant > 3) return -1;
-    return (int64_t) sizeof(uint16_t) * 2 * LDS_TILE;
+    return (int64_t) LDS_SCATTER_BYTES > LDS_MAIN_BYTES ? LDS_SCATTER_BYTES : LDS_MAIN_BYTES;
 }
 
 extern "C" int exl3_reconstruct(uint16_t* out, const uint16_t* packed, int tiles_k, int tiles_n, int bits, int mcg,

@@ -68,9 +68,11 @@ def sort_routes_workspace_bytes(tokens: int, topk: int, n_experts: int) -> int:
 
 def sort_routes(topk_ids: torch.Tensor, topk_weights: torch.Tensor, n_experts: int, token_sorted: torch.Tensor,
                 weight_sorted: torch.Tensor, expert_of_row: torch.Tensor, counts: torch.Tensor,
-                expert_row0: torch.Tensor, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                expert_row0: torch.Tensor, workspace: Optional[torch.Tensor] = None,
+                route_index: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Stable sort of routes by expert (replaces kernel/exl3_grouped_runtime.py:59-68). Returns the workspace;
-    its first int32 holds the number of dropped routes (ids outside [0, n_experts))."""
+    its first int32 holds the number of dropped routes (ids outside [0, n_experts)). route_index (int32 [R],
+    optional) receives each sorted row's flat route index t*topk + j."""
     _check(topk_ids.dim() == 2 and topk_weights.shape == topk_ids.shape, "topk_ids / topk_weights must be [T, topk]")
     _check(topk_ids.dtype in (torch.int64, torch.int32), "topk_ids must be int64 or int32")
     _check(topk_weights.dtype in (torch.float32, torch.float16, torch.bfloat16),
@@ -85,6 +87,9 @@ def sort_routes(topk_ids: torch.Tensor, topk_weights: torch.Tensor, n_experts: i
     _check(counts.dtype == torch.int32 and expert_row0.dtype == torch.int32 and counts.numel() == n_experts and
            expert_row0.numel() == n_experts, "counts / expert_row0 must be int32 [E]")
     _check(0 < n_experts <= 1024, "too many experts")
+    if route_index is not None:
+        _check(route_index.dtype == torch.int32 and route_index.numel() == R and route_index.is_contiguous(),
+               "route_index must be contiguous int32 [T*topk]")
     need = sort_routes_workspace_bytes(T, k, n_experts)
     dev = _require_cuda(topk_ids, topk_weights, token_sorted, weight_sorted, expert_of_row, counts, expert_row0)
     if workspace is None:
@@ -92,8 +97,8 @@ def sort_routes(topk_ids: torch.Tensor, topk_weights: torch.Tensor, n_experts: i
     _check(workspace.numel() * workspace.element_size() >= need, "sort workspace too small")
     with _On(dev) as s:
         _lib.call("exl3_sort_routes", _p(topk_ids), _DT[topk_ids.dtype], _p(topk_weights), _DT[topk_weights.dtype],
-                  T, k, n_experts, _p(token_sorted), _p(weight_sorted), _p(expert_of_row), _p(counts),
-                  _p(expert_row0), _p(workspace), workspace.numel() * workspace.element_size(), s)
+                  T, k, n_experts, _p(token_sorted), _p(weight_sorted), _p(expert_of_row), _p(route_index),
+                  _p(counts), _p(expert_row0), _p(workspace), workspace.numel() * workspace.element_size(), s)
     return workspace
 
 
@@ -155,8 +160,10 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
                  svh_gate: torch.Tensor, svh_up: Optional[torch.Tensor], block_expert: torch.Tensor,
                  block_row0: torch.Tensor, counts: torch.Tensor, expert_row0: torch.Tensor,
                  token_sorted: Optional[torch.Tensor], route_weight: Optional[torch.Tensor], out: torch.Tensor,
-                 mode: int) -> None:
-    """kernel/exl3_grouped_prefill.cu:326-378. mode 0: fp16 store; mode 1: fp32 atomic scatter."""
+                 mode: int, route_index: Optional[torch.Tensor] = None) -> None:
+    """kernel/exl3_grouped_prefill.cu:326-378. mode 0: fp16 store; mode 1: fp32 atomic scatter into
+    out[token_sorted[r]]; mode 2 (new): fp32 store of the weighted row into out[route_index[r]] (out [T*topk, N]),
+    summed per token by combine_routes in a fixed order."""
     _check(a.dtype == torch.float16 and a.is_contiguous(), "a fp16 contiguous")
     _check(packed_gate.dim() == 4 and packed_gate.dtype in (torch.int16, torch.uint16) and
            packed_gate.stride(3) == 1 and packed_gate.stride(2) == packed_gate.size(3) and
@@ -191,15 +198,40 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
                out.is_contiguous(), "mode 1: out fp32 [T, N], single tensor")
         _check(token_sorted is not None and route_weight is not None and token_sorted.dtype == torch.int64 and
                route_weight.dtype == torch.float16, "routing dtypes")
+    elif mode == 2:
+        _check(out.dtype == torch.float32 and out.dim() == 2 and out.size(1) == size_n_each and n_tensors == 1 and
+               out.is_contiguous(), "mode 2: out fp32 [routes, N], single tensor")
+        _check(route_index is not None and route_weight is not None and route_index.dtype == torch.int32 and
+               route_weight.dtype == torch.float16, "mode 2 needs route_index (int32) and route_weight (fp16)")
     else:
-        raise RuntimeError("mode must be 0 or 1")
+        raise RuntimeError("mode must be 0, 1 or 2")
     dev = _require_cuda(a, packed_gate, packed_up, svh_gate, svh_up, block_expert, block_row0, counts,
-                        expert_row0, out, token_sorted if mode == 1 else None, route_weight if mode == 1 else None)
+                        expert_row0, out, token_sorted if mode == 1 else None, route_weight if mode else None,
+                        route_index if mode == 2 else None)
     with _On(dev) as s:
         _lib.call("exl3_grouped_gemm", _p(a), a.size(0), size_k, _p(packed_gate), _p(packed_up), expert_stride,
                   tiles_k, tiles_n, bits, _p(svh_gate), _p(svh_up), svh_stride, _p(block_expert), _p(block_row0),
                   max_blocks, _p(counts), _p(expert_row0), E, _p(token_sorted) if mode == 1 else None,
-                  _p(route_weight) if mode == 1 else None, _p(out), out.size(0), mode, s)
+                  _p(route_weight) if mode else None, _p(route_index) if mode == 2 else None, _p(out), out.size(0),
+                  mode, s)
+
+
+def combine_routes(partial: torch.Tensor, out: torch.Tensor, topk: int, topk_ids: Optional[torch.Tensor] = None,
+                   n_experts: int = 0) -> None:
+    """out[t] = sum_j partial[t*topk + j] in order j = 0..topk-1 (new; pairs with grouped_gemm mode 2). Routes whose id
+    in topk_ids lies outside [0, n_experts) are skipped."""
+    T, n = out.shape
+    _check(partial.dtype == torch.float32 and out.dtype == torch.float32 and partial.is_contiguous() and
+           out.is_contiguous(), "combine: fp32 contiguous tensors")
+    _check(partial.dim() == 2 and partial.size(0) == T * topk and partial.size(1) == n and n % 4 == 0,
+           "combine: partial must be [T*topk, N], N % 4 == 0")
+    if topk_ids is not None:
+        _check(topk_ids.dtype in (torch.int64, torch.int32) and topk_ids.is_contiguous() and
+               topk_ids.numel() == T * topk and 0 < n_experts <= 1024, "combine: topk_ids [T, topk] int64/int32")
+    dev = _require_cuda(partial, out, topk_ids)
+    with _On(dev) as s:
+        _lib.call("exl3_combine_routes", _p(partial), _p(out), _p(topk_ids),
+                  _DT[topk_ids.dtype] if topk_ids is not None else 0, int(n_experts), T, int(topk), n, s)
 
 
 # ------------------------------------------------------------------------------------------- per-expert entry

@@ -8,6 +8,8 @@ the original path untouched (kernel/exl3_grouped_runtime.py:93-98).
 
 Env:
   EXL3_GROUPED_PREFILL=1     enable (read by the hook)
+  EXL3_GROUPED_SCATTER=...   down-projection output: "atomic" (fp32 atomic scatter by token, the reference's
+                             method) or "combine" (per-route fp32 rows + a fixed-order sum per token: deterministic)
   EXL3_GROUPED_LIB=<path>    prebuilt libexl3_grouped.so (default: exl3_grouped/libexl3_grouped.so beside this file)
 """
 import logging
@@ -40,13 +42,25 @@ def _load_ext():
     return _ext
 
 
+SCATTER_MODES = ("atomic", "combine")
+
+
+def scatter_mode() -> str:
+    m = os.environ.get("EXL3_GROUPED_SCATTER", "atomic")
+    if m not in SCATTER_MODES:
+        raise RuntimeError(f"EXL3_GROUPED_SCATTER must be one of {SCATTER_MODES}, got {m!r}")
+    return m
+
+
 def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, layer, limit: float,
-                    stage_events: list | None = None) -> torch.Tensor:
+                    stage_events: list | None = None, scatter: str | None = None) -> torch.Tensor:
     """x2d [T, K] (any float dtype), ids [T, topk] (int64 or int32), weights [T, topk] -> out [T, K] fp32.
     Restates kernel/exl3_grouped_runtime.py:50-83 with the route sort on the GPU (sort_routes).
     stage_events: if a list is given, a timing event recorded on the current stream after each stage is appended
-    as (stage name, event), after a leading ("start", event)."""
+    as (stage name, event), after a leading ("start", event).
+    scatter: "atomic" or "combine" (default: EXL3_GROUPED_SCATTER, else "atomic")."""
     gp = _load_ext()
+    scatter = scatter or scatter_mode()
 
     def mark(name):
         if stage_events is not None:
@@ -69,7 +83,9 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     expert_of_row = torch.empty(R, dtype=torch.int32, device=dev)
     counts = torch.empty(E, dtype=torch.int32, device=dev)
     expert_row0 = torch.empty(E, dtype=torch.int32, device=dev)
-    gp.sort_routes(ids, weights, E, token_sorted, weight_sorted, expert_of_row, counts, expert_row0)
+    route_index = torch.empty(R, dtype=torch.int32, device=dev) if scatter == "combine" else None
+    gp.sort_routes(ids, weights, E, token_sorted, weight_sorted, expert_of_row, counts, expert_row0,
+                   route_index=route_index)
     mark("sort_routes")
     max_blocks = R // 128 + E
     block_expert = torch.empty(max_blocks, dtype=torch.int32, device=dev)
@@ -87,11 +103,21 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     act = torch.empty(R, I, dtype=torch.float16, device=dev)
     gp.act_had(gu, act, expert_of_row, layer.w2_suh, float(limit))
     mark("act_had")
-    out = torch.zeros(T, K, dtype=torch.float32, device=dev)
-    mark("zero_out")
+    if scatter == "atomic":
+        out = torch.zeros(T, K, dtype=torch.float32, device=dev)
+        mark("zero_out")
+        gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
+                        block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, out, 1)
+        mark("gemm_down_scatter")
+        return out
+    partial = torch.empty(R, K, dtype=torch.float32, device=dev)
     gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
-                    block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, out, 1)
-    mark("gemm_down_scatter")
+                    block_expert, block_row0, counts, expert_row0, None, weight_sorted, partial, 2,
+                    route_index=route_index)
+    mark("gemm_down_routes")
+    out = torch.empty(T, K, dtype=torch.float32, device=dev)
+    gp.combine_routes(partial, out, topk, ids, E)
+    mark("combine")
     return out
 
 

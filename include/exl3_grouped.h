@@ -39,6 +39,7 @@ extern "C" {
 
 #define EXL3_GEMM_STORE_F16 0      /* grouped_gemm mode 0: fp16 store into [rows, n_tensors*N] */
 #define EXL3_GEMM_SCATTER_F32 1    /* grouped_gemm mode 1: fp32 atomic add into out[token_sorted[r]] * w[r] */
+#define EXL3_GEMM_STORE_ROUTE_F32 2 /* grouped_gemm mode 2: fp32 store of w[r] * y[r] into out[route_index[r]] */
 
 /* Message for the calling thread's last failing call ("" if none). */
 const char* exl3_last_error(void);
@@ -50,6 +51,7 @@ int exl3_abi_version(void);
  * Route sort: the torch glue of grouped_prefill (kernel/exl3_grouped_runtime.py:59-68) as GPU kernels.
  * Stable sort of the flat route list i = t*topk + j by expert id:
  *   token_sorted[r] = i/topk, weight_sorted[r] = fp16(topk_weights[i]), expert_of_row[r] = topk_ids[i],
+ *   route_index[r] = i (optional output, NULL to skip; new, used by the deterministic combine),
  *   counts[e] = #routes of e, expert_row0[e] = exclusive prefix sum of counts.
  * ids_dtype: EXL3_DTYPE_I64 or EXL3_DTYPE_I32; weights_dtype: EXL3_DTYPE_F32, _F16 or _BF16.
  * Routes whose id is outside [0, n_experts) are dropped; the rows they would have filled (the tail past
@@ -61,7 +63,7 @@ size_t exl3_sort_routes_workspace_bytes(int64_t tokens, int topk, int n_experts)
 int exl3_sort_routes(const void* topk_ids, int ids_dtype, const void* topk_weights, int weights_dtype,
                      int64_t tokens, int topk, int n_experts,
                      int64_t* token_sorted, uint16_t* weight_sorted, int32_t* expert_of_row,
-                     int32_t* counts, int32_t* expert_row0,
+                     int32_t* route_index, int32_t* counts, int32_t* expert_row0,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -107,6 +109,9 @@ int exl3_act_had(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int3
  *   mode EXL3_GEMM_SCATTER_F32 (single tensor only): out fp32 [out_rows, N_each], caller-zeroed,
  *        out[token_sorted[r], n] += fp32(route_weight[r]) * ( H128_n(a[r] @ W'_e) / sqrt(128) * svh_e[n] )
  *        with device-scope fp32 atomics (order of additions is not deterministic).
+ *   mode EXL3_GEMM_STORE_ROUTE_F32 (single tensor, new): out fp32 [T*topk, N_each],
+ *        out[route_index[r], n] = fp32(route_weight[r]) * ( same ): one row per route, plain stores; with
+ *        exl3_combine_routes it gives mode 1's result in a fixed summation order.
  * gate/up tensors must share expert strides (as [E, 2, ...] views do).
  */
 int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
@@ -115,8 +120,16 @@ int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
                       const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
                       const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
                       const int32_t* counts, const int32_t* expert_row0, int n_experts,
-                      const int64_t* token_sorted, const uint16_t* route_weight,
+                      const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
                       void* out, int64_t out_rows, int mode, void* stream);
+
+/*
+ * Deterministic route combine (new; pairs with grouped_gemm mode 2): out[t, :] = sum_{j < topk} partial[t*topk + j, :]
+ * in order j = 0, 1, ..., skipping routes whose id in topk_ids (optional, int64 or int32 [tokens, topk]) lies outside
+ * [0, n_experts). partial fp32 [tokens*topk, n], out fp32 [tokens, n] (overwritten), n % 4 == 0.
+ */
+int exl3_combine_routes(const float* partial, float* out, const void* topk_ids, int ids_dtype, int n_experts,
+                        int64_t tokens, int topk, int64_t n, void* stream);
 
 /*
  * Per-expert weight-stationary trellis GEMM, the exl3_fat_gemm drop-in (pybind ops fat_gemm_v2 /

@@ -57,8 +57,8 @@ def test_act_had_rejects_bad_width():
 
 def _gemm(**kw):
     a = dict(a=FAKE, a_rows=256, size_k=512, pg=FAKE, pu=None, es=32 * 16 * 64, tk=32, tn=16, bits=4, sg=FAKE,
-             su=None, ss=256, be=FAKE, br=FAKE, mb=10, counts=FAKE, row0=FAKE, E=8, tok=FAKE, rw=FAKE, out=FAKE,
-             out_rows=64, mode=1)
+             su=None, ss=256, be=FAKE, br=FAKE, mb=10, counts=FAKE, row0=FAKE, E=8, tok=FAKE, rw=FAKE, ri=None,
+             out=FAKE, out_rows=64, mode=1)
     a.update(kw)
     return rc_and_msg("exl3_grouped_gemm", *a.values(), None)
 
@@ -72,6 +72,8 @@ def test_grouped_gemm_contract():
     assert "single tensor" in _gemm(pu=FAKE, su=FAKE)[1]
     assert "gate/up strides must match" in _gemm(pu=FAKE, su=None)[1]
     assert "mode" in _gemm(mode=3)[1]
+    assert "route_index" in _gemm(mode=2)[1]
+    assert "combine" in rc_and_msg("exl3_combine_routes", FAKE, FAKE, None, 4, 8, 10, 8, 6, None)[1]
 
 
 def test_fat_gemm_contract():
@@ -97,10 +99,10 @@ def test_sort_routes_contract():
     need = lib.exl3_sort_routes_workspace_bytes(100, 8, 288)
     assert need > 0
     rc, msg = rc_and_msg("exl3_sort_routes", FAKE, _lib.DTYPE_I64, FAKE, _lib.DTYPE_F32, 100, 8, 288, FAKE, FAKE, FAKE,
-                         FAKE, FAKE, FAKE, need - 1, None)
+                         None, FAKE, FAKE, FAKE, need - 1, None)
     assert rc == _lib.EXL3_ERR_ARG and "workspace" in msg
     rc, msg = rc_and_msg("exl3_sort_routes", FAKE, _lib.DTYPE_F32, FAKE, _lib.DTYPE_F32, 100, 8, 288, FAKE, FAKE,
-                         FAKE, FAKE, FAKE, FAKE, need, None)
+                         FAKE, None, FAKE, FAKE, FAKE, need, None)
     assert rc == _lib.EXL3_ERR_ARG and "int64 or int32" in msg
 
 

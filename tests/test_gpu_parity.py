@@ -61,7 +61,7 @@ ROUTINGS = [("softmax", 128, 8, 2), ("softmax", 1024, 288, 8), ("zipf", 8192, 28
             ("skewed", 2048, 288, 8), ("softmax", 1, 288, 8), ("softmax", 3000, 1024, 6)]
 
 
-def gpu_sort(ids_t, w_t, E):
+def gpu_sort(ids_t, w_t, E, with_route_index=False):
     dev = ids_t.device
     R = ids_t.numel()
     ts = torch.empty(R, dtype=torch.int64, device=dev)
@@ -69,9 +69,11 @@ def gpu_sort(ids_t, w_t, E):
     eor = torch.empty(R, dtype=torch.int32, device=dev)
     counts = torch.empty(E, dtype=torch.int32, device=dev)
     row0 = torch.empty(E, dtype=torch.int32, device=dev)
-    work = gp.sort_routes(ids_t, w_t, E, ts, ws, eor, counts, row0)
+    ri = torch.empty(R, dtype=torch.int32, device=dev) if with_route_index else None
+    work = gp.sort_routes(ids_t, w_t, E, ts, ws, eor, counts, row0, route_index=ri)
     dropped = int(work[:4].view(torch.int32).item())
-    return ts.cpu().numpy(), ws.cpu().numpy(), eor.cpu().numpy(), counts.cpu().numpy(), row0.cpu().numpy(), dropped
+    res = (ts.cpu().numpy(), ws.cpu().numpy(), eor.cpu().numpy(), counts.cpu().numpy(), row0.cpu().numpy(), dropped)
+    return res + (ri.cpu().numpy(),) if with_route_index else res
 
 
 @pytest.mark.parametrize("kind,T,E,k", ROUTINGS)
@@ -79,10 +81,11 @@ def test_sort_routes_bit_exact(dev, kind, T, E, k):
     ids, w = synth.make_routing(kind, T, E, k, seed=T)
     ref = O.sort_routes(ids, w, E)
     for ids_dt in (torch.int64, torch.int32):
-        got = gpu_sort(torch.from_numpy(ids).to(ids_dt).to(dev), torch.from_numpy(w).to(dev), E)
+        got = gpu_sort(torch.from_numpy(ids).to(ids_dt).to(dev), torch.from_numpy(w).to(dev), E, True)
         assert got[5] == 0
         for g, r in zip(got[:5], ref):
             assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(r).view(np.uint8))
+        assert np.array_equal(got[6], np.argsort(ids.reshape(-1), kind="stable"))       # route_index
 
 
 @pytest.mark.parametrize("wdt", [torch.float16, torch.bfloat16])
@@ -201,6 +204,40 @@ def test_grouped_gemm_down_scatter(dev, name, T):
     assert O.rel_l2(out.cpu().numpy(), ref) < 1e-5
 
 
+@pytest.mark.parametrize("name,T", [("tiny", None), ("layer1k", None)])
+def test_grouped_gemm_down_routes_and_combine(dev, name, T):
+    L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, 3, T=T)
+    R = ids.size
+    rng = np.random.default_rng(10)
+    act = (rng.standard_normal((R, cfg["I"])) * 3).astype(np.float16)
+    ref = O.grouped_gemm_mode1(act, O.WeightCache(layer), counts, row0, ts, ws, cfg["T"])
+    TL = synth.to_device(L, dev)
+    be, br = gpu_blocks(counts, R, cfg["E"], dev)
+    ri = torch.from_numpy(np.argsort(ids.reshape(-1), kind="stable").astype(np.int32)).to(dev)
+    outs = []
+    for _ in range(2):
+        partial = torch.full((R, cfg["H"]), float("nan"), dtype=torch.float32, device=dev)
+        gp.grouped_gemm(t16(act, dev), TL.w2_trellis, None, TL.w2_svh, None, be, br, t16(counts, dev),
+                        t16(row0, dev), None, t16(ws, dev), partial, 2, route_index=ri)
+        assert not torch.isnan(partial).any()                      # every route row written exactly
+        out = torch.full((cfg["T"], cfg["H"]), float("nan"), dtype=torch.float32, device=dev)
+        gp.combine_routes(partial, out, cfg["topk"], t16(ids, dev), cfg["E"])
+        outs.append(out.cpu().numpy())
+    assert O.rel_l2(outs[0], ref) < 1e-5
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))      # deterministic
+
+
+def test_combine_skips_invalid_routes(dev):
+    T, k, N = 5, 3, 16
+    partial = torch.arange(T * k * N, dtype=torch.float32, device=dev).reshape(T * k, N)
+    ids = torch.tensor([[0, 1, 2], [9, 1, 0], [0, -1, 3], [1, 1, 1], [4, 4, 4]], dtype=torch.int64, device=dev)
+    out = torch.empty(T, N, device=dev)
+    gp.combine_routes(partial, out, k, ids, 4)
+    p = partial.cpu().reshape(T, k, N)
+    keep = ((ids >= 0) & (ids < 4)).cpu().float()
+    assert torch.equal(out.cpu(), (p * keep[:, :, None]).sum(1))
+
+
 # ------------------------------------------------------------------------------------------- fat GEMM (config 2)
 @pytest.mark.parametrize("M", [300, 4096])
 def test_fat_gemm_config2(dev, M):
@@ -244,17 +281,18 @@ class Fake:
     pass
 
 
-def run_layer(L, x, ids, w, dev):
+def run_layer(L, x, ids, w, dev, scatter="atomic"):
     TL = synth.to_device(L, dev)
-    out = rt.grouped_prefill(t16(x, dev), t16(ids, dev), t16(w, dev), TL, LIMIT)
+    out = rt.grouped_prefill(t16(x, dev), t16(ids, dev), t16(w, dev), TL, LIMIT, scatter=scatter)
     torch.cuda.synchronize()
     return out
 
 
+@pytest.mark.parametrize("scatter", ["atomic", "combine"])
 @pytest.mark.parametrize("name,svh_scale", [("tiny", 1.0), ("tiny", 1 / 64), ("layer1k", 1.0), ("layer1k", 1 / 64)])
-def test_layer_vs_expert_loop(dev, name, svh_scale):
+def test_layer_vs_expert_loop(dev, name, svh_scale, scatter):
     L, x, ids, w, cfg = synth.make_config(name, seed=4, svh_scale=svh_scale)
-    got = run_layer(L, x, ids, w, dev).cpu().numpy()
+    got = run_layer(L, x, ids, w, dev, scatter).cpu().numpy()
     layer = to_np_layer(L)
     ref = O.expert_loop(x, ids, w, layer, LIMIT)
     assert O.rel_l2(got, ref) < 1e-3
@@ -267,18 +305,19 @@ def sampled_loop(L, x, ids, w, tokens):
     return O.expert_loop(x[tokens], ids[tokens], w[tokens], layer, LIMIT)
 
 
-def test_headline_sampled_tokens_and_properties(dev):
+@pytest.mark.parametrize("scatter", ["atomic", "combine"])
+def test_headline_sampled_tokens_and_properties(dev, scatter):
     L, x, ids, w, cfg = synth.make_config("headline", seed=0)
-    out = run_layer(L, x, ids, w, dev)
+    out = run_layer(L, x, ids, w, dev, scatter)
     tokens = np.random.default_rng(0).choice(cfg["T"], 24, replace=False)
     ref = sampled_loop(L, x, ids, w, tokens)
     assert O.rel_l2(out.cpu().numpy()[tokens], ref) < 1e-3
     # linearity in the route weights (x2 is exact in fp16)
-    out2 = run_layer(L, x, ids, 2 * w, dev)
+    out2 = run_layer(L, x, ids, 2 * w, dev, scatter)
     assert (out2 - 2 * out).norm().item() <= 1e-6 * out.norm().item()
     # token permutation equivariance
     perm = np.random.default_rng(1).permutation(cfg["T"])
-    outp = run_layer(L, x[perm], ids[perm], w[perm], dev)
+    outp = run_layer(L, x[perm], ids[perm], w[perm], dev, scatter)
     assert (outp - out[torch.from_numpy(perm).to(dev)]).norm().item() <= 1e-6 * out.norm().item()
 
 
