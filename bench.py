@@ -25,6 +25,8 @@ sys.path[:0] = [os.path.join(ROOT, "glm53-exl3-prefill_amd")]
 
 MFMA_F16_PEAK_TFLOPS = 2500.0      # MI355X dense fp16 (no sparsity)
 HBM_PEAK_GBS = 8000.0
+# the dominant kernel's name as rocprofv3 reports it (key of the committed traffic summary)
+GATE_UP_KERNEL = "trellis_gemm_kernel<{bits}, 0, false>(GemmParams)"
 
 
 def parse():
@@ -42,18 +44,34 @@ def parse():
     ap.add_argument("--stages", action="store_true", help="print per-stage ms to stderr")
     ap.add_argument("--scatter", choices=["atomic", "combine"], default=None,
                     help="down-projection output method (default: the runtime's, EXL3_GROUPED_SCATTER or atomic)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB a few times (calibrates rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE against known bytes) and exit")
     return ap.parse_args()
 
 
-def traffic_from_profiles(workload: str):
-    """HBM bytes per launch of the gate|up GEMM from the committed rocprofv3 --pmc summary, if there is one."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
-    if not os.path.exists(path):
-        return None
+def copy_probe(mib: int):
+    """A plain copy kernel of known size: reads and writes exactly mib MiB per launch."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.randn(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_per_launch": n * 4, "launches": 5}), flush=True)
+
+
+def traffic_from_profiles(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary of `workload`
+    (profiles/grouped_prefill_<workload>_traffic.md: FETCH_SIZE and WRITE_SIZE passes scaled by a copy-kernel
+    calibration, in its fenced JSON block), or None if there is no such summary."""
+    path = os.path.join(ROOT, "profiles", f"grouped_prefill_{workload}_traffic.md")
     try:
-        data = json.load(open(path))
-        return data.get(workload, {}).get("gemm_gate_up_bytes")
-    except (OSError, ValueError):
+        text = open(path).read()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        return json.loads(block)["bytes_per_launch"].get(kernel)
+    except (OSError, IndexError, ValueError, KeyError):
         return None
 
 
@@ -129,10 +147,10 @@ def run(args, T=None, emit=True):
         "stage_ms": {n: round(v, 4) for n, v in stage_avg.items()},
         "gemm_tflops_gate_up_and_down": round(both_gemm_tflops, 1),
         "mfma_frac_layer": round(layer_tflops / MFMA_F16_PEAK_TFLOPS, 4),
-        "roofline": {"kernel": "grouped_gemm gate|up (trellis_gemm_kernel<4,0,false>)", "bound": "mfma",
+        "roofline": {"kernel": f"grouped_gemm gate|up ({GATE_UP_KERNEL.format(bits=bits)})", "bound": "mfma",
                      "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
-                     "traffic": traffic_from_profiles(cfg_name),
+                     "traffic": traffic_from_profiles(cfg_name, GATE_UP_KERNEL.format(bits=bits)),
                      "work_per_launch": f"4*R*H*I = {gate_up_flop:.4g} flop (R={R} routed rows)"},
     }
     return result, (L, x, ids, w, cfg)
@@ -186,6 +204,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     if args.sweep:
         for T in (1024, 2048, 4096, 8192):
             r, _ = run(args, T=T, emit=False)
