@@ -188,8 +188,9 @@ __global__ void sort_fill_tail_kernel(const int32_t* __restrict__ counts, const 
     }
 }
 
+// Per-expert row tiles of `tile_rows` rows (128 for the reference's block table).
 __global__ __launch_bounds__(1024)
-void build_blocks_kernel(const int32_t* __restrict__ counts, int n_experts, int max_blocks,
+void build_blocks_kernel(const int32_t* __restrict__ counts, int n_experts, int tile_rows, int max_blocks,
                          int32_t* __restrict__ block_expert, int32_t* __restrict__ block_row0,
                          int32_t* __restrict__ meta)
 {
@@ -197,7 +198,7 @@ void build_blocks_kernel(const int32_t* __restrict__ counts, int n_experts, int 
     __shared__ int32_t s_blks[1024];
     const int e = threadIdx.x;
     const int c = (e < n_experts) ? counts[e] : 0;
-    const int nb = (c + 127) / 128;
+    const int nb = (c + tile_rows - 1) / tile_rows;
     s_rows[e] = c;
     s_blks[e] = nb;
     __syncthreads();
@@ -216,7 +217,7 @@ void build_blocks_kernel(const int32_t* __restrict__ counts, int n_experts, int 
         for (int i = 0; i < nb; ++i)
         {
             const int b = blk0 + i;
-            if (b < max_blocks) { block_expert[b] = e; block_row0[b] = row0 + i * 128; }
+            if (b < max_blocks) { block_expert[b] = e; block_row0[b] = row0 + i * tile_rows; }
         }
     const int n_blocks = s_blks[1023];
     if (e == 0) { meta[0] = n_blocks; meta[1] = s_rows[1023]; }
@@ -274,13 +275,20 @@ extern "C" int exl3_sort_routes(const void* topk_ids, int ids_dtype, const void*
     return hip_status("sort_routes");
 }
 
+extern "C" int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_rows, int max_tiles,
+                                int32_t* tile_expert, int32_t* tile_row0, int32_t* meta, void* stream)
+{
+    EXL3_CHECK(n_experts >= 0 && n_experts <= MAX_EXPERTS, "too many experts");
+    EXL3_CHECK(tile_rows == 64 || tile_rows == 128 || tile_rows == 256, "tile_rows must be 64, 128 or 256");
+    EXL3_CHECK(max_tiles >= 0, "bad max_blocks");
+    EXL3_CHECK(counts && meta && (max_tiles == 0 || (tile_expert && tile_row0)), "null pointer");
+    build_blocks_kernel<<<1, 1024, 0, as_stream(stream)>>>(counts, n_experts, tile_rows, max_tiles, tile_expert,
+                                                           tile_row0, meta);
+    return hip_status("build_blocks");
+}
+
 extern "C" int exl3_build_blocks(const int32_t* counts, int n_experts, int max_blocks,
                                  int32_t* block_expert, int32_t* block_row0, int32_t* meta, void* stream)
 {
-    EXL3_CHECK(n_experts >= 0 && n_experts <= MAX_EXPERTS, "too many experts");
-    EXL3_CHECK(max_blocks >= 0, "bad max_blocks");
-    EXL3_CHECK(counts && meta && (max_blocks == 0 || (block_expert && block_row0)), "null pointer");
-    build_blocks_kernel<<<1, 1024, 0, as_stream(stream)>>>(counts, n_experts, max_blocks, block_expert, block_row0,
-                                                           meta);
-    return hip_status("build_blocks");
+    return exl3_build_tiles(counts, n_experts, 128, max_blocks, block_expert, block_row0, meta, stream);
 }

@@ -9,8 +9,8 @@
 //
 // gfx950 cost per weight: the 32-bit multiply by a 16-bit state is split into a 16x16 low-half multiply whose
 // result lands in the upper word (SDWA) plus a 16x16+32 multiply-add that picks the state's half by op_sel,
-// so no state ever needs shifting out of its dword; v_bitop3 does mask-and-xor in one op, and two SDWA fp16
-// adds write the packed result pair. About 4.4 VALU ops per weight at 4 bits.
+// so no state ever needs shifting out of its dword; v_bitop3 does mask-and-xor in one op, SDWA fp16 adds put each
+// sum in its half of a temporary and an OR joins a pair. About 4.9 VALU ops per weight at 4 bits.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -23,9 +23,12 @@ constexpr uint32_t MCG_XOR = 0x3B603B60u;
 constexpr uint32_t MCG_MASK = 0x8FFF8FFFu;
 
 // gfx950 forwards a VALU result written through an SDWA destination select (a partial-register write) to the
-// next instruction stale: the consumer must be at least one instruction later. The compiler cannot place that
-// wait inside an asm statement, so every asm block below orders its instructions so that each partial write is
-// followed by an independent instruction before its first reader.
+// next instruction stale: the consumer must be at least one instruction later. The compiler's hazard recognizer
+// cannot see inside an asm statement, so every SDWA result below is consumed only by a VALU instruction of the same
+// asm block at least one instruction later, and every register an asm block hands back is written by a plain
+// (non-SDWA) instruction, whatever the compiler places after the block. Inputs of these blocks must likewise not come
+// from instructions with wait-state rules of their own (per-lane 64-bit shifts fed into them gave wrong results at
+// random): callers hand them 32-bit funnel shifts, loads and DPP moves.
 
 // x0 = lo(ra) * 0xCBAC1FED, x1 = (HI1 ? hi : lo)(rb) * 0xCBAC1FED  (mod 2^32), both as full 32-bit products.
 template <int HI1>
@@ -49,15 +52,20 @@ __device__ __forceinline__ void mcg_mul2(uint32_t ra, uint32_t rb, uint32_t& x0,
 
 __device__ __forceinline__ uint32_t mcg_mask(uint32_t x) { return (x & MCG_MASK) ^ MCG_XOR; }
 
-// Two packed fp16 pairs: w0 = {fp16(ya.lo + ya.hi), fp16(yb.lo + yb.hi)}, w1 = {same for yc, yd}.
+// Two packed fp16 pairs: w0 = {fp16(ya.lo + ya.hi), fp16(yb.lo + yb.hi)}, w1 = {same for yc, yd}. Each sum goes to its
+// half of a zero-padded temporary by SDWA and the pairs are joined by full-register ORs, so no register the compiler
+// sees was last written through SDWA.
 __device__ __forceinline__ void add_halves_2pairs(uint32_t ya, uint32_t yb, uint32_t yc, uint32_t yd,
                                                   uint32_t& w0, uint32_t& w1)
 {
-    asm("v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-        "v_add_f16_sdwa %1, %4, %4 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-        "v_add_f16_sdwa %0, %3, %3 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-        "v_add_f16_sdwa %1, %5, %5 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
-        : "=&v"(w0), "=&v"(w1) : "v"(ya), "v"(yb), "v"(yc), "v"(yd));
+    uint32_t a, b, c, d;
+    asm("v_add_f16_sdwa %2, %6, %6 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %3, %7, %7 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %4, %8, %8 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %5, %9, %9 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_or_b32 %0, %2, %3\n\t"
+        "v_or_b32 %1, %4, %5"
+        : "=&v"(w0), "=&v"(w1), "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d) : "v"(ya), "v"(yb), "v"(yc), "v"(yd));
 }
 
 // Decoded chunk, as four packed fp16 pairs ordered for a [n][k] (k-contiguous) destination:

@@ -1,36 +1,57 @@
 // Weight-stationary trellis GEMM for gfx950: the grouped gate|up / down stages of the EXL3 MoE prefill
 // (kernel/exl3_grouped_prefill.cu:148-279) and the single-expert fat GEMM (kernel/exl3_fat_gemm_v2.cu:72-234).
 //
-// Workgroup = 2 waves, tile = 128 rows x 128 output columns (one H128 block), K stage = 32.
-//   * Each stage's 16 trellis tiles (32 x 128 weights) are decoded ONCE per workgroup straight from
-//     global -> VGPR raw words into a k-contiguous [n][k] fp16 tile in LDS (padded rows, conflict-free),
-//     then reused by both waves for all 128 rows.
-//   * Each wave owns 64 rows x 128 columns and runs v_mfma_f32_32x32x16_f16 with the DECODED WEIGHTS as the
-//     first operand and the activations as the second, so the accumulator holds out^T: a lane owns one row
-//     (token) and 64 of the 128 output columns of the tile. The output Hadamard then runs 6 of its 7
-//     butterfly stages inside the lane's registers and one across the wave halves (v_permlane32_swap).
-//   * Activations and raw trellis words are prefetched one stage ahead into VGPRs (no LDS round trip for
-//     the activations); one barrier per stage guards the double-buffered decoded tile.
-//   * Workgroups are laid out XCD-aware: the column tiles of one row block share an XCD (and its L2).
+// Workgroup = 4 waves, tile = up to 256 rows x 128 output columns (one H128 block), K stage = 32.
+//   * Each stage's 16 trellis tiles (32 x 128 weights) are decoded ONCE per workgroup -- a 16-lane row per tile, every
+//     lane decoding two 8-weight chunks from one coalesced load of its own stream words -- into a k-contiguous [n][k]
+//     fp16 tile in LDS, and reused by all four waves for every row of the tile. A row tile covers `tile_rows` (128 or
+//     256) rows of one expert, so each decoded weight feeds up to 256 rows of MFMA work.
+//   * Each wave owns 64 rows x 128 columns and runs v_mfma_f32_16x16x32_f16 with the DECODED WEIGHTS as the first
+//     operand and the activations as the second (out^T in the accumulators: a lane owns one row and 32 columns). The
+//     activation operand of one MFMA is 16 rows x 64 contiguous bytes, so each activation load instruction touches 16
+//     cache-line halves -- the vector memory pipeline (TA/TD), not HBM, is what the loads are sized for.
+//   * Pipeline of stage s: barrier; read stage s's weight fragments from LDS; decode stage s+1 (VALU) while stage s's
+//     MFMAs run; write stage s+1 into the other LDS buffer; issue loads for later stages. Raw trellis words are
+//     prefetched RAW_DEPTH stages ahead and activations ACT_DEPTH stages ahead, straight into VGPRs. One barrier per
+//     stage guards the double-buffered decoded tile.
+//   * A wave with <= 16 valid rows multiplies one 16-row group, a wave with none only decodes (thin experts).
+//   * Epilogue: H128 with 5 butterfly stages in registers and 2 across lanes, x svh / sqrt(128), fp16 store, fp32
+//     store, fp32 per-route store, or fp32 atomics staged through LDS so each atomic instruction covers 64 consecutive
+//     floats of one output row.
+//   * Workgroups are laid out XCD-aware: the column tiles of one row tile share an XCD (and its L2).
 #include "exl3_common.h"
 #include "trellis_decode.h"
+
+#include <type_traits>
 
 namespace exl3 {
 namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int GEMM_WAVES = 2;
+constexpr int GEMM_WAVES = 4;
 constexpr int GEMM_THREADS = 64 * GEMM_WAVES;
-constexpr int TILE_M = 64 * GEMM_WAVES;             // 128 rows
+constexpr int TILE_M = 64 * GEMM_WAVES;             // 256 rows
 constexpr int TILE_N = 128;
 constexpr int TILE_K = 32;
-constexpr int LDS_ROW = TILE_K + 8;                 // halves per n-row of the decoded tile (80 B, conflict-free)
-constexpr int LDS_TILE = TILE_N * LDS_ROW;          // halves per decoded stage
+constexpr int LDS_ROW = TILE_K + 8;                 // halves per n-row of the decoded tile (80 B)
+constexpr int LDS_BLK = 16 * LDS_ROW + 64;          // halves per 16-row block: the pad puts neighbouring tiles' decode
+                                                    // stores 32 banks apart
+constexpr int LDS_TILE = 8 * LDS_BLK;               // halves per decoded stage (128 n-rows)
 constexpr int SC_ROW = TILE_N + 4;                  // floats per staged output row of the scatter epilogue
 constexpr int LDS_MAIN_BYTES = 2 * LDS_TILE * 2;
-constexpr int LDS_SCATTER_BYTES = GEMM_WAVES * 32 * SC_ROW * 4;
+constexpr int LDS_SCATTER_BYTES = GEMM_WAVES * 16 * SC_ROW * 4;
+#ifndef EXL3_RAW_DEPTH
+#define EXL3_RAW_DEPTH 4
+#endif
+#ifndef EXL3_ACT_DEPTH
+#define EXL3_ACT_DEPTH 2
+#endif
+constexpr int RAW_DEPTH = EXL3_RAW_DEPTH;           // raw trellis words in flight (stages)
+constexpr int ACT_DEPTH = EXL3_ACT_DEPTH;           // activation tiles in flight (stages)
+constexpr int UNROLL = 4;                           // stages per loop trip: register buffers keep static names
+static_assert(UNROLL % 2 == 0 && UNROLL % RAW_DEPTH == 0 && UNROLL % ACT_DEPTH == 0, "static buffer rotation");
 
 // STORE_F16: fp16 rows (gate|up). SCATTER_F32: fp32 atomic add into out[token[r]]. STORE_F32: fp32 rows (fat GEMM).
 // STORE_ROUTE_F32: fp32 rows at out[route_index[r]] (per-route partials for the deterministic combine).
@@ -48,11 +69,12 @@ struct GemmParams
     const uint16_t* svh0;
     const uint16_t* svh1;
     int64_t svh_stride;
-    const int32_t* block_expert;   // grouped schedule
+    const int32_t* block_expert;   // grouped schedule: row tiles of `tile_rows` rows
     const int32_t* block_row0;
     const int32_t* counts;
     const int32_t* expert_row0;
-    int n_groups;                  // row blocks (grouped: max_blocks; dense: ceil(m / 128))
+    int tile_rows;                 // rows per schedule entry (128 or 256)
+    int n_groups;                  // row tiles (grouped: table entries; dense: ceil(m / 256))
     int n_slots;                   // 128-col tiles over all tensors
     int n_tiles_each;              // 128-col tiles per tensor
     int64_t m;                     // dense rows
@@ -63,13 +85,13 @@ struct GemmParams
     int64_t out_ld;                // elements per output row
 };
 
-// In-place Walsh-Hadamard transform of 64 values (Sylvester order over the index bits).
-__device__ __forceinline__ void fwht64(float (&x)[64])
+// In-place Walsh-Hadamard transform of 32 values (Sylvester order over the index bits).
+__device__ __forceinline__ void fwht32(float (&x)[32])
 {
     #pragma unroll
-    for (int len = 1; len < 64; len <<= 1)
+    for (int len = 1; len < 32; len <<= 1)
         #pragma unroll
-        for (int i = 0; i < 64; ++i)
+        for (int i = 0; i < 32; ++i)
             if (!(i & len))
             {
                 const float a = x[i], b = x[i + len];
@@ -90,6 +112,17 @@ __device__ __forceinline__ void half_wave_butterfly(float& p, float& q)
     q = __uint_as_float(s2[1]);
 }
 
+// Raw stream dwords a lane holds per stage. K=4 / K=2: the lane's own 2 / 1 dwords of the tile (one coalesced load
+// per 16-lane row) -- the 16-bit look-back of its first chunk is the previous lane's last dword (DPP rotate);
+// K=3: the three dwords its two windows touch, loaded directly.
+template <int BITS> constexpr int raw_words() { return BITS == 4 ? 2 : (BITS == 2 ? 1 : 3); }
+
+// Value of `v` in the previous lane of this lane's 16-lane row (lane 0 of the row gets lane 15's).
+__device__ __forceinline__ uint32_t prev_in_row(uint32_t v)
+{
+    return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, 0x121, 0xF, 0xF, false);     // row_ror:1
+}
+
 template <int BITS, int MODE, bool DENSE>
 __global__ __launch_bounds__(GEMM_THREADS, 2)
 void trellis_gemm_kernel(const GemmParams p)
@@ -97,25 +130,24 @@ void trellis_gemm_kernel(const GemmParams p)
     constexpr int LDS_BYTES = (MODE == MODE_SCATTER_F32 && LDS_SCATTER_BYTES > LDS_MAIN_BYTES) ? LDS_SCATTER_BYTES
                                                                                               : LDS_MAIN_BYTES;
     __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
-    uint16_t (*lds_b)[LDS_TILE] = reinterpret_cast<uint16_t (*)[LDS_TILE]>(lds_raw);
+    uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
 
     int group, slot;
     xcd_group_slot((int) blockIdx.x, p.n_slots, group, slot);
     int e, row0, rows_valid;
+    if (group >= p.n_groups) return;
     if constexpr (DENSE)
     {
-        if (group >= p.n_groups) return;
         e = 0;
         row0 = group * TILE_M;
         rows_valid = (int) min((int64_t) TILE_M, p.m - row0);
     }
     else
     {
-        if (group >= p.n_groups) return;
         e = p.block_expert[group];
         if (e < 0) return;
         row0 = p.block_row0[group];
-        rows_valid = min(TILE_M, p.expert_row0[e] + p.counts[e] - row0);
+        rows_valid = min(p.tile_rows, p.expert_row0[e] + p.counts[e] - row0);
     }
     if (rows_valid <= 0) return;
 
@@ -125,139 +157,205 @@ void trellis_gemm_kernel(const GemmParams p)
                                                                (int64_t) e * p.expert_stride_words);
     const uint16_t* svh = (which ? p.svh1 : p.svh0) + (int64_t) e * p.svh_stride + nt * TILE_N;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int num_kb = p.size_k / TILE_K;
 
-    // ---- decode role: lane -> trellis tile (kt, nt8) of the stage, chunks 4j .. 4j+3 (tile columns j, j+8)
-    const int ti = tid >> 3, j = tid & 7;
-    const int kt = ti >> 3, nt8 = ti & 7;
+    // ---- decode role. A stage holds 16 trellis tiles (kt, nt8) = (k-tile 0..1, n-tile 0..7); wave w decodes the four
+    // tiles kt = w >> 1, nt8 = 4 (w & 1) .. + 3 (512 contiguous bytes at 4 bpw), one 16-lane row per tile. Lane j16
+    // of a row decodes chunks 2 j16 and 2 j16 + 1 (positions 16 j16 .. + 15): tile column a = j16 >> 1 and a + 8,
+    // rows 4 b .. 4 b + 3 and 8 + 4 b .. with b = j16 & 1.
     constexpr int NDW = 8 * BITS;                         // dwords per tile
-    int dw_off[BITS + 1];
-    #pragma unroll
-    for (int i = 0; i <= BITS; ++i) dw_off[i] = (BITS * j - 1 + i + NDW) % NDW;
-    const int64_t tile_stride_stage = (int64_t) 2 * p.tiles_n * NDW;      // dwords per K stage
+    constexpr int NR = raw_words<BITS>();
+    const int j16 = lane & 15;
+    const int ta = j16 >> 1, tb = j16 & 1;
+    const int kt = wave >> 1;
+    const int nt8 = 4 * (wave & 1) + (lane >> 4);
+    const int64_t stage_dwords = (int64_t) 2 * p.tiles_n * NDW;
     const uint32_t* raw_base = packed + ((int64_t) kt * p.tiles_n + nt * 8 + nt8) * NDW;
-    const int wcol0 = (nt8 * 16 + j) * LDS_ROW + kt * 16;                  // column j of the tile
-    const int wcol1 = wcol0 + 8 * LDS_ROW;                                 // column j + 8
-
-    // ---- MFMA role: wave rows [64 wave, 64 wave + 64)
-    const int wave_row0 = 64 * wave;
-    const bool wave_active = wave_row0 < rows_valid;
-    const uint16_t* a_ptr[2];
-    #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    int dw_off[NR];
+    if constexpr (BITS == 3)
     {
-        const int r = min(wave_row0 + 32 * mb + l32, rows_valid - 1);
-        a_ptr[mb] = p.a + (int64_t) (row0 + r) * p.size_k + 16 * h;
+        const int d0 = (16 * j16 * BITS + BITS - 16) >> 5;  // dword of the first window bit (may be -1)
+        #pragma unroll
+        for (int i = 0; i < NR; ++i) dw_off[i] = (d0 + i + NDW) % NDW;
     }
-    const int wread = l32 * LDS_ROW + 16 * h;
+    else
+    {
+        #pragma unroll
+        for (int i = 0; i < NR; ++i) dw_off[i] = NR * j16 + i;
+    }
+    const int wcol0 = nt8 * LDS_BLK + ta * LDS_ROW + kt * 16 + 4 * tb;     // column a, rows 4 b ..
+    const int wcol1 = wcol0 + 8 * LDS_ROW;                                  // column a + 8
 
-    auto load_raw = [&](int kb, uint32_t (&r)[BITS + 1]) {
-        const uint32_t* base = raw_base + (int64_t) kb * tile_stride_stage;
-        #pragma unroll
-        for (int i = 0; i <= BITS; ++i) r[i] = base[dw_off[i]];
-    };
-    auto load_a = [&](int kb, half8_t (&a)[2][2]) {
-        #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-        {
-            const half8_t* src = reinterpret_cast<const half8_t*>(a_ptr[mb] + kb * TILE_K);
-            a[mb][0] = src[0];
-            a[mb][1] = src[1];
-        }
-    };
-    auto decode_store = [&](const uint32_t (&r)[BITS + 1], uint16_t* lds) {
-        Chunk4 c[4];
-        #pragma unroll
-        for (int i = 0; i < 4; ++i)
-        {
-            const int b0 = 8 * i * BITS + BITS - 16;           // window start of chunk 4j+i relative to dword bj
-            const int rel = (b0 >= 0 ? b0 / 32 : -1) + 1;
-            const int off = b0 - 32 * (rel - 1);
-            // the lane's bits end inside r[BITS]; a window that ends there never reads its upper dword
-            c[i] = decode_chunk<BITS>(r[rel], r[rel + 1 <= BITS ? rel + 1 : BITS], off);
-        }
-        const uint4 v0 = {c[0].w[0], c[1].w[0], c[2].w[0], c[3].w[0]};
-        const uint4 v1 = {c[0].w[1], c[1].w[1], c[2].w[1], c[3].w[1]};
-        const uint4 v2 = {c[0].w[2], c[1].w[2], c[2].w[2], c[3].w[2]};
-        const uint4 v3 = {c[0].w[3], c[1].w[3], c[2].w[3], c[3].w[3]};
-        *reinterpret_cast<uint4*>(lds + wcol0) = v0;
-        *reinterpret_cast<uint4*>(lds + wcol0 + 8) = v1;
-        *reinterpret_cast<uint4*>(lds + wcol1) = v2;
-        *reinterpret_cast<uint4*>(lds + wcol1 + 8) = v3;
-    };
-
-    float16_t acc[2][4];
+    // ---- MFMA role: wave rows [64 wave, 64 wave + 64) in four groups of 16 (mb). v_mfma_f32_16x16x32_f16 with the
+    // decoded weights as the first operand (16 columns x 32 k) and the activations as the second (32 k x 16 rows):
+    // lane l supplies row / column l & 15 and k 8 (l >> 4) .. + 7 of both, and receives row (token) l & 15, columns
+    // 4 (l >> 4) .. + 3 of the 16 x 16 output. An activation load is 16 rows x 64 contiguous bytes.
+    const int tok = lane & 15, kq = lane >> 4;
+    const int rows_w = rows_valid - 64 * wave;            // valid rows of this wave (uniform)
+    const uint16_t* a_ptr[4];
     #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-        #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = {};
+    for (int mb = 0; mb < 4; ++mb)
+    {
+        const int r = min(64 * wave + 16 * mb + tok, rows_valid - 1);
+        a_ptr[mb] = p.a + (int64_t) (row0 + r) * p.size_k + 8 * kq;
+    }
+    const int wread = tok * LDS_ROW + 8 * kq;
 
-    // Unconditional even for a wave without valid rows (its rows are clamped, results discarded): keeping
-    // the MFMAs in the same basic block as the decode lets the scheduler interleave the two.
-    auto mfma_stage = [&](const half8_t (&a)[2][2], const uint16_t* lds) {
-        #pragma unroll
-        for (int t = 0; t < 2; ++t)
+    auto load_raw = [&](int kb, uint32_t (&r)[NR]) {
+        const uint32_t* base = raw_base + (int64_t) min(kb, num_kb - 1) * stage_dwords;
+        if constexpr (BITS == 4)
         {
-            half8_t w[4];
+            const uint2 v = *reinterpret_cast<const uint2*>(base + 2 * j16);
+            r[0] = v.x;
+            r[1] = v.y;
+        }
+        else
+        {
             #pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-                w[nb] = *reinterpret_cast<const half8_t*>(lds + nb * 32 * LDS_ROW + wread + 8 * t);
+            for (int i = 0; i < NR; ++i) r[i] = base[dw_off[i]];
+        }
+    };
+    auto decode2 = [&](const uint32_t (&r)[NR], Chunk4& c0, Chunk4& c1) {
+        if constexpr (BITS == 4)
+        {
+            const uint32_t prev = prev_in_row(r[1]);
+            c0 = decode_chunk<4>(prev, r[0], 20);
+            c1 = decode_chunk<4>(r[0], r[1], 20);
+        }
+        else if constexpr (BITS == 2)
+        {
+            const uint32_t prev = prev_in_row(r[0]);
+            c0 = decode_chunk<2>(prev, r[0], 18);
+            c1 = decode_chunk<2>(r[0], r[0], 2);              // window ends inside r[0]
+        }
+        else
+        {
+            // chunk pair j16: windows start 19 / 43 bits (j16 even) or 3 / 27 bits (odd) into dw_off[0]. Even lanes
+            // shift their words down by 16 bits first, so both kinds decode at the compile-time offsets 3 and 27:
+            // constant shifts of a 64-bit window compile to 32-bit funnel shifts, while per-lane 64-bit shift amounts
+            // feeding the decoder's asm gave wrong results at random.
+            const uint32_t x0 = tb ? r[0] : __builtin_amdgcn_alignbit(r[1], r[0], 16);
+            const uint32_t x1 = tb ? r[1] : __builtin_amdgcn_alignbit(r[2], r[1], 16);
+            c0 = decode_chunk<3>(x0, x1, 3);
+            c1 = decode_chunk<3>(x0, x1, 27);
+        }
+    };
+    auto store2 = [&](const Chunk4& c0, const Chunk4& c1, uint16_t* lds) {
+        *reinterpret_cast<uint2*>(lds + wcol0) = make_uint2(c0.w[0], c1.w[0]);
+        *reinterpret_cast<uint2*>(lds + wcol0 + 8) = make_uint2(c0.w[1], c1.w[1]);
+        *reinterpret_cast<uint2*>(lds + wcol1) = make_uint2(c0.w[2], c1.w[2]);
+        *reinterpret_cast<uint2*>(lds + wcol1 + 8) = make_uint2(c0.w[3], c1.w[3]);
+    };
+
+    floatx4 acc[4][8];
+    #pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+        #pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = {};
+
+    // ---- main loop, specialised on the number of 16-row groups a wave multiplies (MBA: 0 = decode only, 1 for a
+    // wave with <= 16 valid rows, else 4). Every variant runs the same barriers. Loads past the last stage are clamped
+    // to it, so every path keeps the same loads in flight.
+    auto mainloop = [&](auto mba_tag) {
+        constexpr int MBA = decltype(mba_tag)::value;
+        uint32_t raw[RAW_DEPTH][NR];
+        half8_t act[ACT_DEPTH][4];
+        auto load_act = [&](int kb, half8_t (&a)[4]) {
+            const int k0 = min(kb, num_kb - 1) * TILE_K;
             #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
+            for (int mb = 0; mb < MBA; ++mb) a[mb] = *reinterpret_cast<const half8_t*>(a_ptr[mb] + k0);
+        };
+        {
+            uint32_t r0[NR];
+            load_raw(0, r0);
+            #pragma unroll
+            for (int s = 1; s <= RAW_DEPTH; ++s) load_raw(s, raw[s % RAW_DEPTH]);
+            #pragma unroll
+            for (int s = 0; s < ACT_DEPTH; ++s) load_act(s, act[s]);
+            Chunk4 c0, c1;
+            decode2(r0, c0, c1);
+            store2(c0, c1, lds_b);
+        }
+        // N stages starting at s0 (a multiple of UNROLL, so buffer indices are compile-time)
+        auto trip = [&](int s0, auto n_tag) {
+            constexpr int N = decltype(n_tag)::value;
+            #pragma unroll
+            for (int u = 0; u < N; ++u)
+            {
+                const int s = s0 + u;
+                __syncthreads();                                // stage s decoded; buffer (s + 1) & 1 free
+                const uint16_t* lds_s = lds_b + (u & 1) * LDS_TILE;
+                half8_t w[8];
+                if constexpr (MBA > 0)
+                {
+                    #pragma unroll
+                    for (int nb = 0; nb < 8; ++nb) w[nb] = *reinterpret_cast<const half8_t*>(lds_s + nb * LDS_BLK + wread);
+                }
+                Chunk4 c0, c1;
+                decode2(raw[(u + 1) % RAW_DEPTH], c0, c1);      // stage s + 1
                 #pragma unroll
-                for (int nb = 0; nb < 4; ++nb)
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[nb], a[mb][t], acc[mb][nb], 0, 0, 0);
+                for (int nb = 0; nb < 8; ++nb)
+                    #pragma unroll
+                    for (int mb = 0; mb < MBA; ++mb)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[nb], act[u % ACT_DEPTH][mb], acc[mb][nb],
+                                                                           0, 0, 0);
+                store2(c0, c1, lds_b + ((u + 1) & 1) * LDS_TILE);
+                load_raw(s + 1 + RAW_DEPTH, raw[(u + 1) % RAW_DEPTH]);
+                load_act(s + ACT_DEPTH, act[u % ACT_DEPTH]);
+            }
+        };
+        // The first trip is peeled so that the loads in flight at the loop head are the same on entry and on the
+        // back edge; the compiler's wait counts there then only wait for the stage they feed. num_kb is even
+        // (K % 64 == 0), so what is left after whole trips is 0 or 2 stages.
+        using full = std::integral_constant<int, UNROLL>;
+        int s0 = 0;
+        if (num_kb >= UNROLL)
+        {
+            trip(0, full{});
+            for (s0 = UNROLL; s0 + UNROLL <= num_kb; s0 += UNROLL) trip(s0, full{});
         }
+        if (s0 < num_kb) trip(s0, std::integral_constant<int, 2>{});
     };
+    if (rows_w > 16) mainloop(std::integral_constant<int, 4>{});
+    else if (rows_w > 0) mainloop(std::integral_constant<int, 1>{});
+    else mainloop(std::integral_constant<int, 0>{});
 
-    // ---- main loop, unrolled by two so both register buffers have static names. num_kb is even (K % 64 == 0).
-    // Loads and decodes are unconditional (stage index clamped at the end) so every path keeps the same number
-    // of loads in flight and the waits stay partial: a stage's raw words and activations are waited for only
-    // when they are consumed, one stage after they were issued.
-    uint32_t raw_a[BITS + 1], raw_b[BITS + 1];
-    half8_t act_a[2][2], act_b[2][2];
-    const int last = num_kb - 1;
-    load_raw(0, raw_a);
-    load_a(0, act_a);
-    load_raw(1, raw_b);
-    load_a(1, act_b);
-    decode_store(raw_a, lds_b[0]);
-    for (int kb = 0; kb < num_kb; kb += 2)
-    {
-        __syncthreads();
-        decode_store(raw_b, lds_b[1]);                  // stage kb + 1
-        load_raw(min(kb + 2, last), raw_a);
-        mfma_stage(act_a, lds_b[0]);                    // stage kb
-        load_a(min(kb + 2, last), act_a);
-        __syncthreads();
-        decode_store(raw_a, lds_b[0]);                  // stage kb + 2 (discarded after the last stage)
-        load_raw(min(kb + 3, last), raw_b);
-        mfma_stage(act_b, lds_b[1]);                    // stage kb + 1
-        load_a(min(kb + 3, last), act_b);
-    }
-
-    // ---- epilogue: per 32-row block, H128 over the 128 columns of each row, scale by svh (and the route weight),
-    // then store / scatter. The scatter stages each block through LDS so that every atomic instruction covers 64
-    // consecutive floats of one output row (two cache lines) instead of 32 rows.
+    // ---- epilogue, per 16-row group: H128 over the 128 columns of each row (lane l holds columns
+    // 16 nb + 4 (l >> 4) + r: 5 butterfly stages in registers, column bit 2 across lanes l ^ 16, bit 3 across l ^ 32),
+    // scale by svh / sqrt(128) (and the route weight), then store / scatter. The scatter stages each group through LDS
+    // so that every atomic instruction covers 64 consecutive floats of one output row.
     if constexpr (MODE == MODE_SCATTER_F32) __syncthreads();     // decoded tiles are dead; LDS becomes staging
-    if (!wave_active) return;
+    if (rows_w <= 0) return;
     const int out_col0 = which * p.n_tiles_each * TILE_N + nt * TILE_N;
+    float sv[32];
     #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int nb = 0; nb < 8; ++nb)
     {
-        const int r_local = wave_row0 + 32 * mb + l32;        // this lane's row within the tile
-        if (wave_row0 + 32 * mb >= rows_valid) break;           // uniform over the wave
-        // x[nb * 16 + r] holds column 32 nb + 8 (r >> 2) + 4 h + (r & 3)
-        float x[64];
+        const uint2 v = *reinterpret_cast<const uint2*>(svh + 16 * nb + 4 * kq);
+        sv[4 * nb + 0] = h2f(v.x & 0xFFFF) * HAD_SCALE;
+        sv[4 * nb + 1] = h2f(v.x >> 16) * HAD_SCALE;
+        sv[4 * nb + 2] = h2f(v.y & 0xFFFF) * HAD_SCALE;
+        sv[4 * nb + 3] = h2f(v.y >> 16) * HAD_SCALE;
+    }
+    float* stage = reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW);
+    #pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+    {
+        if (16 * mb >= rows_w) break;                           // uniform over the wave
+        float x[32];
         #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
+        for (int nb = 0; nb < 8; ++nb)
             #pragma unroll
-            for (int r = 0; r < 16; ++r) x[nb * 16 + r] = acc[mb][nb][r];
-        fwht64(x);
+            for (int r = 0; r < 4; ++r) x[4 * nb + r] = acc[mb][nb][r];
+        fwht32(x);
         #pragma unroll
-        for (int i = 0; i < 64; i += 2) half_wave_butterfly(x[i], x[i + 1]);
+        for (int i = 0; i < 32; ++i) x[i] = lane_butterfly<16>(x[i], lane);
+        #pragma unroll
+        for (int i = 0; i < 32; i += 2) half_wave_butterfly(x[i], x[i + 1]);
 
+        const int r_local = 64 * wave + 16 * mb + tok;          // this lane's row within the tile
         const bool row_ok = r_local < rows_valid;
         const int64_t srow = (int64_t) row0 + min(r_local, rows_valid - 1);
         float rw = 1.0f;
@@ -267,45 +365,38 @@ void trellis_gemm_kernel(const GemmParams p)
             rw = h2f(p.route_weight[srow]);
             orow = (MODE == MODE_SCATTER_F32) ? p.token[srow] : (int64_t) p.route_index[srow];
         }
-        float* stage = reinterpret_cast<float*>(lds_raw) + wave * (32 * SC_ROW);
         #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
+        for (int nb = 0; nb < 8; ++nb)
+        {
+            const int col = 16 * nb + 4 * kq;                   // first of this lane's 4 consecutive columns
+            float v[4];
             #pragma unroll
-            for (int g = 0; g < 4; ++g)
+            for (int r = 0; r < 4; ++r) v[r] = x[4 * nb + r] * sv[4 * nb + r] * rw;
+            if constexpr (MODE == MODE_SCATTER_F32)
             {
-                const int col = 32 * nb + 8 * g + 4 * h;          // first of 4 consecutive columns
-                const uint2 sv = *reinterpret_cast<const uint2*>(svh + col);
-                const float sc = HAD_SCALE * rw;
-                const float s[4] = {h2f(sv.x & 0xFFFF) * sc, h2f(sv.x >> 16) * sc, h2f(sv.y & 0xFFFF) * sc,
-                                    h2f(sv.y >> 16) * sc};
-                float v[4];
-                #pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = x[nb * 16 + 4 * g + q] * s[q];
-                if constexpr (MODE == MODE_SCATTER_F32)
-                {
-                    *reinterpret_cast<float4*>(stage + l32 * SC_ROW + col) = make_float4(v[0], v[1], v[2], v[3]);
-                    continue;
-                }
-                if (!row_ok) continue;
-                if constexpr (MODE == MODE_STORE_F16)
-                {
-                    uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + orow * p.out_ld + out_col0 + col;
-                    uint2 pk;
-                    pk.x = (uint32_t) f2h(v[0]) | ((uint32_t) f2h(v[1]) << 16);
-                    pk.y = (uint32_t) f2h(v[2]) | ((uint32_t) f2h(v[3]) << 16);
-                    *reinterpret_cast<uint2*>(o) = pk;
-                }
-                else
-                {
-                    float* o = reinterpret_cast<float*>(p.out) + orow * p.out_ld + out_col0 + col;
-                    *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
-                }
+                *reinterpret_cast<float4*>(stage + tok * SC_ROW + col) = make_float4(v[0], v[1], v[2], v[3]);
+                continue;
             }
+            if (!row_ok) continue;
+            if constexpr (MODE == MODE_STORE_F16)
+            {
+                uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + orow * p.out_ld + out_col0 + col;
+                uint2 pk;
+                pk.x = (uint32_t) f2h(v[0]) | ((uint32_t) f2h(v[1]) << 16);
+                pk.y = (uint32_t) f2h(v[2]) | ((uint32_t) f2h(v[3]) << 16);
+                *reinterpret_cast<uint2*>(o) = pk;
+            }
+            else
+            {
+                float* o = reinterpret_cast<float*>(p.out) + orow * p.out_ld + out_col0 + col;
+                *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        }
         if constexpr (MODE == MODE_SCATTER_F32)
         {
             // LDS accesses of one wave complete in order: the reads below see the writes above, and the next
-            // block's writes land after these reads.
-            const int nrows = min(32, rows_valid - (wave_row0 + 32 * mb));
+            // group's writes land after these reads. Lane t (< 16) holds row t's destination token.
+            const int nrows = min(16, rows_w - 16 * mb);
             const uint32_t tok_lo = (uint32_t) orow, tok_hi = (uint32_t) ((uint64_t) orow >> 32);
             float* outp = reinterpret_cast<float*>(p.out) + out_col0 + lane;
             for (int t = 0; t < nrows; ++t)
@@ -429,15 +520,17 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15)
 
 using namespace exl3;
 
-extern "C" int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
-                                 const uint16_t* packed_gate, const uint16_t* packed_up, int64_t expert_stride_words,
-                                 int tiles_k, int tiles_n, int bits,
-                                 const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
-                                 const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
-                                 const int32_t* counts, const int32_t* expert_row0, int n_experts,
-                                 const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
-                                 void* out, int64_t out_rows, int mode, void* stream)
+extern "C" int exl3_grouped_gemm_tiles(const uint16_t* a, int64_t a_rows, int size_k,
+                                       const uint16_t* packed_gate, const uint16_t* packed_up,
+                                       int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
+                                       const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                                       const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
+                                       int tile_rows, const int32_t* counts, const int32_t* expert_row0,
+                                       int n_experts, const int64_t* token_sorted, const uint16_t* route_weight,
+                                       const int32_t* route_index, void* out, int64_t out_rows, int mode,
+                                       void* stream)
 {
+    EXL3_CHECK(tile_rows == 128 || tile_rows == TILE_M, "tile_rows must be 128 or %d", TILE_M);
     EXL3_CHECK(bits >= 2 && bits <= 4, "unsupported bits %d (2, 3 or 4)", bits);
     EXL3_CHECK(size_k == tiles_k * 16 && size_k % 64 == 0 && size_k > 0, "K mismatch");
     const int size_n_each = tiles_n * 16;
@@ -451,8 +544,8 @@ extern "C" int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
     EXL3_CHECK(a && packed_gate && svh_gate && block_expert && block_row0 && counts && expert_row0 && out,
                "null pointer");
     EXL3_CHECK(aligned16(a) && (size_k * 2) % 16 == 0, "a must be 16-byte aligned");
-    EXL3_CHECK(((reinterpret_cast<uintptr_t>(packed_gate) | reinterpret_cast<uintptr_t>(packed_up)) & 3) == 0 &&
-               expert_stride_words % 2 == 0, "trellis tensors must be 4-byte aligned");
+    EXL3_CHECK(((reinterpret_cast<uintptr_t>(packed_gate) | reinterpret_cast<uintptr_t>(packed_up)) & 7) == 0 &&
+               expert_stride_words % 4 == 0, "trellis tensors must be 8-byte aligned");
     EXL3_CHECK(((reinterpret_cast<uintptr_t>(svh_gate) | reinterpret_cast<uintptr_t>(svh_up)) & 7) == 0 &&
                svh_stride % 4 == 0, "svh must be 8-byte aligned");
     const int n_tensors = packed_up ? 2 : 1;
@@ -461,7 +554,8 @@ extern "C" int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
     p.packed0 = packed_gate; p.packed1 = packed_up; p.expert_stride_words = expert_stride_words;
     p.tiles_n = tiles_n; p.svh0 = svh_gate; p.svh1 = svh_up; p.svh_stride = svh_stride;
     p.block_expert = block_expert; p.block_row0 = block_row0; p.counts = counts; p.expert_row0 = expert_row0;
-    p.n_groups = max_blocks; p.n_tiles_each = size_n_each / TILE_N; p.n_slots = n_tensors * p.n_tiles_each;
+    p.tile_rows = tile_rows; p.n_groups = max_blocks; p.n_tiles_each = size_n_each / TILE_N;
+    p.n_slots = n_tensors * p.n_tiles_each;
     p.token = token_sorted; p.route_weight = route_weight; p.route_index = route_index; p.out = out;
     hipStream_t s = as_stream(stream);
     int rc;
@@ -493,6 +587,21 @@ extern "C" int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
     return hip_status("grouped_gemm");
 }
 
+extern "C" int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
+                                 const uint16_t* packed_gate, const uint16_t* packed_up, int64_t expert_stride_words,
+                                 int tiles_k, int tiles_n, int bits,
+                                 const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                                 const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
+                                 const int32_t* counts, const int32_t* expert_row0, int n_experts,
+                                 const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
+                                 void* out, int64_t out_rows, int mode, void* stream)
+{
+    return exl3_grouped_gemm_tiles(a, a_rows, size_k, packed_gate, packed_up, expert_stride_words, tiles_k, tiles_n,
+                                   bits, svh_gate, svh_up, svh_stride, block_expert, block_row0, max_blocks, 128,
+                                   counts, expert_row0, n_experts, token_sorted, route_weight, route_index, out,
+                                   out_rows, mode, stream);
+}
+
 namespace {
 
 int fat_common(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed, int tiles_k, int tiles_n,
@@ -509,7 +618,7 @@ int fat_common(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed,
     EXL3_CHECK(variant >= 0 && variant <= 3, "unknown variant");
     EXL3_CHECK(m >= 0 && m < ((int64_t) 1 << 31), "bad row count");
     EXL3_CHECK(aligned16(a) && aligned16(out) && (reinterpret_cast<uintptr_t>(svh) & 7) == 0 &&
-               (reinterpret_cast<uintptr_t>(packed) & 3) == 0, "tensors must be contiguous and aligned");
+               (reinterpret_cast<uintptr_t>(packed) & 7) == 0, "tensors must be contiguous and aligned");
     return EXL3_OK;
 }
 

@@ -30,10 +30,13 @@ SIGNATURES = {
     "exl3_sort_routes_workspace_bytes": (SZ, [I64, I32, I32]),
     "exl3_sort_routes": (I32, [P, I32, P, I32, I64, I32, I32, P, P, P, P, P, P, P, SZ, P]),
     "exl3_build_blocks": (I32, [P, I32, I32, P, P, P, P]),
+    "exl3_build_tiles": (I32, [P, I32, I32, I32, P, P, P, P]),
     "exl3_row_had": (I32, [P, P, P, P, P, I64, I64, I64, I32, I32, P]),
     "exl3_act_had": (I32, [P, I64, P, P, P, I64, I64, I32, F32, P]),
     "exl3_grouped_gemm": (I32, [P, I64, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, P, P, I32, P, P,
                                 P, P, I64, I32, P]),
+    "exl3_grouped_gemm_tiles": (I32, [P, I64, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, I32, P, P, I32,
+                                      P, P, P, P, I64, I32, P]),
     "exl3_combine_routes": (I32, [P, P, P, I32, I32, I64, I32, I64, P]),
     "exl3_fat_gemm": (I32, [P, I64, I32, P, I32, I32, I32, P, I64, P, I64, I32, I32, I32, I32, P]),
     "exl3_fat_gemm_scatter": (I32, [P, I64, I32, P, I32, I32, I32, P, I64, P, I64, P, P, I32, I32, I32, I32, P]),
@@ -42,7 +45,7 @@ SIGNATURES = {
     "exl3_decode_states": (I32, [P, P, I64, P]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 _path = None

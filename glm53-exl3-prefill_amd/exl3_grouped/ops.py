@@ -103,17 +103,25 @@ def sort_routes(topk_ids: torch.Tensor, topk_weights: torch.Tensor, n_experts: i
 
 
 def build_blocks(counts: torch.Tensor, block_expert: torch.Tensor, block_row0: torch.Tensor, meta: torch.Tensor) -> None:
-    """kernel/exl3_grouped_prefill.cu:285-294."""
-    _check(counts.dtype == torch.int32 and block_expert.dtype == torch.int32 and block_row0.dtype == torch.int32
+    """kernel/exl3_grouped_prefill.cu:285-294 (128-row blocks)."""
+    build_tiles(counts, block_expert, block_row0, meta, 128)
+
+
+def build_tiles(counts: torch.Tensor, tile_expert: torch.Tensor, tile_row0: torch.Tensor, meta: torch.Tensor,
+                tile_rows: int) -> None:
+    """build_blocks with `tile_rows` (64, 128 or 256) rows per entry (new; 256-row tables feed grouped_gemm's
+    tile_rows=256 schedule)."""
+    _check(counts.dtype == torch.int32 and tile_expert.dtype == torch.int32 and tile_row0.dtype == torch.int32
            and meta.dtype == torch.int32, "int32 tensors")
     _check(counts.numel() <= 1024, "too many experts")
-    _check(block_row0.numel() >= block_expert.numel() and meta.numel() >= 2, "block table shapes")
-    _check(counts.is_contiguous() and block_expert.is_contiguous() and block_row0.is_contiguous()
+    _check(int(tile_rows) in (64, 128, 256), "tile_rows must be 64, 128 or 256")
+    _check(tile_row0.numel() >= tile_expert.numel() and meta.numel() >= 2, "block table shapes")
+    _check(counts.is_contiguous() and tile_expert.is_contiguous() and tile_row0.is_contiguous()
            and meta.is_contiguous(), "contiguous tensors")
-    dev = _require_cuda(counts, block_expert, block_row0, meta)
+    dev = _require_cuda(counts, tile_expert, tile_row0, meta)
     with _On(dev) as s:
-        _lib.call("exl3_build_blocks", _p(counts), counts.numel(), block_expert.numel(), _p(block_expert),
-                  _p(block_row0), _p(meta), s)
+        _lib.call("exl3_build_tiles", _p(counts), counts.numel(), int(tile_rows), tile_expert.numel(),
+                  _p(tile_expert), _p(tile_row0), _p(meta), s)
 
 
 # ------------------------------------------------------------------------------------------- Hadamard passes
@@ -160,10 +168,12 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
                  svh_gate: torch.Tensor, svh_up: Optional[torch.Tensor], block_expert: torch.Tensor,
                  block_row0: torch.Tensor, counts: torch.Tensor, expert_row0: torch.Tensor,
                  token_sorted: Optional[torch.Tensor], route_weight: Optional[torch.Tensor], out: torch.Tensor,
-                 mode: int, route_index: Optional[torch.Tensor] = None) -> None:
+                 mode: int, route_index: Optional[torch.Tensor] = None, tile_rows: int = 128) -> None:
     """kernel/exl3_grouped_prefill.cu:326-378. mode 0: fp16 store; mode 1: fp32 atomic scatter into
     out[token_sorted[r]]; mode 2 (new): fp32 store of the weighted row into out[route_index[r]] (out [T*topk, N]),
-    summed per token by combine_routes in a fixed order."""
+    summed per token by combine_routes in a fixed order. tile_rows (new): rows per block-table entry, 128 for
+    build_blocks' table (the reference's), 256 for a build_tiles(..., 256) table."""
+    _check(int(tile_rows) in (128, 256), "tile_rows must be 128 or 256")
     _check(a.dtype == torch.float16 and a.is_contiguous(), "a fp16 contiguous")
     _check(packed_gate.dim() == 4 and packed_gate.dtype in (torch.int16, torch.uint16) and
            packed_gate.stride(3) == 1 and packed_gate.stride(2) == packed_gate.size(3) and
@@ -209,9 +219,10 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
                         expert_row0, out, token_sorted if mode == 1 else None, route_weight if mode else None,
                         route_index if mode == 2 else None)
     with _On(dev) as s:
-        _lib.call("exl3_grouped_gemm", _p(a), a.size(0), size_k, _p(packed_gate), _p(packed_up), expert_stride,
-                  tiles_k, tiles_n, bits, _p(svh_gate), _p(svh_up), svh_stride, _p(block_expert), _p(block_row0),
-                  max_blocks, _p(counts), _p(expert_row0), E, _p(token_sorted) if mode == 1 else None,
+        _lib.call("exl3_grouped_gemm_tiles", _p(a), a.size(0), size_k, _p(packed_gate), _p(packed_up),
+                  expert_stride, tiles_k, tiles_n, bits, _p(svh_gate), _p(svh_up), svh_stride, _p(block_expert),
+                  _p(block_row0), max_blocks, int(tile_rows), _p(counts), _p(expert_row0), E,
+                  _p(token_sorted) if mode == 1 else None,
                   _p(route_weight) if mode else None, _p(route_index) if mode == 2 else None, _p(out), out.size(0),
                   mode, s)
 

@@ -43,6 +43,7 @@ def _load_ext():
 
 
 SCATTER_MODES = ("atomic", "combine")
+TILE_ROWS = 256
 
 
 def scatter_mode() -> str:
@@ -87,18 +88,21 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     gp.sort_routes(ids, weights, E, token_sorted, weight_sorted, expert_of_row, counts, expert_row0,
                    route_index=route_index)
     mark("sort_routes")
-    max_blocks = R // 128 + E
+    # row tiles of TILE_ROWS rows of one expert: each decoded trellis tile feeds up to TILE_ROWS rows of MFMA work
+    # (the reference's 128-row block table is build_blocks; the GEMM accepts either)
+    max_blocks = R // TILE_ROWS + E
     block_expert = torch.empty(max_blocks, dtype=torch.int32, device=dev)
     block_row0 = torch.empty_like(block_expert)
     meta = torch.zeros(2, dtype=torch.int32, device=dev)
-    gp.build_blocks(counts, block_expert, block_row0, meta)
+    gp.build_tiles(counts, block_expert, block_row0, meta, TILE_ROWS)
     mark("build_blocks")
     h13 = torch.empty(R, K, dtype=torch.float16, device=dev)
     gp.row_had(x16, h13, token_sorted, expert_of_row, layer.w13_suh[:, 0], True)
     mark("row_had")
     gu = torch.empty(R, 2 * I, dtype=torch.float16, device=dev)
     gp.grouped_gemm(h13, layer.w13_trellis[:, 0], layer.w13_trellis[:, 1], layer.w13_svh[:, 0], layer.w13_svh[:, 1],
-                    block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 0)
+                    block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 0,
+                    tile_rows=TILE_ROWS)
     mark("gemm_gate_up")
     act = torch.empty(R, I, dtype=torch.float16, device=dev)
     gp.act_had(gu, act, expert_of_row, layer.w2_suh, float(limit))
@@ -107,13 +111,14 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
         out = torch.zeros(T, K, dtype=torch.float32, device=dev)
         mark("zero_out")
         gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
-                        block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, out, 1)
+                        block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, out, 1,
+                        tile_rows=TILE_ROWS)
         mark("gemm_down_scatter")
         return out
     partial = torch.empty(R, K, dtype=torch.float32, device=dev)
     gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
                     block_expert, block_row0, counts, expert_row0, None, weight_sorted, partial, 2,
-                    route_index=route_index)
+                    route_index=route_index, tile_rows=TILE_ROWS)
     mark("gemm_down_routes")
     out = torch.empty(T, K, dtype=torch.float32, device=dev)
     gp.combine_routes(partial, out, topk, ids, E)

@@ -76,6 +76,14 @@ int exl3_build_blocks(const int32_t* counts, int n_experts, int max_blocks,
                       int32_t* block_expert, int32_t* block_row0, int32_t* meta, void* stream);
 
 /*
+ * Row-tile table of `tile_rows` rows per entry (64, 128 or 256): exl3_build_blocks is this with 128. New (no
+ * reference counterpart): the grouped GEMM amortises each decoded trellis tile over up to 256 rows of one expert
+ * when given a 256-row table (max_tiles >= R/256 + n_experts).
+ */
+int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_rows, int max_tiles,
+                     int32_t* tile_expert, int32_t* tile_row0, int32_t* meta, void* stream);
+
+/*
  * Input Hadamard (pybind op row_had, kernel/exl3_grouped_prefill.cu:101-115 and :296-311):
  *   dst[r, :] = fp16( H128( src[gather ? token_sorted[r] : r, :] * suh[expert_of_row[r], :] ) / sqrt(128) )
  * per 128-column block, fp32 inside. src fp16 [*, K] contiguous, dst fp16 [rows, K] contiguous,
@@ -122,6 +130,19 @@ int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
                       const int32_t* counts, const int32_t* expert_row0, int n_experts,
                       const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
                       void* out, int64_t out_rows, int mode, void* stream);
+
+/*
+ * exl3_grouped_gemm over a row-tile table of `tile_rows` rows per entry (128: the reference's block table, what
+ * exl3_grouped_gemm passes; 256: a table from exl3_build_tiles(..., 256, ...)). Same modes and outputs.
+ */
+int exl3_grouped_gemm_tiles(const uint16_t* a, int64_t a_rows, int size_k,
+                            const uint16_t* packed_gate, const uint16_t* packed_up, int64_t expert_stride_words,
+                            int tiles_k, int tiles_n, int bits,
+                            const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                            const int32_t* block_expert, const int32_t* block_row0, int max_blocks, int tile_rows,
+                            const int32_t* counts, const int32_t* expert_row0, int n_experts,
+                            const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
+                            void* out, int64_t out_rows, int mode, void* stream);
 
 /*
  * Deterministic route combine (new; pairs with grouped_gemm mode 2): out[t, :] = sum_{j < topk} partial[t*topk + j, :]

@@ -231,20 +231,20 @@ int orc_sort_routes(const int64_t* ids, const float* weights, int64_t T, int top
     return 0;
 }
 
-/* Restates kernel/exl3_grouped_prefill.cu:63-96 (TILE_M = 128): block b of expert e covers sorted rows
-   [expert_row0[e] + 128 i, ...). Entries b >= n_blocks get block_expert = -1; block_row0 there is left
-   untouched (the reference never writes it). meta = {n_blocks, n_rows}. */
-void orc_build_blocks(const int32_t* counts, int E, int max_blocks, int32_t* block_expert, int32_t* block_row0,
-                      int32_t* meta)
+/* Restates kernel/exl3_grouped_prefill.cu:63-96 (TILE_M = 128 there; tile_rows here): block b of expert e covers
+   sorted rows [expert_row0[e] + tile_rows i, ...). Entries b >= n_blocks get block_expert = -1; block_row0 there is
+   left untouched (the reference never writes it). meta = {n_blocks, n_rows}. */
+void orc_build_tiles(const int32_t* counts, int E, int tile_rows, int max_blocks, int32_t* block_expert,
+                     int32_t* block_row0, int32_t* meta)
 {
     int64_t row = 0, blk = 0;
     for (int e = 0; e < E; ++e)
     {
-        const int nblk = (counts[e] + 127) / 128;
+        const int nblk = (counts[e] + tile_rows - 1) / tile_rows;
         for (int i = 0; i < nblk; ++i)
         {
             const int64_t b = blk + i;
-            if (b < max_blocks) { block_expert[b] = e; block_row0[b] = (int32_t) (row + 128 * i); }
+            if (b < max_blocks) { block_expert[b] = e; block_row0[b] = (int32_t) (row + (int64_t) tile_rows * i); }
         }
         row += counts[e];
         blk += nblk;
@@ -252,4 +252,10 @@ void orc_build_blocks(const int32_t* counts, int E, int max_blocks, int32_t* blo
     meta[0] = (int32_t) blk;
     meta[1] = (int32_t) row;
     for (int64_t b = blk; b < max_blocks; ++b) block_expert[b] = -1;
+}
+
+void orc_build_blocks(const int32_t* counts, int E, int max_blocks, int32_t* block_expert, int32_t* block_row0,
+                      int32_t* meta)
+{
+    orc_build_tiles(counts, E, 128, max_blocks, block_expert, block_row0, meta);
 }

@@ -60,6 +60,7 @@ def lib():
         L.orc_sort_routes.restype = ctypes.c_int
         L.orc_sort_routes.argtypes = [P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, P, P, P, P, P]
         L.orc_build_blocks.argtypes = [P, ctypes.c_int, ctypes.c_int, P, P, P]
+        L.orc_build_tiles.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P]
         _LIB = L
     return _LIB
 
@@ -144,13 +145,17 @@ def sort_routes(ids: np.ndarray, weights: np.ndarray, n_experts: int):
     return token_sorted, weight_sorted.view(np.float16), expert_of_row, counts, expert_row0
 
 
-def build_blocks(counts: np.ndarray, max_blocks: int, init: int = 0):
-    """kernel/exl3_grouped_prefill.cu:63-96; block_row0 past n_blocks keeps `init`."""
+def build_blocks(counts: np.ndarray, max_blocks: int, init: int = 0, tile_rows: int = 128):
+    """kernel/exl3_grouped_prefill.cu:63-96 (128-row blocks; other tile sizes for the 256-row schedule);
+    block_row0 past n_blocks keeps `init`."""
     counts = np.ascontiguousarray(counts, dtype=np.int32)
     be = np.full(max_blocks, init, dtype=np.int32)
     br = np.full(max_blocks, init, dtype=np.int32)
     meta = np.zeros(2, dtype=np.int32)
-    lib().orc_build_blocks(_p(counts), counts.size, max_blocks, _p(be), _p(br), _p(meta))
+    if tile_rows == 128:
+        lib().orc_build_blocks(_p(counts), counts.size, max_blocks, _p(be), _p(br), _p(meta))
+    else:
+        lib().orc_build_tiles(_p(counts), counts.size, tile_rows, max_blocks, _p(be), _p(br), _p(meta))
     return be, br, meta
 
 

@@ -43,6 +43,11 @@ def test_build_blocks_rejects_too_many_experts():
     assert rc == _lib.EXL3_ERR_ARG and msg == "too many experts"
 
 
+def test_build_tiles_rejects_bad_tile_rows():
+    rc, msg = rc_and_msg("exl3_build_tiles", FAKE, 8, 96, 10, FAKE, FAKE, FAKE, None)
+    assert rc == _lib.EXL3_ERR_ARG and "tile_rows" in msg
+
+
 def test_row_had_rejects_bad_k():
     rc, msg = rc_and_msg("exl3_row_had", FAKE, FAKE, FAKE, FAKE, FAKE, 100, 100, 4, 100, 1, None)
     assert rc == _lib.EXL3_ERR_ARG and "multiple of 128" in msg
@@ -74,6 +79,10 @@ def test_grouped_gemm_contract():
     assert "mode" in _gemm(mode=3)[1]
     assert "route_index" in _gemm(mode=2)[1]
     assert "combine" in rc_and_msg("exl3_combine_routes", FAKE, FAKE, None, 4, 8, 10, 8, 6, None)[1]
+    a = dict(a=FAKE, a_rows=256, size_k=512, pg=FAKE, pu=None, es=32 * 16 * 64, tk=32, tn=16, bits=4, sg=FAKE,
+             su=None, ss=256, be=FAKE, br=FAKE, mb=10, tile_rows=64, counts=FAKE, row0=FAKE, E=8, tok=FAKE, rw=FAKE,
+             ri=None, out=FAKE, out_rows=64, mode=1)
+    assert "tile_rows" in rc_and_msg("exl3_grouped_gemm_tiles", *a.values(), None)[1]
 
 
 def test_fat_gemm_contract():

@@ -108,17 +108,21 @@ def test_sort_routes_empty_and_dropped(dev):
     assert ts[4:].tolist() == [0, 0] and eor[4:].tolist() == [0, 0] and ws[4:].tolist() == [0, 0]
 
 
+@pytest.mark.parametrize("tile_rows", [128, 64, 256])
 @pytest.mark.parametrize("kind,T,E,k", ROUTINGS)
-def test_build_blocks_bit_exact(dev, kind, T, E, k):
+def test_build_blocks_bit_exact(dev, kind, T, E, k, tile_rows):
     ids, w = synth.make_routing(kind, T, E, k, seed=T + 1)
     counts = np.bincount(ids.ravel(), minlength=E).astype(np.int32)
     R = ids.size
-    for max_blocks in (R // 128 + E, max(1, R // 512)):
-        rbe, rbr, rmeta = O.build_blocks(counts, max_blocks, init=-7)
+    for max_blocks in (R // tile_rows + E, max(1, R // 512)):
+        rbe, rbr, rmeta = O.build_blocks(counts, max_blocks, init=-7, tile_rows=tile_rows)
         be = torch.full((max_blocks,), -7, dtype=torch.int32, device=dev)
         br = torch.full((max_blocks,), -7, dtype=torch.int32, device=dev)
         meta = torch.zeros(2, dtype=torch.int32, device=dev)
-        gp.build_blocks(t16(counts, dev), be, br, meta)
+        if tile_rows == 128:
+            gp.build_blocks(t16(counts, dev), be, br, meta)
+        else:
+            gp.build_tiles(t16(counts, dev), be, br, meta, tile_rows)
         assert np.array_equal(be.cpu().numpy(), rbe) and np.array_equal(br.cpu().numpy(), rbr)
         assert np.array_equal(meta.cpu().numpy(), rmeta)
 
@@ -163,62 +167,67 @@ def stage_inputs(name, seed, T=None, bits=None, svh_scale=1.0):
     return L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0)
 
 
-def gpu_blocks(counts, R, E, dev):
-    mb = R // 128 + E
+def gpu_blocks(counts, R, E, dev, tile_rows=128):
+    mb = R // tile_rows + E
     be = torch.empty(mb, dtype=torch.int32, device=dev)
     br = torch.empty(mb, dtype=torch.int32, device=dev)
     meta = torch.zeros(2, dtype=torch.int32, device=dev)
-    gp.build_blocks(t16(counts, dev), be, br, meta)
+    gp.build_tiles(t16(counts, dev), be, br, meta, tile_rows)
     return be, br
 
 
-@pytest.mark.parametrize("name,T", [("tiny", None), ("layer1k", None), ("headline", 256)])
-def test_grouped_gemm_gate_up(dev, name, T):
-    L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, 1, T=T)
+@pytest.mark.parametrize("tile_rows", [128, 256])
+@pytest.mark.parametrize("name,T,bits", [("tiny", None, 4), ("layer1k", None, 4), ("headline", 256, 4),
+                                         ("thin", 1024, 4), ("thin", 1024, 3), ("thin", 1024, 2)])
+def test_grouped_gemm_gate_up(dev, name, T, bits, tile_rows):
+    L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, 1, T=T, bits=bits)
     R = ids.size
     h13 = O.row_had(x.astype(np.float16), ts, eor, L.w13_suh[:, 0], True)
     cache = O.WeightCache(layer)
     ref = O.grouped_gemm_mode0(h13, cache, counts, row0)
     TL = synth.to_device(L, dev)
-    be, br = gpu_blocks(counts, R, cfg["E"], dev)
+    be, br = gpu_blocks(counts, R, cfg["E"], dev, tile_rows)
     gu = torch.empty(R, 2 * cfg["I"], dtype=torch.float16, device=dev)
     gp.grouped_gemm(t16(h13, dev), TL.w13_trellis[:, 0], TL.w13_trellis[:, 1], TL.w13_svh[:, 0], TL.w13_svh[:, 1],
-                    be, br, t16(counts, dev), t16(row0, dev), None, None, gu, 0)
+                    be, br, t16(counts, dev), t16(row0, dev), None, None, gu, 0, tile_rows=tile_rows)
     got = gu.cpu().numpy()
     assert O.rel_l2(got, ref) < 1e-4 and within_f16_steps(got, ref)
 
 
-@pytest.mark.parametrize("name,T", [("tiny", None), ("layer1k", None), ("thin", 512)])
-def test_grouped_gemm_down_scatter(dev, name, T):
-    L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, 2, T=T)
+@pytest.mark.parametrize("tile_rows", [128, 256])
+@pytest.mark.parametrize("name,T,bits", [("tiny", None, 4), ("layer1k", None, 4), ("thin", 512, 4), ("thin", 512, 3),
+                                         ("thin", 512, 2)])
+def test_grouped_gemm_down_scatter(dev, name, T, bits, tile_rows):
+    L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, 2, T=T, bits=bits)
     R = ids.size
     rng = np.random.default_rng(9)
     act = (rng.standard_normal((R, cfg["I"])) * 3).astype(np.float16)
     cache = O.WeightCache(layer)
     ref = O.grouped_gemm_mode1(act, cache, counts, row0, ts, ws, cfg["T"])
     TL = synth.to_device(L, dev)
-    be, br = gpu_blocks(counts, R, cfg["E"], dev)
+    be, br = gpu_blocks(counts, R, cfg["E"], dev, tile_rows)
     out = torch.zeros(cfg["T"], cfg["H"], dtype=torch.float32, device=dev)
     gp.grouped_gemm(t16(act, dev), TL.w2_trellis, None, TL.w2_svh, None, be, br, t16(counts, dev), t16(row0, dev),
-                    t16(ts, dev), t16(ws, dev), out, 1)
+                    t16(ts, dev), t16(ws, dev), out, 1, tile_rows=tile_rows)
     assert O.rel_l2(out.cpu().numpy(), ref) < 1e-5
 
 
+@pytest.mark.parametrize("tile_rows", [128, 256])
 @pytest.mark.parametrize("name,T", [("tiny", None), ("layer1k", None)])
-def test_grouped_gemm_down_routes_and_combine(dev, name, T):
+def test_grouped_gemm_down_routes_and_combine(dev, name, T, tile_rows):
     L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, 3, T=T)
     R = ids.size
     rng = np.random.default_rng(10)
     act = (rng.standard_normal((R, cfg["I"])) * 3).astype(np.float16)
     ref = O.grouped_gemm_mode1(act, O.WeightCache(layer), counts, row0, ts, ws, cfg["T"])
     TL = synth.to_device(L, dev)
-    be, br = gpu_blocks(counts, R, cfg["E"], dev)
+    be, br = gpu_blocks(counts, R, cfg["E"], dev, tile_rows)
     ri = torch.from_numpy(np.argsort(ids.reshape(-1), kind="stable").astype(np.int32)).to(dev)
     outs = []
     for _ in range(2):
         partial = torch.full((R, cfg["H"]), float("nan"), dtype=torch.float32, device=dev)
         gp.grouped_gemm(t16(act, dev), TL.w2_trellis, None, TL.w2_svh, None, be, br, t16(counts, dev),
-                        t16(row0, dev), None, t16(ws, dev), partial, 2, route_index=ri)
+                        t16(row0, dev), None, t16(ws, dev), partial, 2, route_index=ri, tile_rows=tile_rows)
         assert not torch.isnan(partial).any()                      # every route row written exactly
         out = torch.full((cfg["T"], cfg["H"]), float("nan"), dtype=torch.float32, device=dev)
         gp.combine_routes(partial, out, cfg["topk"], t16(ids, dev), cfg["E"])
@@ -264,6 +273,18 @@ def test_fat_gemm_scatter(dev):
     out = torch.zeros(T, 4096, dtype=torch.float32, device=dev)
     gp.fat_gemm_v2_scatter(t16(a, dev), t16(packed, dev), out, t16(svh, dev), t16(tok, dev), t16(rw, dev), 4, True,
                            False, 1)
+    assert O.rel_l2(out.cpu().numpy(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("M,K", [(300, 64), (300, 192), (300, 320), (10, 4096), (40, 4096), (270, 4096)])
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_fat_gemm_short_k(dev, M, K, bits):
+    """K/32 stages not a multiple of the mainloop's 4-stage trip (tail of 2 stages; K=64 is the tail alone), and
+    row counts that leave waves with <= 16 rows or none (the thin-expert variants) over long K."""
+    a, packed, svh = synth.make_fat(3, M=M, K=K, N=256, bits=bits)
+    ref = O.fat_gemm(a, packed, svh)
+    out = torch.empty(M, 256, dtype=torch.float32, device=dev)
+    gp.fat_gemm_v2(t16(a, dev), t16(packed, dev), out, t16(svh, dev), bits, True, False, 1)
     assert O.rel_l2(out.cpu().numpy(), ref) < 1e-5
 
 

@@ -162,31 +162,32 @@ def test_sort_routes_edges():
         O.sort_routes(np.array([[0, 5]]), np.ones((1, 2), np.float32), 4)
 
 
-def _brute_blocks(counts, max_blocks):
+def _brute_blocks(counts, max_blocks, tile_rows=128):
     be, br = [], []
     row = 0
     for e, c in enumerate(counts):
-        for i in range(math.ceil(c / 128)):
+        for i in range(math.ceil(c / tile_rows)):
             be.append(e)
-            br.append(row + 128 * i)
+            br.append(row + tile_rows * i)
         row += c
     return be, br, len(be), row
 
 
+@pytest.mark.parametrize("tile_rows", [128, 64, 256])
 @pytest.mark.parametrize("seed", range(5))
-def test_build_blocks_brute_force(seed):
+def test_build_blocks_brute_force(seed, tile_rows):
     rng = np.random.default_rng(seed)
     E = int(rng.integers(1, 300))
     counts = rng.integers(0, 700, E).astype(np.int32) * (rng.random(E) < 0.7)
     R = int(counts.sum())
-    for max_blocks in (R // 128 + E, max(1, R // 256)):
-        be, br, meta = O.build_blocks(counts, max_blocks, init=-7)
-        rbe, rbr, nb, nrows = _brute_blocks(counts, max_blocks)
+    for max_blocks in (R // tile_rows + E, max(1, R // 512)):
+        be, br, meta = O.build_blocks(counts, max_blocks, init=-7, tile_rows=tile_rows)
+        rbe, rbr, nb, nrows = _brute_blocks(counts, max_blocks, tile_rows)
         assert meta.tolist() == [nb, nrows]
         m = min(nb, max_blocks)
         assert be[:m].tolist() == rbe[:m] and br[:m].tolist() == rbr[:m]
         assert np.all(be[m:] == -1) and np.all(br[m:] == -7)        # tail expert -1, row0 left unwritten
-    assert nb <= R // 128 + E
+    assert nb <= R // tile_rows + E
 
 
 # ------------------------------------------------------------------------------------------- Hadamard / act
