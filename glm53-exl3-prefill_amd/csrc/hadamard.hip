@@ -1,9 +1,10 @@
 // Row Hadamard passes of the grouped prefill:
 //   row_had (kernel/exl3_grouped_prefill.cu:101-115): dst[r] = fp16(H128(src[tok_r or r] * suh[e_r]) / sqrt(128))
 //   act_had (kernel/exl3_grouped_prefill.cu:118-141): act[r] = fp16(H128(fp16(silu(min(g,L)) * clamp(u,+-L)) * suh_down[e_r]) / sqrt(128))
-// Both are HBM-bound. A lane owns 8 consecutive columns (one 16-byte load and store) of a 128-column block,
-// 16 lanes own a block: 3 butterfly stages run in registers, 4 across lanes (DPP / ds_swizzle), fp32 inside.
-// A wave covers 4 (row, block) pairs per step; workgroups stride over all pairs.
+// Both are HBM-bound. Row-major output: a lane owns 8 consecutive columns (one 16-byte load and store) of a
+// 128-column block, 16 lanes own a block: 3 butterfly stages run in registers, 4 across lanes (DPP / ds_swizzle),
+// fp32 inside; a wave covers 4 (row, block) pairs per step. T16 output (the layout the grouped GEMM reads): see
+// the *_t16 kernels below.
 #include "exl3_common.h"
 
 namespace exl3 {
@@ -117,6 +118,135 @@ void act_had_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ act,
     }
 }
 
+// ---- T16-layout passes. A wave owns one 16-row group x one 128-column block: lane l holds row l & 15 and the 8-column
+// chunks 4 (l >> 4) + i (i = 0..3), so for each i the wave stores whole 256-byte T16 chunks (16 rows x 8 columns)
+// side by side: 1 KB contiguous per store. Column bits 0-2 and 3-4 of the block are in the lane's registers
+// (5 butterfly stages), bits 5 and 6 across lanes l ^ 16 and l ^ 32.
+__device__ __forceinline__ void fwht32_regs(float (&x)[32])
+{
+    #pragma unroll
+    for (int len = 1; len < 32; len <<= 1)
+        #pragma unroll
+        for (int i = 0; i < 32; ++i)
+            if (!(i & len)) { const float a = x[i], b = x[i + len]; x[i] = a + b; x[i + len] = a - b; }
+}
+
+__device__ __forceinline__ void had128_t16(float (&x)[32], int lane)
+{
+    fwht32_regs(x);
+    #pragma unroll
+    for (int i = 0; i < 32; ++i) x[i] = lane_butterfly<16>(x[i], lane);
+    #pragma unroll
+    for (int i = 0; i < 32; i += 2)
+    {
+        auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[i]), __float_as_uint(x[i + 1]), false, false);
+        const float a = __uint_as_float(s1[0]), b = __uint_as_float(s1[1]);
+        auto s2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a + b), __float_as_uint(a - b), false, false);
+        x[i] = __uint_as_float(s2[0]) * HAD_SCALE;
+        x[i + 1] = __uint_as_float(s2[1]) * HAD_SCALE;
+    }
+}
+
+template <bool GATHER>
+__global__ __launch_bounds__(HAD_THREADS)
+void row_had_t16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                        const int64_t* __restrict__ token_sorted, const int32_t* __restrict__ expert_of_row,
+                        const uint16_t* __restrict__ suh, int64_t suh_stride, int64_t rows, int K)
+{
+    const int blocks = K / 128;
+    const int64_t groups = (rows + 15) / 16;
+    const int64_t n_items = groups * blocks;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rl = lane & 15, cq = lane >> 4;
+    for (int64_t it = (int64_t) blockIdx.x * (HAD_THREADS / 64) + wave; it < n_items;
+         it += (int64_t) gridDim.x * (HAD_THREADS / 64))                        // uniform per wave
+    {
+        const int64_t g = it / blocks;
+        const int blk = (int) (it - g * blocks);
+        const int64_t r = min(g * 16 + rl, rows - 1);          // rows past the end recompute the last row, unstored
+        const int64_t srow = GATHER ? token_sorted[r] : r;
+        const int e = expert_of_row[r];
+        float x[32];
+        #pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const int c = blk * 128 + 8 * (4 * cq + i);
+            float xs[8], ss[8];
+            unpack8(*reinterpret_cast<const uint4*>(src + srow * K + c), xs);
+            unpack8(*reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + c), ss);
+            #pragma unroll
+            for (int j = 0; j < 8; ++j) x[8 * i + j] = xs[j] * ss[j];
+        }
+        had128_t16(x, lane);
+        if (g * 16 + rl < rows)
+            #pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                float o[8];
+                #pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = x[8 * i + j];
+                const int64_t chunk = g * (K / 8) + blk * 16 + 4 * cq + i;
+                *reinterpret_cast<uint4*>(dst + chunk * 128 + rl * 8) = pack8(o);
+            }
+    }
+}
+
+__global__ __launch_bounds__(HAD_THREADS)
+void act_had_t16_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ act,
+                        const int32_t* __restrict__ expert_of_row, const uint16_t* __restrict__ suh,
+                        int64_t suh_stride, int64_t rows, int I, float limit)
+{
+    const int blocks = I / 128;
+    const int64_t groups = (rows + 15) / 16;
+    const int64_t n_items = groups * blocks;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rl = lane & 15, cq = lane >> 4;
+    for (int64_t it = (int64_t) blockIdx.x * (HAD_THREADS / 64) + wave; it < n_items;
+         it += (int64_t) gridDim.x * (HAD_THREADS / 64))
+    {
+        const int64_t g = it / blocks;
+        const int blk = (int) (it - g * blocks);
+        const int64_t r = min(g * 16 + rl, rows - 1);
+        const int e = expert_of_row[r];
+        float x[32];
+        #pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const int c = blk * 128 + 8 * (4 * cq + i);
+            float gs[8], us[8], ss[8];
+            unpack8(*reinterpret_cast<const uint4*>(gu + r * (2 * (int64_t) I) + c), gs);
+            unpack8(*reinterpret_cast<const uint4*>(gu + r * (2 * (int64_t) I) + I + c), us);
+            unpack8(*reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + c), ss);
+            #pragma unroll
+            for (int j = 0; j < 8; ++j)
+            {
+                const float gc = fminf(gs[j], limit);
+                const float uc = fminf(fmaxf(us[j], -limit), limit);
+                const float a = gc / (1.0f + __expf(-gc)) * uc;
+                x[8 * i + j] = h2f(f2h(a)) * ss[j];                 // fp16 rounding point of the reference
+            }
+        }
+        had128_t16(x, lane);
+        if (g * 16 + rl < rows)
+            #pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                float o[8];
+                #pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = x[8 * i + j];
+                const int64_t chunk = g * (I / 8) + blk * 16 + 4 * cq + i;
+                *reinterpret_cast<uint4*>(act + chunk * 128 + rl * 8) = pack8(o);
+            }
+    }
+}
+
+unsigned t16_grid(int64_t rows, int width)
+{
+    const int64_t items = (rows + 15) / 16 * (width / 128);
+    const int64_t wgs = (items + HAD_THREADS / 64 - 1) / (HAD_THREADS / 64);
+    return (unsigned) (wgs < 16384 ? wgs : 16384);
+}
+
 unsigned had_grid(int64_t n_pairs)
 {
     const int64_t wgs = (n_pairs + PAIRS_PER_WG - 1) / PAIRS_PER_WG;
@@ -128,35 +258,68 @@ unsigned had_grid(int64_t n_pairs)
 
 using namespace exl3;
 
-extern "C" int exl3_row_had(const uint16_t* src, uint16_t* dst, const int64_t* token_sorted, const int32_t* expert_of_row,
-                            const uint16_t* suh, int64_t suh_stride, int64_t suh_len, int64_t rows, int K, int gather,
-                            void* stream)
+extern "C" int exl3_row_had_ex(const uint16_t* src, uint16_t* dst, const int64_t* token_sorted,
+                               const int32_t* expert_of_row, const uint16_t* suh, int64_t suh_stride, int64_t suh_len,
+                               int64_t rows, int K, int gather, int dst_layout, void* stream)
 {
     EXL3_CHECK(K > 0 && K % 128 == 0 && suh_len == K, "K must be a multiple of 128 and match suh");
     EXL3_CHECK(rows >= 0, "bad row count");
+    EXL3_CHECK(dst_layout == EXL3_LAYOUT_ROWS || dst_layout == EXL3_LAYOUT_T16, "unknown layout");
     if (rows == 0) return EXL3_OK;
     EXL3_CHECK(src && dst && expert_of_row && suh && (!gather || token_sorted), "null pointer");
     EXL3_CHECK(((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(suh)) & 15) == 0
                && suh_stride % 8 == 0, "src/dst/suh must be 16-byte aligned");
     const unsigned grid = had_grid(rows * (K / 128));
     hipStream_t s = as_stream(stream);
-    if (gather)
+    if (dst_layout == EXL3_LAYOUT_T16)
+    {
+        const unsigned g16 = t16_grid(rows, K);
+        if (gather)
+            row_had_t16_kernel<true><<<g16, HAD_THREADS, 0, s>>>(src, dst, token_sorted, expert_of_row, suh, suh_stride,
+                                                                 rows, K);
+        else
+            row_had_t16_kernel<false><<<g16, HAD_THREADS, 0, s>>>(src, dst, nullptr, expert_of_row, suh, suh_stride,
+                                                                  rows, K);
+    }
+    else if (gather)
         row_had_kernel<true><<<grid, HAD_THREADS, 0, s>>>(src, dst, token_sorted, expert_of_row, suh, suh_stride, rows, K);
     else
         row_had_kernel<false><<<grid, HAD_THREADS, 0, s>>>(src, dst, nullptr, expert_of_row, suh, suh_stride, rows, K);
     return hip_status("row_had");
 }
 
-extern "C" int exl3_act_had(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
-                            const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, void* stream)
+extern "C" int exl3_row_had(const uint16_t* src, uint16_t* dst, const int64_t* token_sorted, const int32_t* expert_of_row,
+                            const uint16_t* suh, int64_t suh_stride, int64_t suh_len, int64_t rows, int K, int gather,
+                            void* stream)
+{
+    return exl3_row_had_ex(src, dst, token_sorted, expert_of_row, suh, suh_stride, suh_len, rows, K, gather,
+                           EXL3_LAYOUT_ROWS, stream);
+}
+
+extern "C" int exl3_act_had_ex(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
+                               const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit,
+                               int dst_layout, void* stream)
 {
     EXL3_CHECK(I > 0 && gu_width == 2 * (int64_t) I && I % 128 == 0, "gate|up width must be 2I, I multiple of 128");
     EXL3_CHECK(rows >= 0, "bad row count");
+    EXL3_CHECK(dst_layout == EXL3_LAYOUT_ROWS || dst_layout == EXL3_LAYOUT_T16, "unknown layout");
     if (rows == 0) return EXL3_OK;
     EXL3_CHECK(gu && act && expert_of_row && suh_down, "null pointer");
     EXL3_CHECK(((reinterpret_cast<uintptr_t>(gu) | reinterpret_cast<uintptr_t>(act) | reinterpret_cast<uintptr_t>(suh_down)) & 15) == 0
                && suh_stride % 8 == 0, "gu/act/suh must be 16-byte aligned");
-    act_had_kernel<<<had_grid(rows * (I / 128)), HAD_THREADS, 0, as_stream(stream)>>>(gu, act, expert_of_row, suh_down,
-                                                                                      suh_stride, rows, I, limit);
+    if (dst_layout == EXL3_LAYOUT_T16)
+        act_had_t16_kernel<<<t16_grid(rows, I), HAD_THREADS, 0, as_stream(stream)>>>(gu, act, expert_of_row, suh_down,
+                                                                                     suh_stride, rows, I, limit);
+    else
+        act_had_kernel<<<had_grid(rows * (I / 128)), HAD_THREADS, 0, as_stream(stream)>>>(gu, act, expert_of_row,
+                                                                                          suh_down, suh_stride, rows, I,
+                                                                                          limit);
     return hip_status("act_had");
+}
+
+extern "C" int exl3_act_had(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
+                            const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, void* stream)
+{
+    return exl3_act_had_ex(gu, gu_width, act, expert_of_row, suh_down, suh_stride, rows, I, limit, EXL3_LAYOUT_ROWS,
+                           stream);
 }

@@ -59,8 +59,9 @@ enum { MODE_STORE_F16 = 0, MODE_SCATTER_F32 = 1, MODE_STORE_F32 = 2, MODE_STORE_
 
 struct GemmParams
 {
-    const uint16_t* a;             // [a_rows, size_k] fp16
+    const uint16_t* a;             // [a_rows, size_k] fp16, row-major or T16 (a_t16)
     int64_t a_rows;
+    int a_t16;
     int size_k;
     const uint16_t* packed0;       // trellis of tensor 0 (gate / single tensor)
     const uint16_t* packed1;       // trellis of tensor 1 (up), may be null
@@ -124,7 +125,10 @@ __device__ __forceinline__ uint32_t prev_in_row(uint32_t v)
 }
 
 template <int BITS, int MODE, bool DENSE>
-__global__ __launch_bounds__(GEMM_THREADS, 2)
+#ifndef EXL3_GEMM_OCC
+#define EXL3_GEMM_OCC 2
+#endif
+__global__ __launch_bounds__(GEMM_THREADS, EXL3_GEMM_OCC)
 void trellis_gemm_kernel(const GemmParams p)
 {
     constexpr int LDS_BYTES = (MODE == MODE_SCATTER_F32 && LDS_SCATTER_BYTES > LDS_MAIN_BYTES) ? LDS_SCATTER_BYTES
@@ -194,12 +198,16 @@ void trellis_gemm_kernel(const GemmParams p)
     // 4 (l >> 4) .. + 3 of the 16 x 16 output. An activation load is 16 rows x 64 contiguous bytes.
     const int tok = lane & 15, kq = lane >> 4;
     const int rows_w = rows_valid - 64 * wave;            // valid rows of this wave (uniform)
+    // Row-major A: lane l reads 16 bytes of row l & 15 (16 rows per load, one lane per cycle in the address unit).
+    // T16 A: the same operand is 256 contiguous bytes per 16-row group (one coalesced 1 KB load when aligned).
     const uint16_t* a_ptr[4];
+    const int a_step = p.a_t16 ? 4 * 128 : TILE_K;          // halves per stage
     #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
     {
-        const int r = min(64 * wave + 16 * mb + tok, rows_valid - 1);
-        a_ptr[mb] = p.a + (int64_t) (row0 + r) * p.size_k + 8 * kq;
+        const int64_t row = row0 + min(64 * wave + 16 * mb + tok, rows_valid - 1);
+        a_ptr[mb] = p.a_t16 ? p.a + ((((row >> 4) * (p.size_k >> 3) + kq) << 7) + ((row & 15) << 3))
+                            : p.a + row * p.size_k + 8 * kq;
     }
     const int wread = tok * LDS_ROW + 8 * kq;
 
@@ -263,7 +271,7 @@ void trellis_gemm_kernel(const GemmParams p)
         uint32_t raw[RAW_DEPTH][NR];
         half8_t act[ACT_DEPTH][4];
         auto load_act = [&](int kb, half8_t (&a)[4]) {
-            const int k0 = min(kb, num_kb - 1) * TILE_K;
+            const int64_t k0 = (int64_t) min(kb, num_kb - 1) * a_step;
             #pragma unroll
             for (int mb = 0; mb < MBA; ++mb) a[mb] = *reinterpret_cast<const half8_t*>(a_ptr[mb] + k0);
         };
@@ -292,6 +300,9 @@ void trellis_gemm_kernel(const GemmParams p)
                 {
                     #pragma unroll
                     for (int nb = 0; nb < 8; ++nb) w[nb] = *reinterpret_cast<const half8_t*>(lds_s + nb * LDS_BLK + wread);
+#ifdef EXL3_SCHED_READS_FIRST
+                    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);      // all fragment reads first
+#endif
                 }
                 Chunk4 c0, c1;
                 decode2(raw[(u + 1) % RAW_DEPTH], c0, c1);      // stage s + 1
@@ -520,17 +531,18 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15)
 
 using namespace exl3;
 
-extern "C" int exl3_grouped_gemm_tiles(const uint16_t* a, int64_t a_rows, int size_k,
-                                       const uint16_t* packed_gate, const uint16_t* packed_up,
-                                       int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
-                                       const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
-                                       const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
-                                       int tile_rows, const int32_t* counts, const int32_t* expert_row0,
-                                       int n_experts, const int64_t* token_sorted, const uint16_t* route_weight,
-                                       const int32_t* route_index, void* out, int64_t out_rows, int mode,
-                                       void* stream)
+extern "C" int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,
+                                    const uint16_t* packed_gate, const uint16_t* packed_up,
+                                    int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
+                                    const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                                    const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
+                                    int tile_rows, const int32_t* counts, const int32_t* expert_row0,
+                                    int n_experts, const int64_t* token_sorted, const uint16_t* route_weight,
+                                    const int32_t* route_index, void* out, int64_t out_rows, int mode,
+                                    void* stream)
 {
     EXL3_CHECK(tile_rows == 128 || tile_rows == TILE_M, "tile_rows must be 128 or %d", TILE_M);
+    EXL3_CHECK(a_layout == EXL3_LAYOUT_ROWS || a_layout == EXL3_LAYOUT_T16, "unknown layout");
     EXL3_CHECK(bits >= 2 && bits <= 4, "unsupported bits %d (2, 3 or 4)", bits);
     EXL3_CHECK(size_k == tiles_k * 16 && size_k % 64 == 0 && size_k > 0, "K mismatch");
     const int size_n_each = tiles_n * 16;
@@ -550,7 +562,7 @@ extern "C" int exl3_grouped_gemm_tiles(const uint16_t* a, int64_t a_rows, int si
                svh_stride % 4 == 0, "svh must be 8-byte aligned");
     const int n_tensors = packed_up ? 2 : 1;
     GemmParams p{};
-    p.a = a; p.a_rows = a_rows; p.size_k = size_k;
+    p.a = a; p.a_rows = a_rows; p.size_k = size_k; p.a_t16 = a_layout == EXL3_LAYOUT_T16;
     p.packed0 = packed_gate; p.packed1 = packed_up; p.expert_stride_words = expert_stride_words;
     p.tiles_n = tiles_n; p.svh0 = svh_gate; p.svh1 = svh_up; p.svh_stride = svh_stride;
     p.block_expert = block_expert; p.block_row0 = block_row0; p.counts = counts; p.expert_row0 = expert_row0;
@@ -596,10 +608,10 @@ extern "C" int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
                                  const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
                                  void* out, int64_t out_rows, int mode, void* stream)
 {
-    return exl3_grouped_gemm_tiles(a, a_rows, size_k, packed_gate, packed_up, expert_stride_words, tiles_k, tiles_n,
-                                   bits, svh_gate, svh_up, svh_stride, block_expert, block_row0, max_blocks, 128,
-                                   counts, expert_row0, n_experts, token_sorted, route_weight, route_index, out,
-                                   out_rows, mode, stream);
+    return exl3_grouped_gemm_ex(a, a_rows, size_k, EXL3_LAYOUT_ROWS, packed_gate, packed_up, expert_stride_words,
+                                tiles_k, tiles_n, bits, svh_gate, svh_up, svh_stride, block_expert, block_row0,
+                                max_blocks, 128, counts, expert_row0, n_experts, token_sorted, route_weight,
+                                route_index, out, out_rows, mode, stream);
 }
 
 namespace {

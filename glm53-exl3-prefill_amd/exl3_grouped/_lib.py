@@ -16,6 +16,7 @@ EXL3_ERR_ARG = 1
 EXL3_ERR_HIP = 2
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_I32, DTYPE_I64 = 0, 1, 2, 3, 4
+LAYOUT_ROWS, LAYOUT_T16 = 0, 1
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int
@@ -32,11 +33,13 @@ SIGNATURES = {
     "exl3_build_blocks": (I32, [P, I32, I32, P, P, P, P]),
     "exl3_build_tiles": (I32, [P, I32, I32, I32, P, P, P, P]),
     "exl3_row_had": (I32, [P, P, P, P, P, I64, I64, I64, I32, I32, P]),
+    "exl3_row_had_ex": (I32, [P, P, P, P, P, I64, I64, I64, I32, I32, I32, P]),
     "exl3_act_had": (I32, [P, I64, P, P, P, I64, I64, I32, F32, P]),
+    "exl3_act_had_ex": (I32, [P, I64, P, P, P, I64, I64, I32, F32, I32, P]),
     "exl3_grouped_gemm": (I32, [P, I64, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, P, P, I32, P, P,
                                 P, P, I64, I32, P]),
-    "exl3_grouped_gemm_tiles": (I32, [P, I64, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, I32, P, P, I32,
-                                      P, P, P, P, I64, I32, P]),
+    "exl3_grouped_gemm_ex": (I32, [P, I64, I32, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, I32, P, P,
+                                   I32, P, P, P, P, I64, I32, P]),
     "exl3_combine_routes": (I32, [P, P, P, I32, I32, I64, I32, I64, P]),
     "exl3_fat_gemm": (I32, [P, I64, I32, P, I32, I32, I32, P, I64, P, I64, I32, I32, I32, I32, P]),
     "exl3_fat_gemm_scatter": (I32, [P, I64, I32, P, I32, I32, I32, P, I64, P, I64, P, P, I32, I32, I32, I32, P]),
@@ -45,7 +48,7 @@ SIGNATURES = {
     "exl3_decode_states": (I32, [P, P, I64, P]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 _path = None

@@ -125,10 +125,21 @@ def build_tiles(counts: torch.Tensor, tile_expert: torch.Tensor, tile_row0: torc
 
 
 # ------------------------------------------------------------------------------------------- Hadamard passes
+def t16_rows(rows: int) -> int:
+    """Rows a T16-layout buffer of `rows` logical rows holds (whole 16-row groups)."""
+    return (rows + 15) // 16 * 16
+
+
 def row_had(src: torch.Tensor, dst: torch.Tensor, token_sorted: Optional[torch.Tensor], expert_of_row: torch.Tensor,
-            suh: torch.Tensor, gather: bool) -> None:
-    """kernel/exl3_grouped_prefill.cu:297-311."""
-    rows, K = dst.shape
+            suh: torch.Tensor, gather: bool, dst_layout: int = 0, rows: Optional[int] = None) -> None:
+    """kernel/exl3_grouped_prefill.cu:297-311. dst_layout (new): 0 row-major dst [rows, K]; 1 the T16 layout the
+    grouped GEMM reads (dst holds t16_rows(rows) rows; `rows` gives the logical row count)."""
+    K = dst.shape[1]
+    if dst_layout == 0:
+        rows = dst.shape[0]
+    else:
+        _check(dst_layout == 1 and rows is not None and dst.shape[0] >= t16_rows(rows),
+               "T16 dst needs rows= and t16_rows(rows) rows")
     _check(K % 128 == 0 and suh.size(-1) == K, "K must be a multiple of 128 and match suh")
     _check(src.dtype == torch.float16 and dst.dtype == torch.float16 and suh.dtype == torch.float16,
            "fp16 tensors")
@@ -143,14 +154,20 @@ def row_had(src: torch.Tensor, dst: torch.Tensor, token_sorted: Optional[torch.T
         _check(src.size(0) >= rows, "src has too few rows")
     dev = _require_cuda(src, dst, expert_of_row, suh, token_sorted if gather else None)
     with _On(dev) as s:
-        _lib.call("exl3_row_had", _p(src), _p(dst), _p(token_sorted) if gather else None, _p(expert_of_row),
-                  _p(suh), suh.stride(0), suh.size(-1), rows, K, 1 if gather else 0, s)
+        _lib.call("exl3_row_had_ex", _p(src), _p(dst), _p(token_sorted) if gather else None, _p(expert_of_row),
+                  _p(suh), suh.stride(0), suh.size(-1), rows, K, 1 if gather else 0, int(dst_layout), s)
 
 
 def act_had(gu: torch.Tensor, act: torch.Tensor, expert_of_row: torch.Tensor, suh_down: torch.Tensor,
-            limit: float) -> None:
-    """kernel/exl3_grouped_prefill.cu:313-322."""
-    rows, I = act.shape
+            limit: float, dst_layout: int = 0) -> None:
+    """kernel/exl3_grouped_prefill.cu:313-322. dst_layout (new): 0 row-major act [rows, I]; 1 T16 (rows = gu rows,
+    act holds t16_rows(rows) rows)."""
+    I = act.shape[1]
+    if dst_layout == 0:
+        rows = act.shape[0]
+    else:
+        rows = gu.shape[0]
+        _check(dst_layout == 1 and act.shape[0] >= t16_rows(rows), "T16 act needs t16_rows(rows) rows")
     _check(gu.size(1) == 2 * I and I % 128 == 0, "gate|up width must be 2I, I multiple of 128")
     _check(gu.dtype == torch.float16 and act.dtype == torch.float16 and suh_down.dtype == torch.float16,
            "fp16 tensors")
@@ -159,8 +176,8 @@ def act_had(gu: torch.Tensor, act: torch.Tensor, expert_of_row: torch.Tensor, su
     _check(expert_of_row.dtype == torch.int32 and expert_of_row.numel() >= rows, "expert_of_row int32 [rows]")
     dev = _require_cuda(gu, act, expert_of_row, suh_down)
     with _On(dev) as s:
-        _lib.call("exl3_act_had", _p(gu), gu.size(1), _p(act), _p(expert_of_row), _p(suh_down), suh_down.stride(0),
-                  rows, I, float(limit), s)
+        _lib.call("exl3_act_had_ex", _p(gu), gu.size(1), _p(act), _p(expert_of_row), _p(suh_down),
+                  suh_down.stride(0), rows, I, float(limit), int(dst_layout), s)
 
 
 # ------------------------------------------------------------------------------------------- grouped GEMM
@@ -168,12 +185,18 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
                  svh_gate: torch.Tensor, svh_up: Optional[torch.Tensor], block_expert: torch.Tensor,
                  block_row0: torch.Tensor, counts: torch.Tensor, expert_row0: torch.Tensor,
                  token_sorted: Optional[torch.Tensor], route_weight: Optional[torch.Tensor], out: torch.Tensor,
-                 mode: int, route_index: Optional[torch.Tensor] = None, tile_rows: int = 128) -> None:
+                 mode: int, route_index: Optional[torch.Tensor] = None, tile_rows: int = 128, a_layout: int = 0,
+                 a_rows: Optional[int] = None) -> None:
     """kernel/exl3_grouped_prefill.cu:326-378. mode 0: fp16 store; mode 1: fp32 atomic scatter into
     out[token_sorted[r]]; mode 2 (new): fp32 store of the weighted row into out[route_index[r]] (out [T*topk, N]),
     summed per token by combine_routes in a fixed order. tile_rows (new): rows per block-table entry, 128 for
-    build_blocks' table (the reference's), 256 for a build_tiles(..., 256) table."""
+    build_blocks' table (the reference's), 256 for a build_tiles(..., 256) table. a_layout (new): 0 row-major a,
+    1 T16 (a from row_had / act_had with dst_layout=1; a_rows gives its logical rows)."""
     _check(int(tile_rows) in (128, 256), "tile_rows must be 128 or 256")
+    _check(a_layout in (0, 1), "unknown layout")
+    if a_rows is None:
+        a_rows = a.size(0)
+    _check(a_layout == 0 or a.size(0) >= t16_rows(a_rows), "T16 a needs t16_rows(a_rows) rows")
     _check(a.dtype == torch.float16 and a.is_contiguous(), "a fp16 contiguous")
     _check(packed_gate.dim() == 4 and packed_gate.dtype in (torch.int16, torch.uint16) and
            packed_gate.stride(3) == 1 and packed_gate.stride(2) == packed_gate.size(3) and
@@ -202,7 +225,7 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
     max_blocks = block_expert.numel()
     if mode == 0:
         _check(out.dtype == torch.float16 and out.dim() == 2 and out.size(1) == n_tensors * size_n_each and
-               out.is_contiguous() and out.size(0) >= a.size(0), "mode 0: out fp16 [rows, n_tensors*N]")
+               out.is_contiguous() and out.size(0) >= a_rows, "mode 0: out fp16 [rows, n_tensors*N]")
     elif mode == 1:
         _check(out.dtype == torch.float32 and out.dim() == 2 and out.size(1) == size_n_each and n_tensors == 1 and
                out.is_contiguous(), "mode 1: out fp32 [T, N], single tensor")
@@ -219,7 +242,7 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
                         expert_row0, out, token_sorted if mode == 1 else None, route_weight if mode else None,
                         route_index if mode == 2 else None)
     with _On(dev) as s:
-        _lib.call("exl3_grouped_gemm_tiles", _p(a), a.size(0), size_k, _p(packed_gate), _p(packed_up),
+        _lib.call("exl3_grouped_gemm_ex", _p(a), int(a_rows), size_k, int(a_layout), _p(packed_gate), _p(packed_up),
                   expert_stride, tiles_k, tiles_n, bits, _p(svh_gate), _p(svh_up), svh_stride, _p(block_expert),
                   _p(block_row0), max_blocks, int(tile_rows), _p(counts), _p(expert_row0), E,
                   _p(token_sorted) if mode == 1 else None,

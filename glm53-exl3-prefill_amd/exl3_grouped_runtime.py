@@ -96,29 +96,30 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     meta = torch.zeros(2, dtype=torch.int32, device=dev)
     gp.build_tiles(counts, block_expert, block_row0, meta, TILE_ROWS)
     mark("build_blocks")
-    h13 = torch.empty(R, K, dtype=torch.float16, device=dev)
-    gp.row_had(x16, h13, token_sorted, expert_of_row, layer.w13_suh[:, 0], True)
+    # the GEMMs' activation operands (h13, act) are written in the T16 layout, which makes their loads contiguous
+    h13 = torch.empty(gp.t16_rows(R), K, dtype=torch.float16, device=dev)
+    gp.row_had(x16, h13, token_sorted, expert_of_row, layer.w13_suh[:, 0], True, dst_layout=1, rows=R)
     mark("row_had")
     gu = torch.empty(R, 2 * I, dtype=torch.float16, device=dev)
     gp.grouped_gemm(h13, layer.w13_trellis[:, 0], layer.w13_trellis[:, 1], layer.w13_svh[:, 0], layer.w13_svh[:, 1],
                     block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 0,
-                    tile_rows=TILE_ROWS)
+                    tile_rows=TILE_ROWS, a_layout=1, a_rows=R)
     mark("gemm_gate_up")
-    act = torch.empty(R, I, dtype=torch.float16, device=dev)
-    gp.act_had(gu, act, expert_of_row, layer.w2_suh, float(limit))
+    act = torch.empty(gp.t16_rows(R), I, dtype=torch.float16, device=dev)
+    gp.act_had(gu, act, expert_of_row, layer.w2_suh, float(limit), dst_layout=1)
     mark("act_had")
     if scatter == "atomic":
         out = torch.zeros(T, K, dtype=torch.float32, device=dev)
         mark("zero_out")
         gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
                         block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, out, 1,
-                        tile_rows=TILE_ROWS)
+                        tile_rows=TILE_ROWS, a_layout=1, a_rows=R)
         mark("gemm_down_scatter")
         return out
     partial = torch.empty(R, K, dtype=torch.float32, device=dev)
     gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
                     block_expert, block_row0, counts, expert_row0, None, weight_sorted, partial, 2,
-                    route_index=route_index, tile_rows=TILE_ROWS)
+                    route_index=route_index, tile_rows=TILE_ROWS, a_layout=1, a_rows=R)
     mark("gemm_down_routes")
     out = torch.empty(T, K, dtype=torch.float32, device=dev)
     gp.combine_routes(partial, out, topk, ids, E)

@@ -37,6 +37,11 @@ extern "C" {
 #define EXL3_DTYPE_I32 3
 #define EXL3_DTYPE_I64 4
 
+#define EXL3_LAYOUT_ROWS 0           /* fp16 [rows, width] row-major */
+#define EXL3_LAYOUT_T16 1            /* fp16 [ceil(rows/16)*16, width] in 16-row groups: element (r, c) at
+                                        (((r/16) * (width/8) + c/8) * 16 + r%16) * 8 + c%8; the grouped GEMM's
+                                        activation operand loads are then contiguous */
+
 #define EXL3_GEMM_STORE_F16 0      /* grouped_gemm mode 0: fp16 store into [rows, n_tensors*N] */
 #define EXL3_GEMM_SCATTER_F32 1    /* grouped_gemm mode 1: fp32 atomic add into out[token_sorted[r]] * w[r] */
 #define EXL3_GEMM_STORE_ROUTE_F32 2 /* grouped_gemm mode 2: fp32 store of w[r] * y[r] into out[route_index[r]] */
@@ -93,6 +98,10 @@ int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_rows, int ma
 int exl3_row_had(const uint16_t* src, uint16_t* dst, const int64_t* token_sorted, const int32_t* expert_of_row,
                  const uint16_t* suh, int64_t suh_stride, int64_t suh_len, int64_t rows, int K, int gather,
                  void* stream);
+/* exl3_row_had with the destination in layout dst_layout (EXL3_LAYOUT_ROWS or EXL3_LAYOUT_T16). New. */
+int exl3_row_had_ex(const uint16_t* src, uint16_t* dst, const int64_t* token_sorted, const int32_t* expert_of_row,
+                    const uint16_t* suh, int64_t suh_stride, int64_t suh_len, int64_t rows, int K, int gather,
+                    int dst_layout, void* stream);
 
 /*
  * Clamped SwiGLU + down Hadamard (pybind op act_had, kernel/exl3_grouped_prefill.cu:118-141 and :313-322):
@@ -102,6 +111,10 @@ int exl3_row_had(const uint16_t* src, uint16_t* dst, const int64_t* token_sorted
  */
 int exl3_act_had(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
                  const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, void* stream);
+/* exl3_act_had with act in layout dst_layout (EXL3_LAYOUT_ROWS or EXL3_LAYOUT_T16). New. */
+int exl3_act_had_ex(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
+                    const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, int dst_layout,
+                    void* stream);
 
 /*
  * Grouped weight-stationary trellis GEMM over all experts (pybind op grouped_gemm,
@@ -132,17 +145,18 @@ int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
                       void* out, int64_t out_rows, int mode, void* stream);
 
 /*
- * exl3_grouped_gemm over a row-tile table of `tile_rows` rows per entry (128: the reference's block table, what
- * exl3_grouped_gemm passes; 256: a table from exl3_build_tiles(..., 256, ...)). Same modes and outputs.
+ * exl3_grouped_gemm with two extensions (new): a_layout (EXL3_LAYOUT_ROWS, or EXL3_LAYOUT_T16 for an `a` written by
+ * the _ex Hadamard passes) and tile_rows, the rows per block-table entry (128: the reference's build_blocks table,
+ * what exl3_grouped_gemm passes; 256: a table from exl3_build_tiles(..., 256, ...)). Same modes and outputs.
  */
-int exl3_grouped_gemm_tiles(const uint16_t* a, int64_t a_rows, int size_k,
-                            const uint16_t* packed_gate, const uint16_t* packed_up, int64_t expert_stride_words,
-                            int tiles_k, int tiles_n, int bits,
-                            const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
-                            const int32_t* block_expert, const int32_t* block_row0, int max_blocks, int tile_rows,
-                            const int32_t* counts, const int32_t* expert_row0, int n_experts,
-                            const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
-                            void* out, int64_t out_rows, int mode, void* stream);
+int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,
+                         const uint16_t* packed_gate, const uint16_t* packed_up, int64_t expert_stride_words,
+                         int tiles_k, int tiles_n, int bits,
+                         const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                         const int32_t* block_expert, const int32_t* block_row0, int max_blocks, int tile_rows,
+                         const int32_t* counts, const int32_t* expert_row0, int n_experts,
+                         const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
+                         void* out, int64_t out_rows, int mode, void* stream);
 
 /*
  * Deterministic route combine (new; pairs with grouped_gemm mode 2): out[t, :] = sum_{j < topk} partial[t*topk + j, :]

@@ -37,6 +37,20 @@ def within_f16_steps(got, ref, steps=1, frac=0.999):
     return ok.mean() >= frac
 
 
+def to_t16(a):
+    """Row-major [R, W] -> the T16 layout as a [t16_rows(R), W] array (include/exl3_grouped.h EXL3_LAYOUT_T16)."""
+    R, W = a.shape
+    Rp = (R + 15) // 16 * 16
+    pad = np.zeros((Rp, W), a.dtype)
+    pad[:R] = a
+    return pad.reshape(Rp // 16, 16, W // 8, 8).transpose(0, 2, 1, 3).reshape(Rp, W)
+
+
+def from_t16(t, R):
+    Rp, W = t.shape
+    return t.reshape(Rp // 16, W // 8, 16, 8).transpose(0, 2, 1, 3).reshape(Rp, W)[:R]
+
+
 # ------------------------------------------------------------------------------------------- decode
 def test_decode_states_all_65536_bit_exact(dev):
     states = torch.arange(65536, dtype=torch.int32).to(torch.int16).to(dev)
@@ -142,6 +156,10 @@ def test_row_had(dev, gather):
     ref = O.row_had(x, tok if gather else None, eor, suh2[:, 0], gather)
     got = dst.cpu().numpy()
     assert O.rel_l2(got, ref) < 1e-4 and within_f16_steps(got, ref)
+    dst16 = torch.full((gp.t16_rows(R), H), float("nan"), dtype=torch.float16, device=dev)
+    gp.row_had(t16(x, dev), dst16, t16(tok, dev) if gather else None, t16(eor, dev), suh_t[:, 0], gather, dst_layout=1,
+               rows=R)
+    assert np.array_equal(from_t16(dst16.cpu().numpy(), R).view(np.uint16), got.view(np.uint16))     # same values, T16
 
 
 @pytest.mark.parametrize("scale", [1.0, 12.0])
@@ -155,6 +173,9 @@ def test_act_had(dev, scale):
     gp.act_had(t16(gu, dev), act, t16(eor, dev), t16(suh, dev), LIMIT)
     ref = O.act_had(gu, eor, suh, LIMIT)
     got = act.cpu().numpy()
+    act16 = torch.full((gp.t16_rows(R), I), float("nan"), dtype=torch.float16, device=dev)
+    gp.act_had(t16(gu, dev), act16, t16(eor, dev), t16(suh, dev), LIMIT, dst_layout=1)
+    assert np.array_equal(from_t16(act16.cpu().numpy(), R).view(np.uint16), got.view(np.uint16))
     # fp16 rounding of the SwiGLU output can land one step apart (fast exp vs libm exp) before the Hadamard
     assert O.rel_l2(got, ref) < 1e-3 and within_f16_steps(got, ref, steps=2, frac=0.99)
 
@@ -192,6 +213,11 @@ def test_grouped_gemm_gate_up(dev, name, T, bits, tile_rows):
                     be, br, t16(counts, dev), t16(row0, dev), None, None, gu, 0, tile_rows=tile_rows)
     got = gu.cpu().numpy()
     assert O.rel_l2(got, ref) < 1e-4 and within_f16_steps(got, ref)
+    gu16 = torch.empty_like(gu)
+    gp.grouped_gemm(t16(to_t16(h13), dev), TL.w13_trellis[:, 0], TL.w13_trellis[:, 1], TL.w13_svh[:, 0],
+                    TL.w13_svh[:, 1], be, br, t16(counts, dev), t16(row0, dev), None, None, gu16, 0, tile_rows=tile_rows,
+                    a_layout=1, a_rows=R)
+    assert torch.equal(gu16, gu)                                  # T16 activations: identical arithmetic
 
 
 @pytest.mark.parametrize("tile_rows", [128, 256])
@@ -210,6 +236,10 @@ def test_grouped_gemm_down_scatter(dev, name, T, bits, tile_rows):
     gp.grouped_gemm(t16(act, dev), TL.w2_trellis, None, TL.w2_svh, None, be, br, t16(counts, dev), t16(row0, dev),
                     t16(ts, dev), t16(ws, dev), out, 1, tile_rows=tile_rows)
     assert O.rel_l2(out.cpu().numpy(), ref) < 1e-5
+    out16 = torch.zeros_like(out)
+    gp.grouped_gemm(t16(to_t16(act), dev), TL.w2_trellis, None, TL.w2_svh, None, be, br, t16(counts, dev),
+                    t16(row0, dev), t16(ts, dev), t16(ws, dev), out16, 1, tile_rows=tile_rows, a_layout=1, a_rows=R)
+    assert O.rel_l2(out16.cpu().numpy(), ref) < 1e-5
 
 
 @pytest.mark.parametrize("tile_rows", [128, 256])
