@@ -124,95 +124,84 @@ __device__ __forceinline__ uint32_t prev_in_row(uint32_t v)
     return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, 0x121, 0xF, 0xF, false);     // row_ror:1
 }
 
-template <int BITS, int MODE, bool DENSE>
-#ifndef EXL3_GEMM_OCC
-#define EXL3_GEMM_OCC 2
-#endif
-__global__ __launch_bounds__(GEMM_THREADS, EXL3_GEMM_OCC)
-void trellis_gemm_kernel(const GemmParams p)
+// ------------------------------------------------------------------------------------------- workgroup tile
+// The rows (of one expert), tensor and 128-column tile one workgroup computes.
+struct Tile
 {
-    constexpr int LDS_BYTES = (MODE == MODE_SCATTER_F32 && LDS_SCATTER_BYTES > LDS_MAIN_BYTES) ? LDS_SCATTER_BYTES
-                                                                                              : LDS_MAIN_BYTES;
-    __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
-    uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
+    int e, row0, rows_valid, which, nt;
+    const uint32_t* packed;        // the tensor's trellis for expert e
+    const uint16_t* svh;           // svh of the tile's 128 output columns
+};
 
-    int group, slot;
-    xcd_group_slot((int) blockIdx.x, p.n_slots, group, slot);
-    int e, row0, rows_valid;
-    if (group >= p.n_groups) return;
+template <bool DENSE>
+__device__ __forceinline__ bool resolve_tile(const GemmParams& p, int group, int slot, Tile& t)
+{
+    if (group >= p.n_groups) return false;
     if constexpr (DENSE)
     {
-        e = 0;
-        row0 = group * TILE_M;
-        rows_valid = (int) min((int64_t) TILE_M, p.m - row0);
+        t.e = 0;
+        t.row0 = group * TILE_M;
+        t.rows_valid = (int) min((int64_t) TILE_M, p.m - t.row0);
     }
     else
     {
-        e = p.block_expert[group];
-        if (e < 0) return;
-        row0 = p.block_row0[group];
-        rows_valid = min(p.tile_rows, p.expert_row0[e] + p.counts[e] - row0);
+        t.e = p.block_expert[group];
+        if (t.e < 0) return false;
+        t.row0 = p.block_row0[group];
+        t.rows_valid = min(p.tile_rows, p.expert_row0[t.e] + p.counts[t.e] - t.row0);
     }
-    if (rows_valid <= 0) return;
+    if (t.rows_valid <= 0) return false;
+    t.which = slot >= p.n_tiles_each ? 1 : 0;
+    t.nt = slot - t.which * p.n_tiles_each;
+    t.packed = reinterpret_cast<const uint32_t*>((t.which ? p.packed1 : p.packed0) +
+                                                 (int64_t) t.e * p.expert_stride_words);
+    t.svh = (t.which ? p.svh1 : p.svh0) + (int64_t) t.e * p.svh_stride + t.nt * TILE_N;
+    return true;
+}
 
-    const int which = slot >= p.n_tiles_each ? 1 : 0;
-    const int nt = slot - which * p.n_tiles_each;
-    const uint32_t* packed = reinterpret_cast<const uint32_t*>((which ? p.packed1 : p.packed0) +
-                                                               (int64_t) e * p.expert_stride_words);
-    const uint16_t* svh = (which ? p.svh1 : p.svh0) + (int64_t) e * p.svh_stride + nt * TILE_N;
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int num_kb = p.size_k / TILE_K;
-
-    // ---- decode role. A stage holds 16 trellis tiles (kt, nt8) = (k-tile 0..1, n-tile 0..7); wave w decodes the four
-    // tiles kt = w >> 1, nt8 = 4 (w & 1) .. + 3 (512 contiguous bytes at 4 bpw), one 16-lane row per tile. Lane j16
-    // of a row decodes chunks 2 j16 and 2 j16 + 1 (positions 16 j16 .. + 15): tile column a = j16 >> 1 and a + 8,
-    // rows 4 b .. 4 b + 3 and 8 + 4 b .. with b = j16 & 1.
-    constexpr int NDW = 8 * BITS;                         // dwords per tile
-    constexpr int NR = raw_words<BITS>();
-    const int j16 = lane & 15;
-    const int ta = j16 >> 1, tb = j16 & 1;
-    const int kt = wave >> 1;
-    const int nt8 = 4 * (wave & 1) + (lane >> 4);
-    const int64_t stage_dwords = (int64_t) 2 * p.tiles_n * NDW;
-    const uint32_t* raw_base = packed + ((int64_t) kt * p.tiles_n + nt * 8 + nt8) * NDW;
+// ------------------------------------------------------------------------------------------- decoding share
+// Wave dw's (0..3) share of decoding each stage. A stage holds 16 trellis tiles (kt, nt8) = (k-tile 0..1, n-tile
+// 0..7); wave dw decodes the four tiles kt = dw >> 1, nt8 = 4 (dw & 1) .. + 3 (512 contiguous bytes at 4 bpw), one
+// 16-lane row per tile. Lane j16 of a row decodes chunks 2 j16 and 2 j16 + 1 (positions 16 j16 .. + 15): tile column
+// a = j16 >> 1 and a + 8, rows 4 b .. 4 b + 3 and 8 + 4 b .. with b = j16 & 1.
+template <int BITS>
+struct Decoder
+{
+    static constexpr int NDW = 8 * BITS;                  // dwords per tile
+    static constexpr int NR = raw_words<BITS>();
+    const uint32_t* raw_base;
+    int64_t stage_dwords;
+    int last_kb, j16, tb, wcol0, wcol1;
     int dw_off[NR];
-    if constexpr (BITS == 3)
-    {
-        const int d0 = (16 * j16 * BITS + BITS - 16) >> 5;  // dword of the first window bit (may be -1)
-        #pragma unroll
-        for (int i = 0; i < NR; ++i) dw_off[i] = (d0 + i + NDW) % NDW;
-    }
-    else
-    {
-        #pragma unroll
-        for (int i = 0; i < NR; ++i) dw_off[i] = NR * j16 + i;
-    }
-    const int wcol0 = nt8 * LDS_BLK + ta * LDS_ROW + kt * 16 + 4 * tb;     // column a, rows 4 b ..
-    const int wcol1 = wcol0 + 8 * LDS_ROW;                                  // column a + 8
 
-    // ---- MFMA role: wave rows [64 wave, 64 wave + 64) in four groups of 16 (mb). v_mfma_f32_16x16x32_f16 with the
-    // decoded weights as the first operand (16 columns x 32 k) and the activations as the second (32 k x 16 rows):
-    // lane l supplies row / column l & 15 and k 8 (l >> 4) .. + 7 of both, and receives row (token) l & 15, columns
-    // 4 (l >> 4) .. + 3 of the 16 x 16 output. An activation load is 16 rows x 64 contiguous bytes.
-    const int tok = lane & 15, kq = lane >> 4;
-    const int rows_w = rows_valid - 64 * wave;            // valid rows of this wave (uniform)
-    // Row-major A: lane l reads 16 bytes of row l & 15 (16 rows per load, one lane per cycle in the address unit).
-    // T16 A: the same operand is 256 contiguous bytes per 16-row group (one coalesced 1 KB load when aligned).
-    const uint16_t* a_ptr[4];
-    const int a_step = p.a_t16 ? 4 * 128 : TILE_K;          // halves per stage
-    #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    __device__ __forceinline__ Decoder(const GemmParams& p, const Tile& t, int dw, int lane, int num_kb)
     {
-        const int64_t row = row0 + min(64 * wave + 16 * mb + tok, rows_valid - 1);
-        a_ptr[mb] = p.a_t16 ? p.a + ((((row >> 4) * (p.size_k >> 3) + kq) << 7) + ((row & 15) << 3))
-                            : p.a + row * p.size_k + 8 * kq;
+        j16 = lane & 15;
+        const int ta = j16 >> 1;
+        tb = j16 & 1;
+        const int kt = dw >> 1;
+        const int nt8 = 4 * (dw & 1) + (lane >> 4);
+        stage_dwords = (int64_t) 2 * p.tiles_n * NDW;
+        raw_base = t.packed + ((int64_t) kt * p.tiles_n + t.nt * 8 + nt8) * NDW;
+        last_kb = num_kb - 1;
+        if constexpr (BITS == 3)
+        {
+            const int d0 = (16 * j16 * BITS + BITS - 16) >> 5;  // dword of the first window bit (may be -1)
+            #pragma unroll
+            for (int i = 0; i < NR; ++i) dw_off[i] = (d0 + i + NDW) % NDW;
+        }
+        else
+        {
+            #pragma unroll
+            for (int i = 0; i < NR; ++i) dw_off[i] = NR * j16 + i;
+        }
+        wcol0 = nt8 * LDS_BLK + ta * LDS_ROW + kt * 16 + 4 * tb;         // column a, rows 4 b ..
+        wcol1 = wcol0 + 8 * LDS_ROW;                                    // column a + 8
     }
-    const int wread = tok * LDS_ROW + 8 * kq;
-
-    auto load_raw = [&](int kb, uint32_t (&r)[NR]) {
-        const uint32_t* base = raw_base + (int64_t) min(kb, num_kb - 1) * stage_dwords;
+    // Raw words of stage kb (clamped to the last stage, so callers may run ahead of the end).
+    __device__ __forceinline__ void load(int kb, uint32_t (&r)[NR]) const
+    {
+        const uint32_t* base = raw_base + (int64_t) min(kb, last_kb) * stage_dwords;
         if constexpr (BITS == 4)
         {
             const uint2 v = *reinterpret_cast<const uint2*>(base + 2 * j16);
@@ -224,8 +213,9 @@ void trellis_gemm_kernel(const GemmParams p)
             #pragma unroll
             for (int i = 0; i < NR; ++i) r[i] = base[dw_off[i]];
         }
-    };
-    auto decode2 = [&](const uint32_t (&r)[NR], Chunk4& c0, Chunk4& c1) {
+    }
+    __device__ __forceinline__ void decode(const uint32_t (&r)[NR], Chunk4& c0, Chunk4& c1) const
+    {
         if constexpr (BITS == 4)
         {
             const uint32_t prev = prev_in_row(r[1]);
@@ -249,108 +239,87 @@ void trellis_gemm_kernel(const GemmParams p)
             c0 = decode_chunk<3>(x0, x1, 3);
             c1 = decode_chunk<3>(x0, x1, 27);
         }
-    };
-    auto store2 = [&](const Chunk4& c0, const Chunk4& c1, uint16_t* lds) {
+    }
+    __device__ __forceinline__ void store(const Chunk4& c0, const Chunk4& c1, uint16_t* lds) const
+    {
         *reinterpret_cast<uint2*>(lds + wcol0) = make_uint2(c0.w[0], c1.w[0]);
         *reinterpret_cast<uint2*>(lds + wcol0 + 8) = make_uint2(c0.w[1], c1.w[1]);
         *reinterpret_cast<uint2*>(lds + wcol1) = make_uint2(c0.w[2], c1.w[2]);
         *reinterpret_cast<uint2*>(lds + wcol1 + 8) = make_uint2(c0.w[3], c1.w[3]);
-    };
+    }
+};
 
-    floatx4 acc[4][8];
-    #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+// ------------------------------------------------------------------------------------------- multiplying share
+// Wave mw's (0..3) share of the MFMA work: tile rows [64 mw, 64 mw + 64) in four groups of 16 (mb).
+// v_mfma_f32_16x16x32_f16 with the decoded weights as the first operand (16 columns x 32 k) and the activations as the
+// second (32 k x 16 rows): lane l supplies row / column l & 15 and k 8 (l >> 4) .. + 7 of both, and receives row
+// (token) l & 15, columns 4 (l >> 4) .. + 3 of the 16 x 16 output. Row-major A: an activation load is 16 rows x 16
+// bytes per lane (one lane per cycle in the address unit); T16 A: 256 contiguous bytes per 16-row group.
+struct Mma
+{
+    const uint16_t* a_ptr[4];
+    int a_step, wread, last_kb;
+
+    __device__ __forceinline__ Mma(const GemmParams& p, const Tile& t, int mw, int lane, int num_kb)
+    {
+        const int tok = lane & 15, kq = lane >> 4;
+        a_step = p.a_t16 ? 4 * 128 : TILE_K;                  // halves per stage
         #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = {};
-
-    // ---- main loop, specialised on the number of 16-row groups a wave multiplies (MBA: 0 = decode only, 1 for a
-    // wave with <= 16 valid rows, else 4). Every variant runs the same barriers. Loads past the last stage are clamped
-    // to it, so every path keeps the same loads in flight.
-    auto mainloop = [&](auto mba_tag) {
-        constexpr int MBA = decltype(mba_tag)::value;
-        uint32_t raw[RAW_DEPTH][NR];
-        half8_t act[ACT_DEPTH][4];
-        auto load_act = [&](int kb, half8_t (&a)[4]) {
-            const int64_t k0 = (int64_t) min(kb, num_kb - 1) * a_step;
-            #pragma unroll
-            for (int mb = 0; mb < MBA; ++mb) a[mb] = *reinterpret_cast<const half8_t*>(a_ptr[mb] + k0);
-        };
+        for (int mb = 0; mb < 4; ++mb)
         {
-            uint32_t r0[NR];
-            load_raw(0, r0);
-            #pragma unroll
-            for (int s = 1; s <= RAW_DEPTH; ++s) load_raw(s, raw[s % RAW_DEPTH]);
-            #pragma unroll
-            for (int s = 0; s < ACT_DEPTH; ++s) load_act(s, act[s]);
-            Chunk4 c0, c1;
-            decode2(r0, c0, c1);
-            store2(c0, c1, lds_b);
+            const int64_t row = t.row0 + min(64 * mw + 16 * mb + tok, t.rows_valid - 1);
+            a_ptr[mb] = p.a_t16 ? p.a + ((((row >> 4) * (p.size_k >> 3) + kq) << 7) + ((row & 15) << 3))
+                                : p.a + row * p.size_k + 8 * kq;
         }
-        // N stages starting at s0 (a multiple of UNROLL, so buffer indices are compile-time)
-        auto trip = [&](int s0, auto n_tag) {
-            constexpr int N = decltype(n_tag)::value;
+        wread = tok * LDS_ROW + 8 * kq;
+        last_kb = num_kb - 1;
+    }
+    template <int MBA>
+    __device__ __forceinline__ void load_act(int kb, half8_t (&a)[4]) const
+    {
+        const int64_t k0 = (int64_t) min(kb, last_kb) * a_step;
+        #pragma unroll
+        for (int mb = 0; mb < MBA; ++mb) a[mb] = *reinterpret_cast<const half8_t*>(a_ptr[mb] + k0);
+    }
+    __device__ __forceinline__ void read_w(const uint16_t* lds, half8_t (&w)[8]) const
+    {
+        #pragma unroll
+        for (int nb = 0; nb < 8; ++nb) w[nb] = *reinterpret_cast<const half8_t*>(lds + nb * LDS_BLK + wread);
+    }
+    template <int MBA>
+    __device__ __forceinline__ static void mfma(const half8_t (&w)[8], const half8_t (&a)[4], floatx4 (&acc)[4][8])
+    {
+        #pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
             #pragma unroll
-            for (int u = 0; u < N; ++u)
-            {
-                const int s = s0 + u;
-                __syncthreads();                                // stage s decoded; buffer (s + 1) & 1 free
-                const uint16_t* lds_s = lds_b + (u & 1) * LDS_TILE;
-                half8_t w[8];
-                if constexpr (MBA > 0)
-                {
-                    #pragma unroll
-                    for (int nb = 0; nb < 8; ++nb) w[nb] = *reinterpret_cast<const half8_t*>(lds_s + nb * LDS_BLK + wread);
-#ifdef EXL3_SCHED_READS_FIRST
-                    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);      // all fragment reads first
-#endif
-                }
-                Chunk4 c0, c1;
-                decode2(raw[(u + 1) % RAW_DEPTH], c0, c1);      // stage s + 1
-                #pragma unroll
-                for (int nb = 0; nb < 8; ++nb)
-                    #pragma unroll
-                    for (int mb = 0; mb < MBA; ++mb)
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[nb], act[u % ACT_DEPTH][mb], acc[mb][nb],
-                                                                           0, 0, 0);
-                store2(c0, c1, lds_b + ((u + 1) & 1) * LDS_TILE);
-                load_raw(s + 1 + RAW_DEPTH, raw[(u + 1) % RAW_DEPTH]);
-                load_act(s + ACT_DEPTH, act[u % ACT_DEPTH]);
-            }
-        };
-        // The first trip is peeled so that the loads in flight at the loop head are the same on entry and on the
-        // back edge; the compiler's wait counts there then only wait for the stage they feed. num_kb is even
-        // (K % 64 == 0), so what is left after whole trips is 0 or 2 stages.
-        using full = std::integral_constant<int, UNROLL>;
-        int s0 = 0;
-        if (num_kb >= UNROLL)
-        {
-            trip(0, full{});
-            for (s0 = UNROLL; s0 + UNROLL <= num_kb; s0 += UNROLL) trip(s0, full{});
-        }
-        if (s0 < num_kb) trip(s0, std::integral_constant<int, 2>{});
-    };
-    if (rows_w > 16) mainloop(std::integral_constant<int, 4>{});
-    else if (rows_w > 0) mainloop(std::integral_constant<int, 1>{});
-    else mainloop(std::integral_constant<int, 0>{});
+            for (int mb = 0; mb < MBA; ++mb)
+                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[nb], a[mb], acc[mb][nb], 0, 0, 0);
+    }
+};
 
-    // ---- epilogue, per 16-row group: H128 over the 128 columns of each row (lane l holds columns
-    // 16 nb + 4 (l >> 4) + r: 5 butterfly stages in registers, column bit 2 across lanes l ^ 16, bit 3 across l ^ 32),
-    // scale by svh / sqrt(128) (and the route weight), then store / scatter. The scatter stages each group through LDS
-    // so that every atomic instruction covers 64 consecutive floats of one output row.
-    if constexpr (MODE == MODE_SCATTER_F32) __syncthreads();     // decoded tiles are dead; LDS becomes staging
-    if (rows_w <= 0) return;
-    const int out_col0 = which * p.n_tiles_each * TILE_N + nt * TILE_N;
+// ------------------------------------------------------------------------------------------- epilogue
+// Per 16-row group of multiplying wave mw: H128 over the 128 columns of each row (lane l holds columns
+// 16 nb + 4 (l >> 4) + r: 5 butterfly stages in registers, column bit 2 across lanes l ^ 16, bit 3 across l ^ 32),
+// scale by svh / sqrt(128) (and the route weight), then store / scatter. The scatter stages each group through LDS
+// (`stage`: 16 rows x SC_ROW floats of this wave) so that every atomic instruction covers 64 consecutive floats of
+// one output row.
+template <int MODE>
+__device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int mw, int lane, floatx4 (&acc)[4][8],
+                                         float* stage)
+{
+    const int tok = lane & 15, kq = lane >> 4;
+    const int rows_w = t.rows_valid - 64 * mw;
+    const int out_col0 = t.which * p.n_tiles_each * TILE_N + t.nt * TILE_N;
     float sv[32];
     #pragma unroll
     for (int nb = 0; nb < 8; ++nb)
     {
-        const uint2 v = *reinterpret_cast<const uint2*>(svh + 16 * nb + 4 * kq);
+        const uint2 v = *reinterpret_cast<const uint2*>(t.svh + 16 * nb + 4 * kq);
         sv[4 * nb + 0] = h2f(v.x & 0xFFFF) * HAD_SCALE;
         sv[4 * nb + 1] = h2f(v.x >> 16) * HAD_SCALE;
         sv[4 * nb + 2] = h2f(v.y & 0xFFFF) * HAD_SCALE;
         sv[4 * nb + 3] = h2f(v.y >> 16) * HAD_SCALE;
     }
-    float* stage = reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW);
     #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
     {
@@ -366,9 +335,9 @@ void trellis_gemm_kernel(const GemmParams p)
         #pragma unroll
         for (int i = 0; i < 32; i += 2) half_wave_butterfly(x[i], x[i + 1]);
 
-        const int r_local = 64 * wave + 16 * mb + tok;          // this lane's row within the tile
-        const bool row_ok = r_local < rows_valid;
-        const int64_t srow = (int64_t) row0 + min(r_local, rows_valid - 1);
+        const int r_local = 64 * mw + 16 * mb + tok;           // this lane's row within the tile
+        const bool row_ok = r_local < t.rows_valid;
+        const int64_t srow = (int64_t) t.row0 + min(r_local, t.rows_valid - 1);
         float rw = 1.0f;
         int64_t orow = srow;
         if constexpr (MODE == MODE_SCATTER_F32 || MODE == MODE_STORE_ROUTE_F32)
@@ -410,18 +379,110 @@ void trellis_gemm_kernel(const GemmParams p)
             const int nrows = min(16, rows_w - 16 * mb);
             const uint32_t tok_lo = (uint32_t) orow, tok_hi = (uint32_t) ((uint64_t) orow >> 32);
             float* outp = reinterpret_cast<float*>(p.out) + out_col0 + lane;
-            for (int t = 0; t < nrows; ++t)
+            for (int tr = 0; tr < nrows; ++tr)
             {
-                const int64_t trow = (int64_t) (((uint64_t) __builtin_amdgcn_readlane(tok_hi, t) << 32) |
-                                                __builtin_amdgcn_readlane(tok_lo, t));
-                const float v0 = stage[t * SC_ROW + lane];
-                const float v1 = stage[t * SC_ROW + 64 + lane];
+                const int64_t trow = (int64_t) (((uint64_t) __builtin_amdgcn_readlane(tok_hi, tr) << 32) |
+                                                __builtin_amdgcn_readlane(tok_lo, tr));
+                const float v0 = stage[tr * SC_ROW + lane];
+                const float v1 = stage[tr * SC_ROW + 64 + lane];
                 float* o = outp + trow * p.out_ld;
                 unsafeAtomicAdd(o, v0);
                 unsafeAtomicAdd(o + 64, v1);
             }
         }
     }
+}
+
+// ------------------------------------------------------------------------------------------- kernel: 4 waves
+// Every wave decodes a quarter of each stage and multiplies its own 64 rows; two workgroups share a CU.
+// Pipeline of stage s: barrier; read stage s's weight fragments; decode stage s+1 while stage s's MFMAs run; write
+// stage s+1 into the other of two LDS buffers; issue loads for later stages.
+template <int BITS, int MODE, bool DENSE>
+__global__ __launch_bounds__(GEMM_THREADS, 2)
+void trellis_gemm_kernel(const GemmParams p)
+{
+    constexpr int LDS_BYTES = (MODE == MODE_SCATTER_F32 && LDS_SCATTER_BYTES > LDS_MAIN_BYTES) ? LDS_SCATTER_BYTES
+                                                                                              : LDS_MAIN_BYTES;
+    __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
+    uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
+
+    int group, slot;
+    xcd_group_slot((int) blockIdx.x, p.n_slots, group, slot);
+    Tile t;
+    if (!resolve_tile<DENSE>(p, group, slot, t)) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int num_kb = p.size_k / TILE_K;
+    using Dec = Decoder<BITS>;
+    constexpr int NR = Dec::NR;
+    const Dec dec(p, t, wave, lane, num_kb);
+    const Mma mm(p, t, wave, lane, num_kb);
+    const int rows_w = t.rows_valid - 64 * wave;          // valid rows of this wave (uniform)
+
+    floatx4 acc[4][8];
+    #pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+        #pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = {};
+
+    // Main loop, specialised on the number of 16-row groups a wave multiplies (MBA: 0 = decode only, 1 for a wave with
+    // <= 16 valid rows, else 4). Every variant runs the same barriers. Loads past the last stage are clamped to it, so
+    // every path keeps the same loads in flight.
+    auto mainloop = [&](auto mba_tag) {
+        constexpr int MBA = decltype(mba_tag)::value;
+        uint32_t raw[RAW_DEPTH][NR];
+        half8_t act[ACT_DEPTH][4];
+        {
+            uint32_t r0[NR];
+            dec.load(0, r0);
+            #pragma unroll
+            for (int s = 1; s <= RAW_DEPTH; ++s) dec.load(s, raw[s % RAW_DEPTH]);
+            #pragma unroll
+            for (int s = 0; s < ACT_DEPTH; ++s) mm.load_act<MBA>(s, act[s]);
+            Chunk4 c0, c1;
+            dec.decode(r0, c0, c1);
+            dec.store(c0, c1, lds_b);
+        }
+        // N stages starting at s0 (a multiple of UNROLL, so buffer indices are compile-time)
+        auto trip = [&](int s0, auto n_tag) {
+            constexpr int N = decltype(n_tag)::value;
+            #pragma unroll
+            for (int u = 0; u < N; ++u)
+            {
+                const int s = s0 + u;
+                __syncthreads();                                // stage s decoded; buffer (s + 1) & 1 free
+                // Keep every stage's work between its barriers: hoisting a later stage's decode above the barrier
+                // would make it wait for raw words loaded in the same trip.
+                __builtin_amdgcn_sched_barrier(0);
+                half8_t w[8];
+                if constexpr (MBA > 0) mm.read_w(lds_b + (u & 1) * LDS_TILE, w);
+                Chunk4 c0, c1;
+                dec.decode(raw[(u + 1) % RAW_DEPTH], c0, c1);   // stage s + 1
+                Mma::mfma<MBA>(w, act[u % ACT_DEPTH], acc);
+                dec.store(c0, c1, lds_b + ((u + 1) & 1) * LDS_TILE);
+                dec.load(s + 1 + RAW_DEPTH, raw[(u + 1) % RAW_DEPTH]);
+                mm.load_act<MBA>(s + ACT_DEPTH, act[u % ACT_DEPTH]);
+            }
+        };
+        // The first trip is peeled so that the loads in flight at the loop head are the same on entry and on the
+        // back edge; the compiler's wait counts there then only wait for the stage they feed. num_kb is even
+        // (K % 64 == 0), so what is left after whole trips is 0 or 2 stages.
+        using full = std::integral_constant<int, UNROLL>;
+        int s0 = 0;
+        if (num_kb >= UNROLL)
+        {
+            trip(0, full{});
+            for (s0 = UNROLL; s0 + UNROLL <= num_kb; s0 += UNROLL) trip(s0, full{});
+        }
+        if (s0 < num_kb) trip(s0, std::integral_constant<int, 2>{});
+    };
+    if (rows_w > 16) mainloop(std::integral_constant<int, 4>{});
+    else if (rows_w > 0) mainloop(std::integral_constant<int, 1>{});
+    else mainloop(std::integral_constant<int, 0>{});
+
+    if constexpr (MODE == MODE_SCATTER_F32) __syncthreads();     // decoded tiles are dead; LDS becomes staging
+    if (rows_w <= 0) return;
+    epilogue<MODE>(p, t, wave, lane, acc, reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW));
 }
 
 // out[t, :] = sum_j partial[t*topk + j, :] in order j = 0 .. topk-1 (deterministic), skipping routes whose id is
