@@ -142,7 +142,8 @@ def run(args, T=None, emit=True):
         "dtype": "f16",
         "data": "synthetic (seeded random trellis codes, signs, scales, N(0,1) activations, Zipf-skewed router)",
         "config": {"workload": workload, "experts": E, "hidden": H, "intermediate": I, "bits": bits,
-                   "tokens": T_, "topk": k, "routing": cfg["routing"], "routed_rows": R, "scatter": scatter},
+                   "tokens": T_, "topk": k, "routing": cfg["routing"], "routed_rows": R, "scatter": scatter,
+                   "tile_rows": rt.tile_rows()},
         "tokens_per_s": round(T_ / (ms_per_step * 1e-3), 1),
         "stage_ms": {n: round(v, 4) for n, v in stage_avg.items()},
         "gemm_tflops_gate_up_and_down": round(both_gemm_tflops, 1),

@@ -279,7 +279,8 @@ extern "C" int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_r
                                 int32_t* tile_expert, int32_t* tile_row0, int32_t* meta, void* stream)
 {
     EXL3_CHECK(n_experts >= 0 && n_experts <= MAX_EXPERTS, "too many experts");
-    EXL3_CHECK(tile_rows == 64 || tile_rows == 128 || tile_rows == 256, "tile_rows must be 64, 128 or 256");
+    EXL3_CHECK(tile_rows == 64 || tile_rows == 128 || tile_rows == 256 || tile_rows == 512,
+               "tile_rows must be 64, 128, 256 or 512");
     EXL3_CHECK(max_tiles >= 0, "bad max_blocks");
     EXL3_CHECK(counts && meta && (max_tiles == 0 || (tile_expert && tile_row0)), "null pointer");
     build_blocks_kernel<<<1, 1024, 0, as_stream(stream)>>>(counts, n_experts, tile_rows, max_tiles, tile_expert,

@@ -30,25 +30,24 @@ constexpr uint32_t MCG_MASK = 0x8FFF8FFFu;
 // from instructions with wait-state rules of their own (per-lane 64-bit shifts fed into them gave wrong results at
 // random): callers hand them 32-bit funnel shifts, loads and DPP moves.
 
-// x0 = lo(ra) * 0xCBAC1FED, x1 = (HI1 ? hi : lo)(rb) * 0xCBAC1FED  (mod 2^32), both as full 32-bit products.
-template <int HI1>
+// x0 = (SEL0 ? hi : lo)(ra) * 0xCBAC1FED, x1 = (SEL1 ? hi : lo)(rb) * 0xCBAC1FED  (mod 2^32), as full 32-bit products.
+#define EXL3_MCG_MUL2(S0, S1, OP0, OP1)                                                                               \
+    asm("v_mul_lo_u16_sdwa %0, %4, %6 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:" S0 " src1_sel:DWORD\n\t"       \
+        "v_mul_lo_u16_sdwa %1, %5, %6 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:" S1 " src1_sel:DWORD\n\t"       \
+        "v_mad_u32_u16 %2, %4, %7, %0" OP0 "\n\t"                                                                    \
+        "v_mad_u32_u16 %3, %5, %7, %1" OP1                                                                          \
+        : "=&v"(t0), "=&v"(t1), "=&v"(x0), "=&v"(x1) : "v"(ra), "v"(rb), "v"(chi), "v"(clo))
+template <int SEL0, int SEL1>
 __device__ __forceinline__ void mcg_mul2(uint32_t ra, uint32_t rb, uint32_t& x0, uint32_t& x1)
 {
     uint32_t t0, t1;
     const uint32_t chi = MCG_MUL_HI, clo = MCG_MUL_LO;
-    if constexpr (HI1)
-        asm("v_mul_lo_u16_sdwa %0, %4, %6 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD\n\t"
-            "v_mul_lo_u16_sdwa %1, %5, %6 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:DWORD\n\t"
-            "v_mad_u32_u16 %2, %4, %7, %0\n\t"
-            "v_mad_u32_u16 %3, %5, %7, %1 op_sel:[1,0,0,0]"
-            : "=&v"(t0), "=&v"(t1), "=&v"(x0), "=&v"(x1) : "v"(ra), "v"(rb), "v"(chi), "v"(clo));
-    else
-        asm("v_mul_lo_u16_sdwa %0, %4, %6 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD\n\t"
-            "v_mul_lo_u16_sdwa %1, %5, %6 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD\n\t"
-            "v_mad_u32_u16 %2, %4, %7, %0\n\t"
-            "v_mad_u32_u16 %3, %5, %7, %1"
-            : "=&v"(t0), "=&v"(t1), "=&v"(x0), "=&v"(x1) : "v"(ra), "v"(rb), "v"(chi), "v"(clo));
+    if constexpr (!SEL0 && !SEL1) EXL3_MCG_MUL2("WORD_0", "WORD_0", "", "");
+    else if constexpr (!SEL0 && SEL1) EXL3_MCG_MUL2("WORD_0", "WORD_1", "", " op_sel:[1,0,0,0]");
+    else if constexpr (SEL0 && !SEL1) EXL3_MCG_MUL2("WORD_1", "WORD_0", " op_sel:[1,0,0,0]", "");
+    else EXL3_MCG_MUL2("WORD_1", "WORD_1", " op_sel:[1,0,0,0]", " op_sel:[1,0,0,0]");
 }
+#undef EXL3_MCG_MUL2
 
 __device__ __forceinline__ uint32_t mcg_mask(uint32_t x) { return (x & MCG_MASK) ^ MCG_XOR; }
 
@@ -102,10 +101,10 @@ __device__ __forceinline__ Chunk4 decode_chunk(uint32_t lo, uint32_t hi, int off
         const uint32_t r1 = __builtin_amdgcn_alignbit(hi, lo, 20);   // states 0, 4
         const uint32_t r2 = __builtin_amdgcn_alignbit(hi, lo, 24);   // states 1, 5
         const uint32_t r3 = __builtin_amdgcn_alignbit(hi, lo, 28);   // states 2, 6
-        mcg_mul2<1>(r1, r1, x[0], x[4]);
-        mcg_mul2<1>(r2, r2, x[1], x[5]);
-        mcg_mul2<1>(r3, r3, x[2], x[6]);
-        mcg_mul2<1>(r0, r0, x[3], x[7]);
+        mcg_mul2<0, 1>(r1, r1, x[0], x[4]);
+        mcg_mul2<0, 1>(r2, r2, x[1], x[5]);
+        mcg_mul2<0, 1>(r3, r3, x[2], x[6]);
+        mcg_mul2<0, 1>(r0, r0, x[3], x[7]);
     }
     else
     {
@@ -114,7 +113,7 @@ __device__ __forceinline__ Chunk4 decode_chunk(uint32_t lo, uint32_t hi, int off
         #pragma unroll
         for (int j = 0; j < 8; ++j) r[j] = (uint32_t) (q >> (off + j * BITS));
         #pragma unroll
-        for (int j = 0; j < 8; j += 2) mcg_mul2<0>(r[j], r[j + 1], x[j], x[j + 1]);
+        for (int j = 0; j < 8; j += 2) mcg_mul2<0, 0>(r[j], r[j + 1], x[j], x[j + 1]);
     }
     uint32_t y[8];
     #pragma unroll
@@ -129,8 +128,8 @@ __device__ __forceinline__ Chunk4 decode_chunk(uint32_t lo, uint32_t hi, int off
 __device__ __forceinline__ void decode_state_pairs(uint32_t ra, uint32_t rb, uint32_t& wa, uint32_t& wb)
 {
     uint32_t x0, x1, x2, x3;
-    mcg_mul2<1>(ra, ra, x0, x1);
-    mcg_mul2<1>(rb, rb, x2, x3);
+    mcg_mul2<0, 1>(ra, ra, x0, x1);
+    mcg_mul2<0, 1>(rb, rb, x2, x3);
     add_halves_2pairs(mcg_mask(x0), mcg_mask(x1), mcg_mask(x2), mcg_mask(x3), wa, wb);
 }
 

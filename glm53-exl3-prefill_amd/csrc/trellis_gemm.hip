@@ -19,6 +19,10 @@
 //     store, fp32 per-route store, or fp32 atomics staged through LDS so each atomic instruction covers 64 consecutive
 //     floats of one output row.
 //   * Workgroups are laid out XCD-aware: the column tiles of one row tile share an XCD (and its L2).
+//   * Activations and trellis words are read through buffer resources: fixed per-lane offsets plus a scalar stage
+//     offset, and zero instead of a fault outside the operand.
+// 512-row tiles run an 8-wave ping-pong variant (trellis_gemm_pp_kernel): two groups of four waves alternate between
+// MFMA phases and decode/load phases, each decoded weight feeding 512 rows.
 #include "exl3_common.h"
 #include "trellis_decode.h"
 
@@ -30,9 +34,6 @@ namespace {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int GEMM_WAVES = 4;
-constexpr int GEMM_THREADS = 64 * GEMM_WAVES;
-constexpr int TILE_M = 64 * GEMM_WAVES;             // 256 rows
 constexpr int TILE_N = 128;
 constexpr int TILE_K = 32;
 constexpr int LDS_ROW = TILE_K + 8;                 // halves per n-row of the decoded tile (80 B)
@@ -41,7 +42,6 @@ constexpr int LDS_BLK = 16 * LDS_ROW + 64;          // halves per 16-row block: 
 constexpr int LDS_TILE = 8 * LDS_BLK;               // halves per decoded stage (128 n-rows)
 constexpr int SC_ROW = TILE_N + 4;                  // floats per staged output row of the scatter epilogue
 constexpr int LDS_MAIN_BYTES = 2 * LDS_TILE * 2;
-constexpr int LDS_SCATTER_BYTES = GEMM_WAVES * 16 * SC_ROW * 4;
 #ifndef EXL3_RAW_DEPTH
 #define EXL3_RAW_DEPTH 4
 #endif
@@ -74,8 +74,8 @@ struct GemmParams
     const int32_t* block_row0;
     const int32_t* counts;
     const int32_t* expert_row0;
-    int tile_rows;                 // rows per schedule entry (128 or 256)
-    int n_groups;                  // row tiles (grouped: table entries; dense: ceil(m / 256))
+    int tile_rows;                 // rows per row tile (grouped: 128, 256 or 512; dense: 64 x waves)
+    int n_groups;                  // row tiles (grouped: table entries; dense: ceil(m / tile_rows))
     int n_slots;                   // 128-col tiles over all tensors
     int n_tiles_each;              // 128-col tiles per tensor
     int64_t m;                     // dense rows
@@ -124,6 +124,27 @@ __device__ __forceinline__ uint32_t prev_in_row(uint32_t v)
     return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, 0x121, 0xF, 0xF, false);     // row_ror:1
 }
 
+// Raw buffer resource over [base, base + bytes): loads through it take a per-lane 32-bit offset and a uniform scalar
+// offset, and return zero (instead of faulting) outside the range. Word 3 selects 32-bit data for untyped access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int64_t bytes)
+{
+    const int n = (int) (bytes < 0 ? 0 : (bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes));
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short) 0, n, 0x00020000);
+}
+
+// f(integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for_from(F&& f)
+{
+    if constexpr (I < N)
+    {
+        f(std::integral_constant<int, I>{});
+        static_for_from<I + 1, N>(f);
+    }
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) { static_for_from<0, N>(f); }
+
 // ------------------------------------------------------------------------------------------- workgroup tile
 // The rows (of one expert), tensor and 128-column tile one workgroup computes.
 struct Tile
@@ -140,8 +161,8 @@ __device__ __forceinline__ bool resolve_tile(const GemmParams& p, int group, int
     if constexpr (DENSE)
     {
         t.e = 0;
-        t.row0 = group * TILE_M;
-        t.rows_valid = (int) min((int64_t) TILE_M, p.m - t.row0);
+        t.row0 = group * p.tile_rows;
+        t.rows_valid = (int) min((int64_t) p.tile_rows, p.m - t.row0);
     }
     else
     {
@@ -164,36 +185,40 @@ __device__ __forceinline__ bool resolve_tile(const GemmParams& p, int group, int
 // 0..7); wave dw decodes the four tiles kt = dw >> 1, nt8 = 4 (dw & 1) .. + 3 (512 contiguous bytes at 4 bpw), one
 // 16-lane row per tile. Lane j16 of a row decodes chunks 2 j16 and 2 j16 + 1 (positions 16 j16 .. + 15): tile column
 // a = j16 >> 1 and a + 8, rows 4 b .. 4 b + 3 and 8 + 4 b .. with b = j16 & 1.
+template <int N> struct Chunks { Chunk4 c[N]; };
+
 template <int BITS>
 struct Decoder
 {
     static constexpr int NDW = 8 * BITS;                  // dwords per tile
     static constexpr int NR = raw_words<BITS>();
-    const uint32_t* raw_base;
-    int64_t stage_dwords;
-    int last_kb, j16, tb, wcol0, wcol1;
-    int dw_off[NR];
+    using Out = Chunks<2>;
+    __amdgpu_buffer_rsrc_t raw;    // based at the wave's first tile of stage 0
+    int stage_bytes, last_kb, tb, wcol0, wcol1;
+    uint32_t off[NR];              // per-lane byte offsets of the raw words
 
     __device__ __forceinline__ Decoder(const GemmParams& p, const Tile& t, int dw, int lane, int num_kb)
     {
-        j16 = lane & 15;
+        const int j16 = lane & 15;
         const int ta = j16 >> 1;
         tb = j16 & 1;
         const int kt = dw >> 1;
         const int nt8 = 4 * (dw & 1) + (lane >> 4);
-        stage_dwords = (int64_t) 2 * p.tiles_n * NDW;
-        raw_base = t.packed + ((int64_t) kt * p.tiles_n + t.nt * 8 + nt8) * NDW;
+        stage_bytes = 2 * p.tiles_n * NDW * 4;
+        const int64_t first = ((int64_t) kt * p.tiles_n + t.nt * 8 + 4 * (dw & 1)) * NDW;
+        raw = buffer_rsrc(t.packed + first, ((int64_t) (p.size_k >> 4) * p.tiles_n * NDW - first) * 4);
         last_kb = num_kb - 1;
+        const int tile_off = (lane >> 4) * NDW;
         if constexpr (BITS == 3)
         {
             const int d0 = (16 * j16 * BITS + BITS - 16) >> 5;  // dword of the first window bit (may be -1)
             #pragma unroll
-            for (int i = 0; i < NR; ++i) dw_off[i] = (d0 + i + NDW) % NDW;
+            for (int i = 0; i < NR; ++i) off[i] = 4 * (tile_off + (d0 + i + NDW) % NDW);
         }
         else
         {
             #pragma unroll
-            for (int i = 0; i < NR; ++i) dw_off[i] = NR * j16 + i;
+            for (int i = 0; i < NR; ++i) off[i] = 4 * (tile_off + NR * j16 + i);
         }
         wcol0 = nt8 * LDS_BLK + ta * LDS_ROW + kt * 16 + 4 * tb;         // column a, rows 4 b ..
         wcol1 = wcol0 + 8 * LDS_ROW;                                    // column a + 8
@@ -201,21 +226,23 @@ struct Decoder
     // Raw words of stage kb (clamped to the last stage, so callers may run ahead of the end).
     __device__ __forceinline__ void load(int kb, uint32_t (&r)[NR]) const
     {
-        const uint32_t* base = raw_base + (int64_t) min(kb, last_kb) * stage_dwords;
+        const int so = min(kb, last_kb) * stage_bytes;
         if constexpr (BITS == 4)
         {
-            const uint2 v = *reinterpret_cast<const uint2*>(base + 2 * j16);
-            r[0] = v.x;
-            r[1] = v.y;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(raw, off[0], so, 0);
+            r[0] = v[0];
+            r[1] = v[1];
         }
         else
         {
             #pragma unroll
-            for (int i = 0; i < NR; ++i) r[i] = base[dw_off[i]];
+            for (int i = 0; i < NR; ++i) r[i] = __builtin_amdgcn_raw_buffer_load_b32(raw, off[i], so, 0);
         }
     }
-    __device__ __forceinline__ void decode(const uint32_t (&r)[NR], Chunk4& c0, Chunk4& c1) const
+    __device__ __forceinline__ void decode(const uint32_t (&r)[NR], Out& o) const
     {
+        Chunk4& c0 = o.c[0];
+        Chunk4& c1 = o.c[1];
         if constexpr (BITS == 4)
         {
             const uint32_t prev = prev_in_row(r[1]);
@@ -240,12 +267,75 @@ struct Decoder
             c1 = decode_chunk<3>(x0, x1, 27);
         }
     }
-    __device__ __forceinline__ void store(const Chunk4& c0, const Chunk4& c1, uint16_t* lds) const
+    __device__ __forceinline__ void store(const Out& o, uint16_t* lds) const
     {
+        const Chunk4& c0 = o.c[0];
+        const Chunk4& c1 = o.c[1];
         *reinterpret_cast<uint2*>(lds + wcol0) = make_uint2(c0.w[0], c1.w[0]);
         *reinterpret_cast<uint2*>(lds + wcol0 + 8) = make_uint2(c0.w[1], c1.w[1]);
         *reinterpret_cast<uint2*>(lds + wcol1) = make_uint2(c0.w[2], c1.w[2]);
         *reinterpret_cast<uint2*>(lds + wcol1 + 8) = make_uint2(c0.w[3], c1.w[3]);
+    }
+};
+
+// Wave dw's (0..7) share of decoding each stage in an 8-wave workgroup: the two tiles kt = dw >> 2,
+// nt8 = 2 (dw & 3) .. + 1, one 32-lane half per tile. Lane c (0..31) of a half decodes chunk c (positions 8c .. 8c + 7):
+// tile column c >> 2 and (c >> 2) + 8, rows 2 (c & 3), + 1, + 8, + 9. Its window bits [8cK + K - 16, 8cK + 8K) sit in
+// the two tile dwords lo = floor(b / 32), hi = lo + 1 (mod 8K, the stream is tail-biting) starting `shift` bits into
+// lo; 16 + 7K <= 44 bits and shift <= 27 for K <= 4, so two dwords always hold them.
+template <int BITS>
+struct Decoder1
+{
+    static constexpr int NDW = 8 * BITS;
+    static constexpr int NR = 2;
+    using Out = Chunks<1>;
+    __amdgpu_buffer_rsrc_t raw;    // based at the wave's first tile of stage 0
+    int stage_bytes, last_kb, shift, wcol0, wcol1;
+    uint32_t lo_off, hi_off;       // per-lane byte offsets of the two raw words
+
+    __device__ __forceinline__ Decoder1(const GemmParams& p, const Tile& t, int dw, int lane, int num_kb)
+    {
+        const int c = lane & 31;
+        const int kt = dw >> 2;
+        const int nt8 = 2 * (dw & 3) + (lane >> 5);
+        stage_bytes = 2 * p.tiles_n * NDW * 4;
+        const int64_t first = ((int64_t) kt * p.tiles_n + t.nt * 8 + 2 * (dw & 3)) * NDW;
+        raw = buffer_rsrc(t.packed + first, ((int64_t) (p.size_k >> 4) * p.tiles_n * NDW - first) * 4);
+        last_kb = num_kb - 1;
+        const int b0 = 8 * c * BITS + BITS - 16;              // first window bit, >= -15
+        const int d0 = b0 >= 0 ? (b0 >> 5) : -1;
+        shift = b0 - 32 * d0;
+        lo_off = 4 * ((lane >> 5) * NDW + (d0 + NDW) % NDW);
+        hi_off = 4 * ((lane >> 5) * NDW + (d0 + 1) % NDW);
+        wcol0 = nt8 * LDS_BLK + (c >> 2) * LDS_ROW + kt * 16 + 2 * (c & 3);
+        wcol1 = wcol0 + 8 * LDS_ROW;
+    }
+    __device__ __forceinline__ void load(int kb, uint32_t (&r)[NR]) const
+    {
+        const int so = min(kb, last_kb) * stage_bytes;
+        r[0] = __builtin_amdgcn_raw_buffer_load_b32(raw, lo_off, so, 0);
+        r[1] = __builtin_amdgcn_raw_buffer_load_b32(raw, hi_off, so, 0);
+    }
+    __device__ __forceinline__ void decode(const uint32_t (&r)[NR], Out& o) const
+    {
+        if constexpr (BITS == 4)
+            o.c[0] = decode_chunk<4>(r[0], r[1], 20);             // shift is 20 for every chunk
+        else
+        {
+            // Realign with 32-bit funnel shifts (per-lane 64-bit shift amounts feeding the decoder's asm gave wrong
+            // results at random), then decode at the compile-time offset 0.
+            const uint32_t x0 = __builtin_amdgcn_alignbit(r[1], r[0], shift);
+            const uint32_t x1 = r[1] >> shift;
+            o.c[0] = decode_chunk<BITS>(x0, x1, 0);
+        }
+    }
+    __device__ __forceinline__ void store(const Out& o, uint16_t* lds) const
+    {
+        const Chunk4& c = o.c[0];
+        *reinterpret_cast<uint32_t*>(lds + wcol0) = c.w[0];
+        *reinterpret_cast<uint32_t*>(lds + wcol0 + 8) = c.w[1];
+        *reinterpret_cast<uint32_t*>(lds + wcol1) = c.w[2];
+        *reinterpret_cast<uint32_t*>(lds + wcol1 + 8) = c.w[3];
     }
 };
 
@@ -255,21 +345,28 @@ struct Decoder
 // second (32 k x 16 rows): lane l supplies row / column l & 15 and k 8 (l >> 4) .. + 7 of both, and receives row
 // (token) l & 15, columns 4 (l >> 4) .. + 3 of the 16 x 16 output. Row-major A: an activation load is 16 rows x 16
 // bytes per lane (one lane per cycle in the address unit); T16 A: 256 contiguous bytes per 16-row group.
+// Activations are read through a buffer resource based at the tile's first row: per-lane offsets are fixed, the
+// stage advance is a scalar offset, so a load needs no vector address arithmetic.
 struct Mma
 {
-    const uint16_t* a_ptr[4];
+    __amdgpu_buffer_rsrc_t a_rsrc;
+    uint32_t a_off[4];
     int a_step, wread, last_kb;
 
     __device__ __forceinline__ Mma(const GemmParams& p, const Tile& t, int mw, int lane, int num_kb)
     {
         const int tok = lane & 15, kq = lane >> 4;
-        a_step = p.a_t16 ? 4 * 128 : TILE_K;                  // halves per stage
+        a_step = p.a_t16 ? 4 * 128 * 2 : TILE_K * 2;          // bytes per stage
+        const int g0 = t.row0 >> 4;
+        const int64_t base_el = p.a_t16 ? (int64_t) g0 * (p.size_k >> 3) * 128 : (int64_t) t.row0 * p.size_k;
+        const int64_t total_el = (p.a_t16 ? (p.a_rows + 15) / 16 * 16 : p.a_rows) * p.size_k;
+        a_rsrc = buffer_rsrc(p.a + base_el, (total_el - base_el) * 2);
         #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
         {
-            const int64_t row = t.row0 + min(64 * mw + 16 * mb + tok, t.rows_valid - 1);
-            a_ptr[mb] = p.a_t16 ? p.a + ((((row >> 4) * (p.size_k >> 3) + kq) << 7) + ((row & 15) << 3))
-                                : p.a + row * p.size_k + 8 * kq;
+            const int row = t.row0 + min(64 * mw + 16 * mb + tok, t.rows_valid - 1);
+            a_off[mb] = p.a_t16 ? (uint32_t) ((((row >> 4) - g0) * (p.size_k >> 3) + kq) * 256 + (row & 15) * 16)
+                                : (uint32_t) ((row - t.row0) * p.size_k * 2 + 16 * kq);
         }
         wread = tok * LDS_ROW + 8 * kq;
         last_kb = num_kb - 1;
@@ -277,9 +374,10 @@ struct Mma
     template <int MBA>
     __device__ __forceinline__ void load_act(int kb, half8_t (&a)[4]) const
     {
-        const int64_t k0 = (int64_t) min(kb, last_kb) * a_step;
+        const int so = min(kb, last_kb) * a_step;
         #pragma unroll
-        for (int mb = 0; mb < MBA; ++mb) a[mb] = *reinterpret_cast<const half8_t*>(a_ptr[mb] + k0);
+        for (int mb = 0; mb < MBA; ++mb)
+            a[mb] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off[mb], so, 0));
     }
     __device__ __forceinline__ void read_w(const uint16_t* lds, half8_t (&w)[8]) const
     {
@@ -394,15 +492,17 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
 }
 
 // ------------------------------------------------------------------------------------------- kernel: 4 waves
-// Every wave decodes a quarter of each stage and multiplies its own 64 rows; two workgroups share a CU.
-// Pipeline of stage s: barrier; read stage s's weight fragments; decode stage s+1 while stage s's MFMAs run; write
-// stage s+1 into the other of two LDS buffers; issue loads for later stages.
+// 128- and 256-row tiles: every wave decodes a quarter of each stage and multiplies its own 64 rows; two workgroups
+// share a CU. Pipeline of stage s: barrier; read stage s's weight fragments; decode stage s+1 while stage s's MFMAs run;
+// write stage s+1 into the other of two LDS buffers; issue loads for later stages.
+template <int WAVES> constexpr int lds_scatter_bytes() { return WAVES * 16 * SC_ROW * 4; }
+
 template <int BITS, int MODE, bool DENSE>
-__global__ __launch_bounds__(GEMM_THREADS, 2)
+__global__ __launch_bounds__(256, 2)
 void trellis_gemm_kernel(const GemmParams p)
 {
-    constexpr int LDS_BYTES = (MODE == MODE_SCATTER_F32 && LDS_SCATTER_BYTES > LDS_MAIN_BYTES) ? LDS_SCATTER_BYTES
-                                                                                              : LDS_MAIN_BYTES;
+    constexpr int SCB = lds_scatter_bytes<4>();
+    constexpr int LDS_BYTES = (MODE == MODE_SCATTER_F32 && SCB > LDS_MAIN_BYTES) ? SCB : LDS_MAIN_BYTES;
     __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
     uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
 
@@ -439,9 +539,9 @@ void trellis_gemm_kernel(const GemmParams p)
             for (int s = 1; s <= RAW_DEPTH; ++s) dec.load(s, raw[s % RAW_DEPTH]);
             #pragma unroll
             for (int s = 0; s < ACT_DEPTH; ++s) mm.load_act<MBA>(s, act[s]);
-            Chunk4 c0, c1;
-            dec.decode(r0, c0, c1);
-            dec.store(c0, c1, lds_b);
+            typename Dec::Out o;
+            dec.decode(r0, o);
+            dec.store(o, lds_b);
         }
         // N stages starting at s0 (a multiple of UNROLL, so buffer indices are compile-time)
         auto trip = [&](int s0, auto n_tag) {
@@ -456,10 +556,10 @@ void trellis_gemm_kernel(const GemmParams p)
                 __builtin_amdgcn_sched_barrier(0);
                 half8_t w[8];
                 if constexpr (MBA > 0) mm.read_w(lds_b + (u & 1) * LDS_TILE, w);
-                Chunk4 c0, c1;
-                dec.decode(raw[(u + 1) % RAW_DEPTH], c0, c1);   // stage s + 1
+                typename Dec::Out o;
+                dec.decode(raw[(u + 1) % RAW_DEPTH], o);        // stage s + 1
                 Mma::mfma<MBA>(w, act[u % ACT_DEPTH], acc);
-                dec.store(c0, c1, lds_b + ((u + 1) & 1) * LDS_TILE);
+                dec.store(o, lds_b + ((u + 1) & 1) * LDS_TILE);
                 dec.load(s + 1 + RAW_DEPTH, raw[(u + 1) % RAW_DEPTH]);
                 mm.load_act<MBA>(s + ACT_DEPTH, act[u % ACT_DEPTH]);
             }
@@ -481,6 +581,142 @@ void trellis_gemm_kernel(const GemmParams p)
     else mainloop(std::integral_constant<int, 0>{});
 
     if constexpr (MODE == MODE_SCATTER_F32) __syncthreads();     // decoded tiles are dead; LDS becomes staging
+    if (rows_w <= 0) return;
+    epilogue<MODE>(p, t, wave, lane, acc, reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW));
+}
+
+// ------------------------------------------------------------------------------------------- kernel: ping-pong
+// 512-row tiles with 8 waves in two groups of four (group g = waves 4g .. 4g + 3, one wave of each group per SIMD;
+// wave w multiplies rows 64 w ..). The two waves of a SIMD take turns: while one group runs a stage's MFMAs from weight
+// fragments already in registers, the other group reads its next fragments from LDS, decodes its half of a later stage
+// (group g decodes k-tile g of every stage, one chunk per lane) and issues loads. The MFMA pipe of each SIMD is fed by
+// one group or the other in every phase, and the decode VALU work runs beside it. Phases, each ended by a barrier:
+//   A(s): group 0 multiplies stage s;  group 1 reads W(s), decodes its half of W(s + 1)
+//   B(s): group 1 multiplies stage s;  group 0 reads W(s + 1), decodes its half of W(s + 2)
+// W(s) lives in LDS buffer s % 2. Group 0 reaches its epilogue while group 1 runs the last phase.
+template <int BITS, int MODE, bool DENSE>
+__global__ __launch_bounds__(512, 1)
+void trellis_gemm_pp_kernel(const GemmParams p)
+{
+    constexpr int SCB = lds_scatter_bytes<8>();
+    constexpr int LDS_BYTES = (MODE == MODE_SCATTER_F32 && SCB > LDS_MAIN_BYTES) ? SCB : LDS_MAIN_BYTES;
+    __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
+    uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
+
+    int group, slot;
+    xcd_group_slot((int) blockIdx.x, p.n_slots, group, slot);
+    Tile t;
+    if (!resolve_tile<DENSE>(p, group, slot, t)) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = wave >> 2;
+    const int num_kb = p.size_k / TILE_K;
+    using Dec = Decoder1<BITS>;
+    const Dec dec(p, t, wave, lane, num_kb);
+    const Mma mm(p, t, wave, lane, num_kb);
+    const int rows_w = t.rows_valid - 64 * wave;          // valid rows of this wave (uniform)
+
+    floatx4 acc[4][8];
+    #pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+        #pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = {};
+
+    // Each group runs its own copy of the loop (G is a compile-time constant), so neither instruction stream carries
+    // the other's branches and the compiler's wait counts follow the loads of one role only. Both copies execute the
+    // same barriers in the same order.
+    // A phase boundary: the barrier, with scheduling fences so that the compiler keeps every MFMA and decode
+    // instruction in the phase it was written in (register-only work may otherwise move across the barrier).
+    auto phase_end = [] {
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto mainloop = [&](auto mba_tag, auto g_tag) {
+        constexpr int MBA = decltype(mba_tag)::value;
+        constexpr int G = decltype(g_tag)::value;
+        uint32_t raw[RAW_DEPTH][Dec::NR];                   // slot d % RAW_DEPTH: this wave's half of stage d
+        half8_t act[2][4];                                  // slot s % 2: stage s
+        half8_t w[8];
+        auto decode_to = [&](int d, int slot_d, uint16_t* dst) {
+            typename Dec::Out o;
+            dec.decode(raw[slot_d], o);
+            dec.store(o, dst);
+            dec.load(d + RAW_DEPTH, raw[slot_d]);
+        };
+        #pragma unroll
+        for (int d = 0; d < RAW_DEPTH; ++d) dec.load(d, raw[d]);
+        mm.load_act<MBA>(0, act[0]);
+        mm.load_act<MBA>(1, act[1]);
+        decode_to(0, 0, lds_b);                             // both groups: their halves of W(0)
+        phase_end();
+        if constexpr (G == 0)                               // group 0's phase B(-1)
+        {
+            if constexpr (MBA > 0) mm.read_w(lds_b, w);
+            if (num_kb > 1) decode_to(1, 1, lds_b + LDS_TILE);
+        }
+        phase_end();
+        // N stages from s0 (a multiple of RAW_DEPTH, so every buffer index is compile-time). The last trip (TAIL)
+        // skips the work past the last stage at compile time: no branch inside a trip, so wait counts stay exact.
+        auto trip = [&](int s0, auto n_tag, auto tail_tag) {
+            constexpr int N = decltype(n_tag)::value;
+            constexpr bool TAIL = decltype(tail_tag)::value;
+            static_for<N>([&](auto u_tag) {
+                constexpr int U = decltype(u_tag)::value;
+                constexpr bool HAS1 = !TAIL || U + 1 < N;           // stage s + 1 exists
+                constexpr bool HAS2 = !TAIL || U + 2 < N;           // stage s + 2 exists
+                const int s = s0 + U;
+                // phase A(s)
+                if constexpr (G == 0)
+                {
+                    Mma::mfma<MBA>(w, act[U & 1], acc);
+                    mm.load_act<MBA>(s + 2, act[U & 1]);
+                }
+                else
+                {
+                    if constexpr (MBA > 0) mm.read_w(lds_b + (U & 1) * LDS_TILE, w);
+                    if constexpr (HAS1) decode_to(s + 1, (U + 1) % RAW_DEPTH, lds_b + ((U + 1) & 1) * LDS_TILE);
+                }
+                phase_end();
+                // phase B(s)
+                if constexpr (G == 1)
+                {
+                    Mma::mfma<MBA>(w, act[U & 1], acc);
+                    mm.load_act<MBA>(s + 2, act[U & 1]);
+                }
+                else
+                {
+                    if constexpr (MBA > 0 && HAS1) mm.read_w(lds_b + ((U + 1) & 1) * LDS_TILE, w);
+                    if constexpr (HAS2) decode_to(s + 2, (U + 2) % RAW_DEPTH, lds_b + (U & 1) * LDS_TILE);
+                }
+                if constexpr (HAS1) phase_end();
+            });
+        };
+        // num_kb is even (K % 64 == 0): whole trips of RAW_DEPTH stages and possibly a 2-stage tail.
+        using full = std::integral_constant<int, RAW_DEPTH>;
+        using half_trip = std::integral_constant<int, 2>;
+        using no = std::false_type;
+        using yes = std::true_type;
+        const bool rem2 = (num_kb % RAW_DEPTH) != 0;
+        const int body = rem2 ? num_kb / RAW_DEPTH : num_kb / RAW_DEPTH - 1;     // trips before the tail
+        int s0 = 0;
+        if (body > 0)
+        {
+            trip(0, full{}, no{});
+            for (s0 = RAW_DEPTH; s0 < body * RAW_DEPTH; s0 += RAW_DEPTH) trip(s0, full{}, no{});
+        }
+        if (rem2) trip(s0, half_trip{}, yes{});
+        else trip(s0, full{}, yes{});
+    };
+    auto by_rows = [&](auto g_tag) {
+        if (rows_w > 16) mainloop(std::integral_constant<int, 4>{}, g_tag);
+        else if (rows_w > 0) mainloop(std::integral_constant<int, 1>{}, g_tag);
+        else mainloop(std::integral_constant<int, 0>{}, g_tag);
+    };
+    if (g == 0) by_rows(std::integral_constant<int, 0>{});
+    else by_rows(std::integral_constant<int, 1>{});
+
+    // No barrier: after the last phase no wave touches the weight buffers, and the scatter's staging rows are per wave.
     if (rows_w <= 0) return;
     epilogue<MODE>(p, t, wave, lane, acc, reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW));
 }
@@ -562,6 +798,7 @@ __global__ void decode_states_kernel(const uint32_t* __restrict__ states, uint32
     if (i + 1 < n2) out[i + 1] = wb;
 }
 
+// 512-row tiles run the 8-wave ping-pong kernel, 128- and 256-row tiles the 4-wave one.
 template <int BITS, int MODE, bool DENSE>
 int launch_gemm(const GemmParams& p, hipStream_t s)
 {
@@ -569,7 +806,10 @@ int launch_gemm(const GemmParams& p, hipStream_t s)
     const int64_t grid = (int64_t) groups8 * p.n_slots;
     if (grid == 0) return EXL3_OK;
     if (grid > 0x7FFFFFFF) return fail("grid too large");
-    trellis_gemm_kernel<BITS, MODE, DENSE><<<(unsigned) grid, GEMM_THREADS, 0, s>>>(p);
+    if (p.tile_rows > 256)
+        trellis_gemm_pp_kernel<BITS, MODE, DENSE><<<(unsigned) grid, 512, 0, s>>>(p);
+    else
+        trellis_gemm_kernel<BITS, MODE, DENSE><<<(unsigned) grid, 256, 0, s>>>(p);
     return EXL3_OK;
 }
 
@@ -602,7 +842,7 @@ extern "C" int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_
                                     const int32_t* route_index, void* out, int64_t out_rows, int mode,
                                     void* stream)
 {
-    EXL3_CHECK(tile_rows == 128 || tile_rows == TILE_M, "tile_rows must be 128 or %d", TILE_M);
+    EXL3_CHECK(tile_rows == 128 || tile_rows == 256 || tile_rows == 512, "tile_rows must be 128, 256 or 512");
     EXL3_CHECK(a_layout == EXL3_LAYOUT_ROWS || a_layout == EXL3_LAYOUT_T16, "unknown layout");
     EXL3_CHECK(bits >= 2 && bits <= 4, "unsupported bits %d (2, 3 or 4)", bits);
     EXL3_CHECK(size_k == tiles_k * 16 && size_k % 64 == 0 && size_k > 0, "K mismatch");
@@ -695,6 +935,9 @@ int fat_common(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed,
     return EXL3_OK;
 }
 
+// Single-expert row tiles: 512 rows (8-wave kernel) unless the matrix is thin enough for one 256-row tile.
+int dense_tile_rows(int64_t m) { return m > 256 ? 512 : 256; }
+
 }  // namespace
 
 extern "C" int exl3_fat_gemm(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed, int tiles_k, int tiles_n,
@@ -706,7 +949,8 @@ extern "C" int exl3_fat_gemm(const uint16_t* a, int64_t m, int size_k, const uin
     EXL3_CHECK(out_rows == m, "out shape must be [M, N]");
     GemmParams p{};
     p.a = a; p.a_rows = m; p.size_k = size_k; p.packed0 = packed; p.tiles_n = tiles_n;
-    p.svh0 = svh; p.n_groups = (int) ((m + TILE_M - 1) / TILE_M); p.n_tiles_each = (int) (svh_len / TILE_N);
+    p.svh0 = svh; p.tile_rows = dense_tile_rows(m); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
+    p.n_tiles_each = (int) (svh_len / TILE_N);
     p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = svh_len;
     rc = launch_bits<MODE_STORE_F32, true>(bits, p, as_stream(stream));
     if (rc) return rc;
@@ -724,7 +968,8 @@ extern "C" int exl3_fat_gemm_scatter(const uint16_t* a, int64_t m, int size_k, c
     EXL3_CHECK(out_rows >= 0, "bad out rows");
     GemmParams p{};
     p.a = a; p.a_rows = m; p.size_k = size_k; p.packed0 = packed; p.tiles_n = tiles_n;
-    p.svh0 = svh; p.n_groups = (int) ((m + TILE_M - 1) / TILE_M); p.n_tiles_each = (int) (svh_len / TILE_N);
+    p.svh0 = svh; p.tile_rows = dense_tile_rows(m); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
+    p.n_tiles_each = (int) (svh_len / TILE_N);
     p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = svh_len;
     p.token = token_idx; p.route_weight = route_weight;
     rc = launch_bits<MODE_SCATTER_F32, true>(bits, p, as_stream(stream));
@@ -751,7 +996,7 @@ extern "C" int exl3_combine_routes(const float* partial, float* out, const void*
 extern "C" int64_t exl3_smem_bytes(int64_t variant)
 {
     if (variant < 0 || variant > 3) return -1;
-    return (int64_t) LDS_SCATTER_BYTES > LDS_MAIN_BYTES ? LDS_SCATTER_BYTES : LDS_MAIN_BYTES;
+    return (int64_t) (lds_scatter_bytes<8>() > LDS_MAIN_BYTES ? lds_scatter_bytes<8>() : LDS_MAIN_BYTES);
 }
 
 extern "C" int exl3_reconstruct(uint16_t* out, const uint16_t* packed, int tiles_k, int tiles_n, int bits, int mcg,

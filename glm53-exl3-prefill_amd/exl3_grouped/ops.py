@@ -109,12 +109,12 @@ def build_blocks(counts: torch.Tensor, block_expert: torch.Tensor, block_row0: t
 
 def build_tiles(counts: torch.Tensor, tile_expert: torch.Tensor, tile_row0: torch.Tensor, meta: torch.Tensor,
                 tile_rows: int) -> None:
-    """build_blocks with `tile_rows` (64, 128 or 256) rows per entry (new; 256-row tables feed grouped_gemm's
-    tile_rows=256 schedule)."""
+    """build_blocks with `tile_rows` (64, 128, 256 or 512) rows per entry (new; 256- and 512-row tables feed
+    grouped_gemm's tile_rows=256 / 512 schedules)."""
     _check(counts.dtype == torch.int32 and tile_expert.dtype == torch.int32 and tile_row0.dtype == torch.int32
            and meta.dtype == torch.int32, "int32 tensors")
     _check(counts.numel() <= 1024, "too many experts")
-    _check(int(tile_rows) in (64, 128, 256), "tile_rows must be 64, 128 or 256")
+    _check(int(tile_rows) in (64, 128, 256, 512), "tile_rows must be 64, 128, 256 or 512")
     _check(tile_row0.numel() >= tile_expert.numel() and meta.numel() >= 2, "block table shapes")
     _check(counts.is_contiguous() and tile_expert.is_contiguous() and tile_row0.is_contiguous()
            and meta.is_contiguous(), "contiguous tensors")
@@ -190,9 +190,10 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
     """kernel/exl3_grouped_prefill.cu:326-378. mode 0: fp16 store; mode 1: fp32 atomic scatter into
     out[token_sorted[r]]; mode 2 (new): fp32 store of the weighted row into out[route_index[r]] (out [T*topk, N]),
     summed per token by combine_routes in a fixed order. tile_rows (new): rows per block-table entry, 128 for
-    build_blocks' table (the reference's), 256 for a build_tiles(..., 256) table. a_layout (new): 0 row-major a,
+    build_blocks' table (the reference's), 256 or 512 for a build_tiles(..., 256 | 512) table (512 runs the 8-wave
+    kernel). a_layout (new): 0 row-major a,
     1 T16 (a from row_had / act_had with dst_layout=1; a_rows gives its logical rows)."""
-    _check(int(tile_rows) in (128, 256), "tile_rows must be 128 or 256")
+    _check(int(tile_rows) in (128, 256, 512), "tile_rows must be 128, 256 or 512")
     _check(a_layout in (0, 1), "unknown layout")
     if a_rows is None:
         a_rows = a.size(0)

@@ -43,6 +43,7 @@ def _load_ext():
 
 
 SCATTER_MODES = ("atomic", "combine")
+TILE_ROWS_CHOICES = (128, 256, 512)
 TILE_ROWS = 256
 
 
@@ -53,8 +54,20 @@ def scatter_mode() -> str:
     return m
 
 
+def tile_rows() -> int:
+    """Rows per expert row tile of the grouped GEMMs (EXL3_GROUPED_TILE_ROWS, default TILE_ROWS): 512-row tiles run
+    the 8-wave GEMM kernel, which decodes each trellis stage once for twice the MFMA work."""
+    v = os.environ.get("EXL3_GROUPED_TILE_ROWS")
+    if v is None:
+        return TILE_ROWS
+    if not v.isdigit() or int(v) not in TILE_ROWS_CHOICES:
+        raise RuntimeError(f"EXL3_GROUPED_TILE_ROWS must be one of {TILE_ROWS_CHOICES}, got {v!r}")
+    return int(v)
+
+
 def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, layer, limit: float,
-                    stage_events: list | None = None, scatter: str | None = None) -> torch.Tensor:
+                    stage_events: list | None = None, scatter: str | None = None,
+                    rows_per_tile: int | None = None) -> torch.Tensor:
     """x2d [T, K] (any float dtype), ids [T, topk] (int64 or int32), weights [T, topk] -> out [T, K] fp32.
     Restates kernel/exl3_grouped_runtime.py:50-83 with the route sort on the GPU (sort_routes).
     stage_events: if a list is given, a timing event recorded on the current stream after each stage is appended
@@ -88,13 +101,16 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     gp.sort_routes(ids, weights, E, token_sorted, weight_sorted, expert_of_row, counts, expert_row0,
                    route_index=route_index)
     mark("sort_routes")
-    # row tiles of TILE_ROWS rows of one expert: each decoded trellis tile feeds up to TILE_ROWS rows of MFMA work
+    # row tiles of `tr` rows of one expert: each decoded trellis tile feeds up to `tr` rows of MFMA work
     # (the reference's 128-row block table is build_blocks; the GEMM accepts either)
-    max_blocks = R // TILE_ROWS + E
+    tr = rows_per_tile or tile_rows()
+    if tr not in TILE_ROWS_CHOICES:
+        raise RuntimeError(f"rows_per_tile must be one of {TILE_ROWS_CHOICES}, got {tr}")
+    max_blocks = R // tr + E
     block_expert = torch.empty(max_blocks, dtype=torch.int32, device=dev)
     block_row0 = torch.empty_like(block_expert)
     meta = torch.zeros(2, dtype=torch.int32, device=dev)
-    gp.build_tiles(counts, block_expert, block_row0, meta, TILE_ROWS)
+    gp.build_tiles(counts, block_expert, block_row0, meta, tr)
     mark("build_blocks")
     # the GEMMs' activation operands (h13, act) are written in the T16 layout, which makes their loads contiguous
     h13 = torch.empty(gp.t16_rows(R), K, dtype=torch.float16, device=dev)
@@ -103,7 +119,7 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     gu = torch.empty(R, 2 * I, dtype=torch.float16, device=dev)
     gp.grouped_gemm(h13, layer.w13_trellis[:, 0], layer.w13_trellis[:, 1], layer.w13_svh[:, 0], layer.w13_svh[:, 1],
                     block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 0,
-                    tile_rows=TILE_ROWS, a_layout=1, a_rows=R)
+                    tile_rows=tr, a_layout=1, a_rows=R)
     mark("gemm_gate_up")
     act = torch.empty(gp.t16_rows(R), I, dtype=torch.float16, device=dev)
     gp.act_had(gu, act, expert_of_row, layer.w2_suh, float(limit), dst_layout=1)
@@ -113,13 +129,13 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
         mark("zero_out")
         gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
                         block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, out, 1,
-                        tile_rows=TILE_ROWS, a_layout=1, a_rows=R)
+                        tile_rows=tr, a_layout=1, a_rows=R)
         mark("gemm_down_scatter")
         return out
     partial = torch.empty(R, K, dtype=torch.float32, device=dev)
     gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
                     block_expert, block_row0, counts, expert_row0, None, weight_sorted, partial, 2,
-                    route_index=route_index, tile_rows=TILE_ROWS, a_layout=1, a_rows=R)
+                    route_index=route_index, tile_rows=tr, a_layout=1, a_rows=R)
     mark("gemm_down_routes")
     out = torch.empty(T, K, dtype=torch.float32, device=dev)
     gp.combine_routes(partial, out, topk, ids, E)

@@ -81,9 +81,9 @@ int exl3_build_blocks(const int32_t* counts, int n_experts, int max_blocks,
                       int32_t* block_expert, int32_t* block_row0, int32_t* meta, void* stream);
 
 /*
- * Row-tile table of `tile_rows` rows per entry (64, 128 or 256): exl3_build_blocks is this with 128. New (no
- * reference counterpart): the grouped GEMM amortises each decoded trellis tile over up to 256 rows of one expert
- * when given a 256-row table (max_tiles >= R/256 + n_experts).
+ * Row-tile table of `tile_rows` rows per entry (64, 128, 256 or 512): exl3_build_blocks is this with 128. New (no
+ * reference counterpart): the grouped GEMM amortises each decoded trellis tile over up to 256 (512) rows of one
+ * expert when given a 256-row (512-row) table (max_tiles >= R/tile_rows + n_experts).
  */
 int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_rows, int max_tiles,
                      int32_t* tile_expert, int32_t* tile_row0, int32_t* meta, void* stream);
@@ -147,7 +147,8 @@ int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
 /*
  * exl3_grouped_gemm with two extensions (new): a_layout (EXL3_LAYOUT_ROWS, or EXL3_LAYOUT_T16 for an `a` written by
  * the _ex Hadamard passes) and tile_rows, the rows per block-table entry (128: the reference's build_blocks table,
- * what exl3_grouped_gemm passes; 256: a table from exl3_build_tiles(..., 256, ...)). Same modes and outputs.
+ * what exl3_grouped_gemm passes; 256 or 512: a table from exl3_build_tiles(..., 256 | 512, ...); 512-row tiles run
+ * an 8-wave kernel). Same modes and outputs.
  */
 int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,
                          const uint16_t* packed_gate, const uint16_t* packed_up, int64_t expert_stride_words,

@@ -7,6 +7,8 @@ accumulation order). At the headline size, where the full CPU loop is too slow f
 sampled tokens plus size-independent properties (linearity in the route weights, token-permutation
 equivariance).
 """
+import functools
+
 import numpy as np
 import pytest
 import torch
@@ -122,7 +124,7 @@ def test_sort_routes_empty_and_dropped(dev):
     assert ts[4:].tolist() == [0, 0] and eor[4:].tolist() == [0, 0] and ws[4:].tolist() == [0, 0]
 
 
-@pytest.mark.parametrize("tile_rows", [128, 64, 256])
+@pytest.mark.parametrize("tile_rows", [128, 64, 256, 512])
 @pytest.mark.parametrize("kind,T,E,k", ROUTINGS)
 def test_build_blocks_bit_exact(dev, kind, T, E, k, tile_rows):
     ids, w = synth.make_routing(kind, T, E, k, seed=T + 1)
@@ -181,11 +183,28 @@ def test_act_had(dev, scale):
 
 
 # ------------------------------------------------------------------------------------------- grouped GEMM
+@functools.lru_cache(maxsize=4)
 def stage_inputs(name, seed, T=None, bits=None, svh_scale=1.0):
     L, x, ids, w, cfg = synth.make_config(name, seed=seed, T=T, bits=bits, svh_scale=svh_scale)
     layer = to_np_layer(L)
     ts, ws, eor, counts, row0 = O.sort_routes(ids, w, cfg["E"])
     return L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0)
+
+
+# Oracle results are shared by the tile sizes of one case (the expert loop dominates the test time).
+@functools.lru_cache(maxsize=2)
+def gate_up_case(name, T, bits):
+    L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, 1, T=T, bits=bits)
+    h13 = O.row_had(x.astype(np.float16), ts, eor, L.w13_suh[:, 0], True)
+    return h13, O.grouped_gemm_mode0(h13, O.WeightCache(layer), counts, row0)
+
+
+@functools.lru_cache(maxsize=2)
+def down_case(name, T, bits, seed, act_seed):
+    L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, seed, T=T, bits=bits)
+    rng = np.random.default_rng(act_seed)
+    act = (rng.standard_normal((ids.size, cfg["I"])) * 3).astype(np.float16)
+    return act, O.grouped_gemm_mode1(act, O.WeightCache(layer), counts, row0, ts, ws, cfg["T"])
 
 
 def gpu_blocks(counts, R, E, dev, tile_rows=128):
@@ -197,15 +216,13 @@ def gpu_blocks(counts, R, E, dev, tile_rows=128):
     return be, br
 
 
-@pytest.mark.parametrize("tile_rows", [128, 256])
+@pytest.mark.parametrize("tile_rows", [128, 256, 512])
 @pytest.mark.parametrize("name,T,bits", [("tiny", None, 4), ("layer1k", None, 4), ("headline", 256, 4),
                                          ("thin", 1024, 4), ("thin", 1024, 3), ("thin", 1024, 2)])
 def test_grouped_gemm_gate_up(dev, name, T, bits, tile_rows):
     L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, 1, T=T, bits=bits)
     R = ids.size
-    h13 = O.row_had(x.astype(np.float16), ts, eor, L.w13_suh[:, 0], True)
-    cache = O.WeightCache(layer)
-    ref = O.grouped_gemm_mode0(h13, cache, counts, row0)
+    h13, ref = gate_up_case(name, T, bits)
     TL = synth.to_device(L, dev)
     be, br = gpu_blocks(counts, R, cfg["E"], dev, tile_rows)
     gu = torch.empty(R, 2 * cfg["I"], dtype=torch.float16, device=dev)
@@ -220,16 +237,13 @@ def test_grouped_gemm_gate_up(dev, name, T, bits, tile_rows):
     assert torch.equal(gu16, gu)                                  # T16 activations: identical arithmetic
 
 
-@pytest.mark.parametrize("tile_rows", [128, 256])
+@pytest.mark.parametrize("tile_rows", [128, 256, 512])
 @pytest.mark.parametrize("name,T,bits", [("tiny", None, 4), ("layer1k", None, 4), ("thin", 512, 4), ("thin", 512, 3),
                                          ("thin", 512, 2)])
 def test_grouped_gemm_down_scatter(dev, name, T, bits, tile_rows):
     L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, 2, T=T, bits=bits)
     R = ids.size
-    rng = np.random.default_rng(9)
-    act = (rng.standard_normal((R, cfg["I"])) * 3).astype(np.float16)
-    cache = O.WeightCache(layer)
-    ref = O.grouped_gemm_mode1(act, cache, counts, row0, ts, ws, cfg["T"])
+    act, ref = down_case(name, T, bits, 2, 9)
     TL = synth.to_device(L, dev)
     be, br = gpu_blocks(counts, R, cfg["E"], dev, tile_rows)
     out = torch.zeros(cfg["T"], cfg["H"], dtype=torch.float32, device=dev)
@@ -242,14 +256,12 @@ def test_grouped_gemm_down_scatter(dev, name, T, bits, tile_rows):
     assert O.rel_l2(out16.cpu().numpy(), ref) < 1e-5
 
 
-@pytest.mark.parametrize("tile_rows", [128, 256])
+@pytest.mark.parametrize("tile_rows", [128, 256, 512])
 @pytest.mark.parametrize("name,T", [("tiny", None), ("layer1k", None)])
 def test_grouped_gemm_down_routes_and_combine(dev, name, T, tile_rows):
     L, layer, x, ids, w, cfg, (ts, ws, eor, counts, row0) = stage_inputs(name, 3, T=T)
     R = ids.size
-    rng = np.random.default_rng(10)
-    act = (rng.standard_normal((R, cfg["I"])) * 3).astype(np.float16)
-    ref = O.grouped_gemm_mode1(act, O.WeightCache(layer), counts, row0, ts, ws, cfg["T"])
+    act, ref = down_case(name, T, None, 3, 10)
     TL = synth.to_device(L, dev)
     be, br = gpu_blocks(counts, R, cfg["E"], dev, tile_rows)
     ri = torch.from_numpy(np.argsort(ids.reshape(-1), kind="stable").astype(np.int32)).to(dev)

@@ -173,7 +173,7 @@ def _brute_blocks(counts, max_blocks, tile_rows=128):
     return be, br, len(be), row
 
 
-@pytest.mark.parametrize("tile_rows", [128, 64, 256])
+@pytest.mark.parametrize("tile_rows", [128, 64, 256, 512])
 @pytest.mark.parametrize("seed", range(5))
 def test_build_blocks_brute_force(seed, tile_rows):
     rng = np.random.default_rng(seed)
