@@ -72,6 +72,27 @@ __device__ __forceinline__ float lane_butterfly(float v, int lane)
     return (lane & M) ? (p - v) : (v + p);
 }
 
+// Butterflies across lanes l and l ^ 16 (rows of 16 lanes) or l ^ 32 (wave halves) for two registers at once, with
+// the gfx950 row-swap permutes (no LDS traffic): afterwards the lower lane of each pair holds own + partner and the
+// upper lane partner - own, for p and for q. The first swap gathers {p_lower, q_lower} / {p_upper, q_upper}, the
+// second puts the sums and differences back.
+__device__ __forceinline__ void pair_butterfly16(float& p, float& q)
+{
+    auto s1 = __builtin_amdgcn_permlane16_swap(__float_as_uint(p), __float_as_uint(q), false, false);
+    const float a = __uint_as_float(s1[0]), b = __uint_as_float(s1[1]);
+    auto s2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(a + b), __float_as_uint(a - b), false, false);
+    p = __uint_as_float(s2[0]);
+    q = __uint_as_float(s2[1]);
+}
+__device__ __forceinline__ void pair_butterfly32(float& p, float& q)
+{
+    auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(p), __float_as_uint(q), false, false);
+    const float a = __uint_as_float(s1[0]), b = __uint_as_float(s1[1]);
+    auto s2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a + b), __float_as_uint(a - b), false, false);
+    p = __uint_as_float(s2[0]);
+    q = __uint_as_float(s2[1]);
+}
+
 // XCD-aware workgroup order: workgroups are handed to the 8 XCDs round robin by dispatch id, so dispatch id
 // i runs on XCD i % 8. Map it to (group, slot) such that every slot of one group lands on the same XCD
 // (they share an activation tile through that XCD's L2) and groups interleave over XCDs.

@@ -135,15 +135,13 @@ __device__ __forceinline__ void had128_t16(float (&x)[32], int lane)
 {
     fwht32_regs(x);
     #pragma unroll
-    for (int i = 0; i < 32; ++i) x[i] = lane_butterfly<16>(x[i], lane);
+    for (int i = 0; i < 32; i += 2) pair_butterfly16(x[i], x[i + 1]);
     #pragma unroll
     for (int i = 0; i < 32; i += 2)
     {
-        auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[i]), __float_as_uint(x[i + 1]), false, false);
-        const float a = __uint_as_float(s1[0]), b = __uint_as_float(s1[1]);
-        auto s2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a + b), __float_as_uint(a - b), false, false);
-        x[i] = __uint_as_float(s2[0]) * HAD_SCALE;
-        x[i + 1] = __uint_as_float(s2[1]) * HAD_SCALE;
+        pair_butterfly32(x[i], x[i + 1]);
+        x[i] *= HAD_SCALE;
+        x[i + 1] *= HAD_SCALE;
     }
 }
 

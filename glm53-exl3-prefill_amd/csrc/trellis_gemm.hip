@@ -101,18 +101,6 @@ __device__ __forceinline__ void fwht32(float (&x)[32])
             }
 }
 
-// Butterfly between lane l and lane l + 32 for two registers at once: lanes 0-31 get p_lo + p_hi, lanes 32-63
-// get p_lo - p_hi (same for q).
-__device__ __forceinline__ void half_wave_butterfly(float& p, float& q)
-{
-    auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(p), __float_as_uint(q), false, false);
-    const float a = __uint_as_float(s1[0]), b = __uint_as_float(s1[1]);
-    const float s = a + b, d = a - b;
-    auto s2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(d), false, false);
-    p = __uint_as_float(s2[0]);
-    q = __uint_as_float(s2[1]);
-}
-
 // Raw stream dwords a lane holds per stage. K=4 / K=2: the lane's own 2 / 1 dwords of the tile (one coalesced load
 // per 16-lane row) -- the 16-bit look-back of its first chunk is the previous lane's last dword (DPP rotate);
 // K=3: the three dwords its two windows touch, loaded directly.
@@ -429,9 +417,9 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
             for (int r = 0; r < 4; ++r) x[4 * nb + r] = acc[mb][nb][r];
         fwht32(x);
         #pragma unroll
-        for (int i = 0; i < 32; ++i) x[i] = lane_butterfly<16>(x[i], lane);
+        for (int i = 0; i < 32; i += 2) pair_butterfly16(x[i], x[i + 1]);
         #pragma unroll
-        for (int i = 0; i < 32; i += 2) half_wave_butterfly(x[i], x[i + 1]);
+        for (int i = 0; i < 32; i += 2) pair_butterfly32(x[i], x[i + 1]);
 
         const int r_local = 64 * mw + 16 * mb + tok;           // this lane's row within the tile
         const bool row_ok = r_local < t.rows_valid;
