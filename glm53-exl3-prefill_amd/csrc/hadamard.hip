@@ -67,7 +67,7 @@ void row_had_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst
         const int64_t r = prc / blocks;
         const int blk = (int) (prc - r * blocks);
         const int64_t srow = GATHER ? token_sorted[r] : r;
-        const int e = expert_of_row[r];
+        const int e = expert_of_row ? expert_of_row[r] : 0;
         const uint4 xv = *reinterpret_cast<const uint4*>(src + srow * K + blk * 128 + col);
         const uint4 sv = *reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + blk * 128 + col);
         float x[8], s[8];
@@ -96,7 +96,7 @@ void act_had_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ act,
         const int64_t prc = ok ? pr : n_pairs - 1;
         const int64_t r = prc / blocks;
         const int blk = (int) (prc - r * blocks);
-        const int e = expert_of_row[r];
+        const int e = expert_of_row ? expert_of_row[r] : 0;
         const uint16_t* g = gu + r * (2 * (int64_t) I) + blk * 128 + col;
         const uint4 gv = *reinterpret_cast<const uint4*>(g);
         const uint4 uv = *reinterpret_cast<const uint4*>(g + I);
@@ -163,7 +163,7 @@ void row_had_t16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__
         const int blk = (int) (it - g * blocks);
         const int64_t r = min(g * 16 + rl, rows - 1);          // rows past the end recompute the last row, unstored
         const int64_t srow = GATHER ? token_sorted[r] : r;
-        const int e = expert_of_row[r];
+        const int e = expert_of_row ? expert_of_row[r] : 0;
         float x[32];
         #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -205,7 +205,7 @@ void act_had_t16_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ 
         const int64_t g = it / blocks;
         const int blk = (int) (it - g * blocks);
         const int64_t r = min(g * 16 + rl, rows - 1);
-        const int e = expert_of_row[r];
+        const int e = expert_of_row ? expert_of_row[r] : 0;
         float x[32];
         #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -264,7 +264,7 @@ extern "C" int exl3_row_had_ex(const uint16_t* src, uint16_t* dst, const int64_t
     EXL3_CHECK(rows >= 0, "bad row count");
     EXL3_CHECK(dst_layout == EXL3_LAYOUT_ROWS || dst_layout == EXL3_LAYOUT_T16, "unknown layout");
     if (rows == 0) return EXL3_OK;
-    EXL3_CHECK(src && dst && expert_of_row && suh && (!gather || token_sorted), "null pointer");
+    EXL3_CHECK(src && dst && suh && (!gather || token_sorted), "null pointer");
     EXL3_CHECK(((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(suh)) & 15) == 0
                && suh_stride % 8 == 0, "src/dst/suh must be 16-byte aligned");
     const unsigned grid = had_grid(rows * (K / 128));
@@ -290,6 +290,7 @@ extern "C" int exl3_row_had(const uint16_t* src, uint16_t* dst, const int64_t* t
                             const uint16_t* suh, int64_t suh_stride, int64_t suh_len, int64_t rows, int K, int gather,
                             void* stream)
 {
+    EXL3_CHECK(rows == 0 || expert_of_row, "null pointer");
     return exl3_row_had_ex(src, dst, token_sorted, expert_of_row, suh, suh_stride, suh_len, rows, K, gather,
                            EXL3_LAYOUT_ROWS, stream);
 }
@@ -302,7 +303,7 @@ extern "C" int exl3_act_had_ex(const uint16_t* gu, int64_t gu_width, uint16_t* a
     EXL3_CHECK(rows >= 0, "bad row count");
     EXL3_CHECK(dst_layout == EXL3_LAYOUT_ROWS || dst_layout == EXL3_LAYOUT_T16, "unknown layout");
     if (rows == 0) return EXL3_OK;
-    EXL3_CHECK(gu && act && expert_of_row && suh_down, "null pointer");
+    EXL3_CHECK(gu && act && suh_down, "null pointer");
     EXL3_CHECK(((reinterpret_cast<uintptr_t>(gu) | reinterpret_cast<uintptr_t>(act) | reinterpret_cast<uintptr_t>(suh_down)) & 15) == 0
                && suh_stride % 8 == 0, "gu/act/suh must be 16-byte aligned");
     if (dst_layout == EXL3_LAYOUT_T16)
@@ -318,6 +319,7 @@ extern "C" int exl3_act_had_ex(const uint16_t* gu, int64_t gu_width, uint16_t* a
 extern "C" int exl3_act_had(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
                             const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, void* stream)
 {
+    EXL3_CHECK(rows == 0 || expert_of_row, "null pointer");
     return exl3_act_had_ex(gu, gu_width, act, expert_of_row, suh_down, suh_stride, rows, I, limit, EXL3_LAYOUT_ROWS,
                            stream);
 }

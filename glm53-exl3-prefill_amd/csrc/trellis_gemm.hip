@@ -965,6 +965,40 @@ extern "C" int exl3_fat_gemm_scatter(const uint16_t* a, int64_t m, int size_k, c
     return hip_status("fat_gemm_v2_scatter");
 }
 
+extern "C" int64_t exl3_linear_workspace_bytes(int64_t m, int k)
+{
+    if (m < 0 || k <= 0) return -1;
+    return (m + 15) / 16 * 16 * (int64_t) k * 2;
+}
+
+extern "C" int exl3_linear(const uint16_t* x, int64_t m, int k, const uint16_t* packed, int tiles_k, int tiles_n,
+                           int bits, const uint16_t* suh, const uint16_t* svh, uint16_t* work, void* out, int out_dtype,
+                           void* stream)
+{
+    EXL3_CHECK(bits >= 2 && bits <= 4, "unsupported bits %d (2, 3 or 4)", bits);
+    EXL3_CHECK(k == tiles_k * 16 && k % 128 == 0 && k > 0, "K must be a multiple of 128 and match the packed tensor");
+    EXL3_CHECK(tiles_n > 0 && (tiles_n * 16) % TILE_N == 0, "N must be a multiple of 128");
+    EXL3_CHECK(m >= 0 && m < ((int64_t) 1 << 31), "bad row count");
+    EXL3_CHECK(out_dtype == EXL3_DTYPE_F32 || out_dtype == EXL3_DTYPE_F16, "out must be fp32 or fp16");
+    if (m == 0) return EXL3_OK;
+    EXL3_CHECK(x && packed && suh && svh && work && out, "null pointer");
+    EXL3_CHECK(aligned16(x) && aligned16(work) && aligned16(suh) && aligned16(out) &&
+               (reinterpret_cast<uintptr_t>(svh) & 7) == 0 && (reinterpret_cast<uintptr_t>(packed) & 7) == 0,
+               "tensors must be contiguous and aligned");
+    hipStream_t s = as_stream(stream);
+    int rc = exl3_row_had_ex(x, work, nullptr, nullptr, suh, 0, k, m, k, 0, EXL3_LAYOUT_T16, stream);
+    if (rc) return rc;
+    const int n = tiles_n * 16;
+    GemmParams p{};
+    p.a = work; p.a_rows = m; p.a_t16 = 1; p.size_k = k; p.packed0 = packed; p.tiles_n = tiles_n;
+    p.svh0 = svh; p.tile_rows = dense_tile_rows(m); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
+    p.n_tiles_each = n / TILE_N; p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = n;
+    rc = out_dtype == EXL3_DTYPE_F32 ? launch_bits<MODE_STORE_F32, true>(bits, p, s)
+                                     : launch_bits<MODE_STORE_F16, true>(bits, p, s);
+    if (rc) return rc;
+    return hip_status("linear");
+}
+
 extern "C" int exl3_combine_routes(const float* partial, float* out, const void* topk_ids, int ids_dtype, int n_experts,
                                    int64_t tokens, int topk, int64_t n, void* stream)
 {

@@ -4,8 +4,8 @@ Reference ops (paths relative to the reference repository):
   build_blocks, row_had, act_had, grouped_gemm   kernel/exl3_grouped_prefill.cu:283-386 (pybind module)
   fat_gemm_v2, fat_gemm_v2_scatter, smem_bytes   kernel/exl3_fat_gemm_v2.cu:298-333
   reconstruct                                     exllamav3 ext.reconstruct, called at kernel/test_fat_v2.py:91-94
-New ops (no reference counterpart): sort_routes (the torch glue of kernel/exl3_grouped_runtime.py:59-68 as a
-GPU counting sort) and decode_states (pins the device trellis decoder).
+New ops (no reference counterpart): linear_exl3 (the dense EXL3 linear), sort_routes (the torch glue of
+kernel/exl3_grouped_runtime.py:59-68 as a GPU counting sort) and decode_states (pins the device trellis decoder).
 
 Each op checks dtypes / shapes / strides on the host first (a bad call raises RuntimeError, like the
 reference's TORCH_CHECK, before anything touches a GPU), then enqueues HIP kernels on the current stream of
@@ -316,6 +316,43 @@ def fat_gemm_v2_scatter(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor
         _lib.call("exl3_fat_gemm_scatter", _p(a), a.size(0), a.size(1), _p(packed), packed.size(0), packed.size(1),
                   packed.size(2), _p(out), out.size(0), _p(svh), svh.numel(), _p(token_idx), _p(route_weight),
                   int(K), int(bool(mcg)), int(bool(mul1)), int(variant), s)
+
+
+def linear_workspace_bytes(m: int, k: int) -> int:
+    """Bytes of the scratch buffer linear_exl3 needs for m rows of width k (the input Hadamard in the T16 layout)."""
+    return int(_lib.load().exl3_linear_workspace_bytes(int(m), int(k)))
+
+
+def linear_exl3(x: torch.Tensor, packed: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, K: int = 4,
+                out: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.float16,
+                work: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Dense EXL3 linear (new; the LinearEXL3 forward the reference's path sits next to):
+    y = H128(H128(x * suh)/sqrt(128) @ W')/sqrt(128) * svh over x fp16 [M, in], packed [in/16, out/16, 16*K] int16,
+    suh fp16 [in], svh fp16 [out]; returns y [M, out] in out_dtype (fp16 or fp32). `work` (uint8 or any dtype, at
+    least linear_workspace_bytes(M, in) bytes) is allocated when not given."""
+    _check(x.dim() == 2 and x.dtype == torch.float16 and x.is_contiguous(), "x must be contiguous fp16 [M, in]")
+    _check(packed.dim() == 3 and packed.dtype == torch.int16 and packed.is_contiguous(),
+           "packed must be contiguous int16 [in/16, out/16, 16*K]")
+    _check(packed.size(2) == 16 * int(K), "packed block width must be 16*K int16 words")
+    _check(suh.dtype == torch.float16 and svh.dtype == torch.float16 and suh.is_contiguous() and svh.is_contiguous(),
+           "suh/svh must be contiguous fp16")
+    M, k = x.shape
+    n = packed.size(1) * 16
+    _check(k == packed.size(0) * 16 and suh.numel() == k, "x in-features must match the packed tensor and suh")
+    _check(svh.numel() == n, "svh must have out-features elements")
+    _check(out_dtype in (torch.float16, torch.float32), "out must be fp16 or fp32")
+    if out is None:
+        out = torch.empty(M, n, dtype=out_dtype, device=x.device)
+    _check(out.dtype == out_dtype and tuple(out.shape) == (M, n) and out.is_contiguous(), "out must be [M, out]")
+    need = linear_workspace_bytes(M, k)
+    if work is None:
+        work = torch.empty(max(need, 16), dtype=torch.uint8, device=x.device)
+    _check(work.is_contiguous() and work.numel() * work.element_size() >= need, "work buffer too small")
+    dev = _require_cuda(x, packed, suh, svh, out, work)
+    with _On(dev) as s:
+        _lib.call("exl3_linear", _p(x), M, k, _p(packed), packed.size(0), packed.size(1), int(K), _p(suh), _p(svh),
+                  _p(work), _p(out), 0 if out_dtype == torch.float32 else 1, s)
+    return out
 
 
 def smem_bytes(variant: int) -> int:

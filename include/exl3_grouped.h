@@ -98,7 +98,8 @@ int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_rows, int ma
 int exl3_row_had(const uint16_t* src, uint16_t* dst, const int64_t* token_sorted, const int32_t* expert_of_row,
                  const uint16_t* suh, int64_t suh_stride, int64_t suh_len, int64_t rows, int K, int gather,
                  void* stream);
-/* exl3_row_had with the destination in layout dst_layout (EXL3_LAYOUT_ROWS or EXL3_LAYOUT_T16). New. */
+/* exl3_row_had with the destination in layout dst_layout (EXL3_LAYOUT_ROWS or EXL3_LAYOUT_T16); expert_of_row may be
+ * NULL (every row uses suh row 0: a single linear). New. */
 int exl3_row_had_ex(const uint16_t* src, uint16_t* dst, const int64_t* token_sorted, const int32_t* expert_of_row,
                     const uint16_t* suh, int64_t suh_stride, int64_t suh_len, int64_t rows, int K, int gather,
                     int dst_layout, void* stream);
@@ -111,7 +112,8 @@ int exl3_row_had_ex(const uint16_t* src, uint16_t* dst, const int64_t* token_sor
  */
 int exl3_act_had(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
                  const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, void* stream);
-/* exl3_act_had with act in layout dst_layout (EXL3_LAYOUT_ROWS or EXL3_LAYOUT_T16). New. */
+/* exl3_act_had with act in layout dst_layout (EXL3_LAYOUT_ROWS or EXL3_LAYOUT_T16); expert_of_row may be NULL (every
+ * row uses suh_down row 0). New. */
 int exl3_act_had_ex(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
                     const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, int dst_layout,
                     void* stream);
@@ -186,6 +188,19 @@ int exl3_fat_gemm_scatter(const uint16_t* a, int64_t m, int size_k, const uint16
                           int64_t svh_len, const int64_t* token_idx, const uint16_t* route_weight,
                           int bits, int mcg, int mul1, int variant, void* stream);
 int64_t exl3_smem_bytes(int64_t variant);
+
+/*
+ * Dense EXL3 linear (LinearEXL3 forward at M = rows; the dense / shared-expert projection the reference lists next to
+ * this path, no kernel of its own there). Same weight convention as the expert GEMMs:
+ *   h = fp16( H128(x * suh) / sqrt(128) )                (per 128-column block of K)
+ *   y = H128( h . W' ) / sqrt(128) * svh                 (W' = decoded trellis [K, N], fp32 accumulate)
+ * x fp16 [m, k] row-major (k % 128 == 0); packed [k/16, n/16, 16*bits] int16 (n % 128 == 0); suh fp16 [k], svh fp16
+ * [n]; work: caller-owned scratch of exl3_linear_workspace_bytes(m, k) bytes (h in the T16 layout); out [m, n] fp32
+ * (out_dtype EXL3_DTYPE_F32) or fp16 (EXL3_DTYPE_F16). New.
+ */
+int64_t exl3_linear_workspace_bytes(int64_t m, int k);
+int exl3_linear(const uint16_t* x, int64_t m, int k, const uint16_t* packed, int tiles_k, int tiles_n, int bits,
+                const uint16_t* suh, const uint16_t* svh, uint16_t* work, void* out, int out_dtype, void* stream);
 
 /*
  * Trellis reconstruct (exllamav3 ext.reconstruct(w, packed, K, mcg, mul1), called by the reference's tests

@@ -336,6 +336,16 @@ def fat_gemm(a: np.ndarray, packed: np.ndarray, svh: np.ndarray, dtype=np.float6
     return expert_gemm(a, w, svh, dtype).astype(np.float32)
 
 
+def linear(x: np.ndarray, packed: np.ndarray, suh: np.ndarray, svh: np.ndarray, out_dtype=np.float32,
+           dtype=np.float64) -> np.ndarray:
+    """Dense EXL3 linear, the LinearEXL3 forward on the real-domain weight diag(suh) H W' H diag(svh)
+    (harness/proto_fp8.py:66-76) in factored form with the expert GEMM's rounding points: h = fp16(H128(x * suh)),
+    y = H128(h @ W') * svh accumulated in fp32 or wider, then rounded to out_dtype."""
+    rows = np.asarray(x).shape[0]
+    h = row_had(np.asarray(x), None, np.zeros(rows, np.int64), np.asarray(suh)[None, :], False)
+    return fat_gemm(h, packed, svh, dtype).astype(out_dtype)
+
+
 def fat_gemm_scatter(a, packed, svh, token_idx, route_weight, out, dtype=np.float64) -> np.ndarray:
     """out[token_idx[m]] += fp32(route_weight[m]) * y[m] (kernel/exl3_fat_gemm_v2.cu:221-226; reference
     check kernel/test_fat_v2.py:135 uses index_add_)."""

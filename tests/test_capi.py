@@ -165,3 +165,29 @@ def test_shim_grouped_gemm_messages():
     with pytest.raises(RuntimeError, match="tensors must be CUDA"):
         gp.grouped_gemm(a, w13[:, 0], w13[:, 1], svh[:, 0], svh[:, 1], i32, i32, i32[:8], i32[:8], None, None,
                         gu, 0)
+
+
+def test_linear_contract():
+    args = dict(x=FAKE, m=300, k=4096, pk=FAKE, tk=256, tn=96, bits=4, suh=FAKE, svh=FAKE, work=FAKE, out=FAKE,
+                dtype=1)                         # EXL3_DTYPE_F16
+
+    def call(**kw):
+        a = dict(args)
+        a.update(kw)
+        return rc_and_msg("exl3_linear", a["x"], a["m"], a["k"], a["pk"], a["tk"], a["tn"], a["bits"], a["suh"],
+                          a["svh"], a["work"], a["out"], a["dtype"], None)
+
+    rc, msg = call(bits=5)
+    assert rc == _lib.EXL3_ERR_ARG and "bits" in msg
+    rc, msg = call(k=4000, tk=250)
+    assert rc == _lib.EXL3_ERR_ARG and "multiple of 128" in msg
+    rc, msg = call(tn=95)
+    assert rc == _lib.EXL3_ERR_ARG and "N must be a multiple of 128" in msg
+    rc, msg = call(dtype=4)
+    assert rc == _lib.EXL3_ERR_ARG and "fp32 or fp16" in msg
+    rc, msg = call(x=None)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "null pointer"
+    rc, msg = call(m=0, x=None)                      # nothing to do: no pointer is needed
+    assert rc == _lib.EXL3_OK
+    assert _lib.load().exl3_linear_workspace_bytes(300, 4096) == 304 * 4096 * 2
+    assert _lib.load().exl3_linear_workspace_bytes(-1, 4096) == -1

@@ -289,6 +289,26 @@ def test_combine_skips_invalid_routes(dev):
     assert torch.equal(out.cpu(), (p * keep[:, :, None]).sum(1))
 
 
+# ------------------------------------------------------------------------------------------- dense EXL3 linear
+@pytest.mark.parametrize("M,K,N,bits", [(1, 4096, 1536, 4), (300, 768, 4096, 4), (4096, 4096, 1536, 4),
+                                        (200, 4096, 1536, 3), (70, 1024, 512, 2), (0, 512, 256, 4)])
+def test_linear_exl3(dev, M, K, N, bits):
+    rng = np.random.default_rng(M + K + bits)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    packed = synth._random_words(rng, (K // 16, N // 16, 16 * bits))
+    suh = synth._signs(rng, (K,))
+    svh = synth._svh(rng, (N,))
+    y32 = gp.linear_exl3(t16(x, dev), t16(packed, dev), t16(suh, dev), t16(svh, dev), bits, out_dtype=torch.float32)
+    y16 = gp.linear_exl3(t16(x, dev), t16(packed, dev), t16(suh, dev), t16(svh, dev), bits)
+    assert y32.shape == (M, N) and y16.dtype == torch.float16
+    if M == 0:
+        return
+    ref = O.linear(x, packed, suh, svh)
+    got = y32.cpu().numpy()
+    assert O.rel_l2(got, ref) < 1e-4
+    assert within_f16_steps(y16.cpu().numpy(), got.astype(np.float16))      # fp16 store = rounded fp32 result
+
+
 # ------------------------------------------------------------------------------------------- fat GEMM (config 2)
 @pytest.mark.parametrize("M", [300, 4096])
 def test_fat_gemm_config2(dev, M):

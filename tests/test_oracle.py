@@ -266,6 +266,24 @@ def test_gemm_stage_commutes_with_real_domain_weight():
     assert np.allclose(y, x.astype(np.float64) @ Wg, rtol=1e-9, atol=1e-9)
 
 
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_linear_is_x_times_real_domain_weight(bits):
+    """The dense linear equals x @ diag(suh) H W' H diag(svh) up to the fp16 rounding of h."""
+    rng = np.random.default_rng(bits)
+    K, N, M = 256, 384, 24
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    packed = synth._random_words(rng, (K // 16, N // 16, 16 * bits))
+    suh = synth._signs(rng, (K,))
+    svh = synth._svh(rng, (N,))
+    got = O.linear(x, packed, suh, svh)
+    ref = x.astype(np.float64) @ _real_weight(packed, suh, svh)
+    assert O.rel_l2(got, ref) < 1e-3
+    # the same without rounding h to fp16 matches to float64 accuracy: only that rounding separates the two
+    h = O.had128(x.astype(np.float64) * suh.astype(np.float64))
+    exact = O.expert_gemm(h, O.reconstruct(packed).astype(np.float64), svh)
+    assert np.allclose(exact, ref, rtol=1e-9, atol=1e-9)
+
+
 def test_fat_scatter_is_index_add_of_store():
     a, packed, svh = synth.make_fat(0, M=40, K=128, N=128)
     y = O.fat_gemm(a, packed, svh)
