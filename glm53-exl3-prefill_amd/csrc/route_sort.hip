@@ -8,7 +8,10 @@
 //      a ballot match over the id bits, across the chunk's waves from per-wave counts in LDS, so the write
 //      order is exactly the stable order.
 // build_blocks restates kernel/exl3_grouped_prefill.cu:63-96 with a parallel scan instead of the serial one.
+// route_topk is the router glue in front of the sort (GLM-5.3-Flash's noaux_tc top-k): one wave per token.
 #include "exl3_common.h"
+
+#include <math.h>
 
 namespace exl3 {
 namespace {
@@ -224,6 +227,81 @@ void build_blocks_kernel(const int32_t* __restrict__ counts, int n_experts, int 
     for (int b = n_blocks + e; b < max_blocks; b += 1024) block_expert[b] = -1;
 }
 
+// ------------------------------------------------------------------------------------------- router top-k
+constexpr int ROUTER_VPL = MAX_EXPERTS / 64;           // scores per lane (expert e = lane + 64 i)
+constexpr int ROUTER_MAX_TOPK = 16;
+
+__device__ __forceinline__ float load_logit(const void* p, int dtype, int64_t i)
+{
+    if (dtype == EXL3_DTYPE_F32) return reinterpret_cast<const float*>(p)[i];
+    if (dtype == EXL3_DTYPE_F16) return h2f(reinterpret_cast<const uint16_t*>(p)[i]);
+    return __uint_as_float((uint32_t) reinterpret_cast<const uint16_t*>(p)[i] << 16);    // bf16
+}
+
+// Per token t (one wave): s_e = sigmoid(logit_e) in fp32; the k experts with the largest s_e + bias_e (ties: lower
+// expert id) in decreasing order; weight_j = s_(j) / sum_j s_(j) * scale (renorm; the sum runs in selection order) or
+// s_(j) * scale. NaN scores are never chosen; if fewer than k finite candidates exist the rest get id -1, weight 0.
+__global__ __launch_bounds__(256)
+void route_topk_kernel(const void* __restrict__ logits, int logits_dtype, int64_t ld, const float* __restrict__ bias,
+                       int64_t tokens, int E, int k, int renorm, float scale, void* __restrict__ ids, int ids_dtype,
+                       float* __restrict__ weights)
+{
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    for (int64_t t = (int64_t) blockIdx.x * 4 + wv; t < tokens; t += (int64_t) gridDim.x * 4)
+    {
+        float sel[ROUTER_VPL], sc[ROUTER_VPL];
+        #pragma unroll
+        for (int i = 0; i < ROUTER_VPL; ++i)
+        {
+            const int e = lane + 64 * i;
+            sel[i] = -INFINITY;
+            sc[i] = 0.0f;
+            if (e < E)
+            {
+                const float s = 1.0f / (1.0f + expf(-load_logit(logits, logits_dtype, t * ld + e)));
+                sc[i] = s;
+                sel[i] = s + (bias ? bias[e] : 0.0f);
+            }
+        }
+        int my_id = -1;
+        float my_score = 0.0f, sum = 0.0f;
+        for (int j = 0; j < k; ++j)
+        {
+            float best = -INFINITY, bsc = 0.0f;
+            int be = 0x7FFFFFFF;
+            #pragma unroll
+            for (int i = 0; i < ROUTER_VPL; ++i)
+                if (sel[i] > best) { best = sel[i]; bsc = sc[i]; be = lane + 64 * i; }
+            #pragma unroll
+            for (int off = 32; off >= 1; off >>= 1)
+            {
+                const float ob = __shfl_xor(best, off);
+                const int oe = __shfl_xor(be, off);
+                const float os = __shfl_xor(bsc, off);
+                if (ob > best || (ob == best && oe < be)) { best = ob; be = oe; bsc = os; }
+            }
+            if (best == -INFINITY) { be = -1; bsc = 0.0f; }      // no finite candidate left
+            else if ((be & 63) == lane)
+            {
+                #pragma unroll
+                for (int i = 0; i < ROUTER_VPL; ++i)
+                    if (i == (be >> 6)) sel[i] = -INFINITY;
+            }
+            if (lane == j) { my_id = be; my_score = bsc; }
+            sum += bsc;
+        }
+        if (lane < k)
+        {
+            const float w = renorm ? (sum > 0.0f ? my_score / sum * scale : 0.0f) : my_score * scale;
+            const int64_t o = t * k + lane;
+            if (ids_dtype == EXL3_DTYPE_I64) reinterpret_cast<int64_t*>(ids)[o] = my_id;
+            else reinterpret_cast<int32_t*>(ids)[o] = my_id;
+            weights[o] = w;
+        }
+    }
+}
+
 }  // namespace
 }  // namespace exl3
 
@@ -292,4 +370,23 @@ extern "C" int exl3_build_blocks(const int32_t* counts, int n_experts, int max_b
                                  int32_t* block_expert, int32_t* block_row0, int32_t* meta, void* stream)
 {
     return exl3_build_tiles(counts, n_experts, 128, max_blocks, block_expert, block_row0, meta, stream);
+}
+
+extern "C" int exl3_route_topk(const void* logits, int logits_dtype, int64_t logits_ld, const float* bias,
+                               int64_t tokens, int n_experts, int topk, int renorm, float scale, void* topk_ids,
+                               int ids_dtype, float* topk_weights, void* stream)
+{
+    EXL3_CHECK(n_experts > 0 && n_experts <= MAX_EXPERTS, "too many experts");
+    EXL3_CHECK(topk > 0 && topk <= ROUTER_MAX_TOPK && topk <= n_experts, "topk must be in [1, min(16, n_experts)]");
+    EXL3_CHECK(logits_dtype == EXL3_DTYPE_F32 || logits_dtype == EXL3_DTYPE_F16 || logits_dtype == EXL3_DTYPE_BF16,
+               "logits must be fp32, fp16 or bf16");
+    EXL3_CHECK(ids_dtype == EXL3_DTYPE_I64 || ids_dtype == EXL3_DTYPE_I32, "topk_ids must be int64 or int32");
+    EXL3_CHECK(tokens >= 0 && logits_ld >= n_experts, "bad sizes");
+    if (tokens == 0) return EXL3_OK;
+    EXL3_CHECK(logits && topk_ids && topk_weights, "null pointer");
+    const int64_t blocks = (tokens + 3) / 4;
+    route_topk_kernel<<<(unsigned) (blocks < 65536 ? blocks : 65536), 256, 0, as_stream(stream)>>>(
+        logits, logits_dtype, logits_ld, bias, tokens, n_experts, topk, renorm, scale, topk_ids, ids_dtype,
+        topk_weights);
+    return hip_status("route_topk");
 }

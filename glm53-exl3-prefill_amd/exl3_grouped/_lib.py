@@ -45,12 +45,13 @@ SIGNATURES = {
     "exl3_fat_gemm_scatter": (I32, [P, I64, I32, P, I32, I32, I32, P, I64, P, I64, P, P, I32, I32, I32, I32, P]),
     "exl3_smem_bytes": (I64, [I64]),
     "exl3_linear_workspace_bytes": (I64, [I64, I32]),
+    "exl3_route_topk": (I32, [P, I32, I64, P, I64, I32, I32, I32, F32, P, I32, P, P]),
     "exl3_linear": (I32, [P, I64, I32, P, I32, I32, I32, P, P, P, P, I32, P]),
     "exl3_reconstruct": (I32, [P, P, I32, I32, I32, I32, I32, P]),
     "exl3_decode_states": (I32, [P, P, I64, P]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib = None
 _path = None

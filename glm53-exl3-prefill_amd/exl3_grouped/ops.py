@@ -4,7 +4,7 @@ Reference ops (paths relative to the reference repository):
   build_blocks, row_had, act_had, grouped_gemm   kernel/exl3_grouped_prefill.cu:283-386 (pybind module)
   fat_gemm_v2, fat_gemm_v2_scatter, smem_bytes   kernel/exl3_fat_gemm_v2.cu:298-333
   reconstruct                                     exllamav3 ext.reconstruct, called at kernel/test_fat_v2.py:91-94
-New ops (no reference counterpart): linear_exl3 (the dense EXL3 linear), sort_routes (the torch glue of
+New ops (no reference counterpart): route_topk (the router top-k), linear_exl3 (the dense EXL3 linear), sort_routes (the torch glue of
 kernel/exl3_grouped_runtime.py:59-68 as a GPU counting sort) and decode_states (pins the device trellis decoder).
 
 Each op checks dtypes / shapes / strides on the host first (a bad call raises RuntimeError, like the
@@ -100,6 +100,34 @@ def sort_routes(topk_ids: torch.Tensor, topk_weights: torch.Tensor, n_experts: i
                   T, k, n_experts, _p(token_sorted), _p(weight_sorted), _p(expert_of_row), _p(route_index),
                   _p(counts), _p(expert_row0), _p(workspace), workspace.numel() * workspace.element_size(), s)
     return workspace
+
+
+def route_topk(logits: torch.Tensor, e_score_correction_bias: Optional[torch.Tensor] = None, topk: int = 8,
+               routed_scaling_factor: float = 2.5, renormalize: bool = True,
+               ids_dtype: torch.dtype = torch.int64) -> tuple[torch.Tensor, torch.Tensor]:
+    """Router top-k feeding sort_routes (new; GLM-5.3-Flash's noaux_tc router): sigmoid scores in fp32, selection by
+    score + bias, top-k in decreasing order (ties: lower expert id), weights = un-biased scores renormalised to sum 1
+    (renormalize) times routed_scaling_factor. logits [T, E] fp32/fp16/bf16 (rows may be strided); returns
+    (topk_ids [T, topk] ids_dtype, topk_weights [T, topk] fp32)."""
+    _check(logits.dim() == 2 and logits.dtype in (torch.float32, torch.float16, torch.bfloat16), "logits must be [T, E]")
+    _check(logits.stride(1) == 1 or logits.size(0) == 0, "logits rows must be contiguous")
+    T, E = logits.shape
+    _check(0 < E <= 1024, "too many experts")
+    _check(0 < int(topk) <= min(16, E), "topk must be in [1, min(16, n_experts)]")
+    _check(ids_dtype in (torch.int64, torch.int32), "topk_ids must be int64 or int32")
+    if e_score_correction_bias is not None:
+        _check(e_score_correction_bias.dtype == torch.float32 and e_score_correction_bias.is_contiguous()
+               and e_score_correction_bias.numel() == E, "bias must be contiguous fp32 [E]")
+    ids = torch.empty(T, int(topk), dtype=ids_dtype, device=logits.device)
+    weights = torch.empty(T, int(topk), dtype=torch.float32, device=logits.device)
+    if T == 0:
+        return ids, weights
+    dev = _require_cuda(logits, ids, weights, *([e_score_correction_bias] if e_score_correction_bias is not None else []))
+    with _On(dev) as s:
+        _lib.call("exl3_route_topk", _p(logits), _DT[logits.dtype], logits.stride(0), _p(e_score_correction_bias), T, E,
+                  int(topk), int(bool(renormalize)), float(routed_scaling_factor), _p(ids), _DT[ids_dtype], _p(weights),
+                  s)
+    return ids, weights
 
 
 def build_blocks(counts: torch.Tensor, block_expert: torch.Tensor, block_row0: torch.Tensor, meta: torch.Tensor) -> None:

@@ -143,6 +143,18 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     return out
 
 
+def grouped_prefill_from_logits(x2d: torch.Tensor, router_logits: torch.Tensor, layer, limit: float,
+                                e_score_correction_bias: torch.Tensor | None = None, topk: int = 8,
+                                routed_scaling_factor: float = 2.5, renormalize: bool = True,
+                                scatter: str | None = None) -> torch.Tensor:
+    """The router glue in front of grouped_prefill, on the GPU (new): GLM-5.3-Flash's noaux_tc top-k (sigmoid scores,
+    biased selection, renormalised un-biased weights x routed_scaling_factor) straight into the route sort and the
+    grouped path. router_logits [T, E] as the gate linear produced them (fp32, fp16 or bf16)."""
+    gp = _load_ext()
+    ids, weights = gp.route_topk(router_logits, e_score_correction_bias, topk, routed_scaling_factor, renormalize)
+    return grouped_prefill(x2d, ids, weights, layer, limit, scatter=scatter)
+
+
 def install(ov):
     """Wrap ov.apply_exl3_experts: prefill-sized calls use the grouped path; everything else is untouched
     (kernel/exl3_grouped_runtime.py:86-112)."""

@@ -72,6 +72,20 @@ int exl3_sort_routes(const void* topk_ids, int ids_dtype, const void* topk_weigh
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Router top-k in front of the sort (new; the glue the reference's path takes as given: GLM-5.3-Flash's noaux_tc
+ * router -- sigmoid scores in fp32, selection by score + e_score_correction_bias, top-k, weights from the un-biased
+ * scores renormalised to sum 1 (norm_topk_prob) times routed_scaling_factor).
+ *   logits [tokens, >= n_experts] (row stride logits_ld elements) fp32 / fp16 / bf16; bias fp32 [n_experts] or NULL.
+ *   topk_ids [tokens, topk] int64 or int32, decreasing selection score (ties: lower expert id); topk_weights fp32
+ *   [tokens, topk] = s / sum(s) * scale (renorm != 0, sum in selection order) or s * scale.
+ * NaN scores are never chosen; when fewer than topk finite scores exist the remaining ids are -1 (dropped by
+ * exl3_sort_routes) with weight 0. topk <= 16, n_experts <= 1024.
+ */
+int exl3_route_topk(const void* logits, int logits_dtype, int64_t logits_ld, const float* bias, int64_t tokens,
+                    int n_experts, int topk, int renorm, float scale, void* topk_ids, int ids_dtype,
+                    float* topk_weights, void* stream);
+
+/*
  * Block table (pybind op build_blocks, kernel/exl3_grouped_prefill.cu:63-96 and :285-294).
  * counts int32 [n_experts] -> for each 128-row block b of each expert (experts in order):
  *   block_expert[b] = e, block_row0[b] = expert_row0[e] + 128*i; entries b >= n_blocks get block_expert = -1

@@ -145,6 +145,24 @@ def sort_routes(ids: np.ndarray, weights: np.ndarray, n_experts: int):
     return token_sorted, weight_sorted.view(np.float16), expert_of_row, counts, expert_row0
 
 
+def route_topk(logits: np.ndarray, bias, topk: int, scale: float, renorm: bool = True):
+    """GLM-5.3-Flash noaux_tc router (docs/research/02-glm-5.3-flash-architecture.md:33): s = sigmoid(logit) in fp32;
+    the topk experts with the largest s + bias in decreasing order, ties to the lower expert id; weights = s / sum(s)
+    * scale (sum in selection order, fp32) or s * scale. Returns (ids int64 [T, k], weights fp32 [T, k])."""
+    lg = np.asarray(logits, np.float32).astype(np.float64)
+    s = (1.0 / (1.0 + np.exp(-lg))).astype(np.float32)
+    sel = s + (np.asarray(bias, np.float32) if bias is not None else np.float32(0))
+    order = np.argsort(-sel, axis=1, kind="stable")[:, :topk]
+    sc = np.take_along_axis(s, order, axis=1)
+    w = np.empty_like(sc)
+    for t in range(sc.shape[0]):
+        tot = np.float32(0)
+        for j in range(topk):
+            tot = np.float32(tot + sc[t, j])
+        w[t] = (sc[t] / tot * np.float32(scale)) if renorm else sc[t] * np.float32(scale)
+    return order.astype(np.int64), w.astype(np.float32)
+
+
 def build_blocks(counts: np.ndarray, max_blocks: int, init: int = 0, tile_rows: int = 128):
     """kernel/exl3_grouped_prefill.cu:63-96 (128-row blocks; other tile sizes for the 256-row schedule);
     block_row0 past n_blocks keeps `init`."""

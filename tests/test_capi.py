@@ -191,3 +191,25 @@ def test_linear_contract():
     assert rc == _lib.EXL3_OK
     assert _lib.load().exl3_linear_workspace_bytes(300, 4096) == 304 * 4096 * 2
     assert _lib.load().exl3_linear_workspace_bytes(-1, 4096) == -1
+
+
+def test_route_topk_contract():
+    def call(E=288, k=8, ldt=0, idt=4, T=10, ld=288, logits=FAKE):
+        return rc_and_msg("exl3_route_topk", logits, ldt, ld, None, T, E, k, 1, ctypes.c_float(2.5), FAKE, idt,
+                          FAKE, None)
+    rc, msg = call(E=1025)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "too many experts"
+    rc, msg = call(k=17)
+    assert rc == _lib.EXL3_ERR_ARG and "topk" in msg
+    rc, msg = call(E=4, k=5)
+    assert rc == _lib.EXL3_ERR_ARG and "topk" in msg
+    rc, msg = call(ldt=3)
+    assert rc == _lib.EXL3_ERR_ARG and "logits" in msg
+    rc, msg = call(idt=0)
+    assert rc == _lib.EXL3_ERR_ARG and "int64 or int32" in msg
+    rc, msg = call(ld=100)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "bad sizes"
+    rc, msg = call(logits=None)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "null pointer"
+    rc, msg = call(T=0, logits=None)
+    assert rc == _lib.EXL3_OK

@@ -143,6 +143,82 @@ def test_build_blocks_bit_exact(dev, kind, T, E, k, tile_rows):
         assert np.array_equal(meta.cpu().numpy(), rmeta)
 
 
+# ------------------------------------------------------------------------------------------- router top-k
+def _margins(logits, bias, k):
+    """Per token: is the chosen set unambiguous (k-th and (k+1)-th selection scores more than 1e-5 apart), and is the
+    order too (every adjacent pair among the first k + 1 apart)? fp32 sigmoids may differ by an ulp between devices."""
+    s = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    sel = np.sort(s + (bias if bias is not None else 0), axis=1)[:, ::-1][:, :k + 1]
+    gaps = sel[:, :-1] - sel[:, 1:]
+    clear = (gaps > 1e-5) | (gaps == 0)              # exact ties (equal logits) break by expert id on both sides
+    set_ok = clear[:, k - 1] if sel.shape[1] > k else np.ones(sel.shape[0], bool)
+    return set_ok, set_ok & clear[:, :k - 1].all(axis=1)
+
+
+@pytest.mark.parametrize("T,E,k,dt,ids_dt,renorm,with_bias", [
+    (8192, 288, 8, torch.float32, torch.int64, True, True),         # the headline router (GLM-5.3-Flash)
+    (1000, 288, 8, torch.bfloat16, torch.int32, True, True),
+    (777, 1024, 16, torch.float16, torch.int64, False, False),
+    (64, 8, 1, torch.float32, torch.int32, True, True),
+    (0, 288, 8, torch.float32, torch.int64, True, True)])
+def test_route_topk(dev, T, E, k, dt, ids_dt, renorm, with_bias):
+    rng = np.random.default_rng(T + E)
+    lg = torch.from_numpy((rng.standard_normal((T, E)) * 2).astype(np.float32)).to(dt)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32) if with_bias else None
+    ids, w = gp.route_topk(lg.to(dev), t16(bias, dev) if with_bias else None, k, 2.5, renorm, ids_dt)
+    assert ids.dtype == ids_dt and w.dtype == torch.float32 and tuple(ids.shape) == (T, k)
+    if T == 0:
+        return
+    lg32 = lg.float().numpy()
+    rid, rw = O.route_topk(lg32, bias, k, 2.5, renorm)
+    set_ok, order_ok = _margins(lg32, bias, k)
+    assert set_ok.mean() > 0.95 and order_ok.mean() > 0.8
+    gid = ids.cpu().numpy().astype(np.int64)
+    gw = w.cpu().numpy()
+    assert np.array_equal(gid[order_ok], rid[order_ok])                 # same experts in the same order
+    # same experts with the same weights wherever the chosen set is unambiguous (pair weights with ids)
+    gi, ri = np.argsort(gid[set_ok], axis=1), np.argsort(rid[set_ok], axis=1)
+    assert np.array_equal(np.take_along_axis(gid[set_ok], gi, 1), np.take_along_axis(rid[set_ok], ri, 1))
+    assert np.allclose(np.take_along_axis(gw[set_ok], gi, 1), np.take_along_axis(rw[set_ok], ri, 1), rtol=2e-6,
+                       atol=1e-7)
+
+
+def test_route_topk_nan_and_feeds_sort(dev):
+    T, E, k = 300, 64, 8
+    rng = np.random.default_rng(3)
+    lg = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+    lg[7, :] = np.nan
+    lg[7, [3, 5]] = 1.0                                             # only two finite candidates
+    ids, w = gp.route_topk(t16(lg, dev), None, k, 1.0)
+    gid = ids.cpu().numpy()
+    assert gid[7, :2].tolist() == [3, 5] and (gid[7, 2:] == -1).all() and (w.cpu().numpy()[7, 2:] == 0).all()
+    assert not np.isnan(w.cpu().numpy()).any()
+    # the ids and weights go straight into the sort; the dropped -1 routes are counted, not placed
+    R = T * k
+    ts = torch.empty(R, dtype=torch.int64, device=dev)
+    ws = torch.empty(R, dtype=torch.float16, device=dev)
+    eor = torch.empty(R, dtype=torch.int32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    row0 = torch.empty(E, dtype=torch.int32, device=dev)
+    gp.sort_routes(ids, w, E, ts, ws, eor, counts, row0)
+    assert int(counts.sum()) == R - 6
+
+
+def test_prefill_from_router_logits(dev):
+    """Router top-k on the GPU feeding the grouped path equals the staged oracle on the oracle's routing."""
+    L, x, _, _, cfg = synth.make_config("tiny", seed=4)
+    rng = np.random.default_rng(4)
+    lg = (rng.standard_normal((cfg["T"], cfg["E"])) * 2).astype(np.float32)
+    bias = (rng.standard_normal(cfg["E"]) * 0.1).astype(np.float32)
+    rid, rw = O.route_topk(lg, bias, cfg["topk"], 2.5)
+    set_ok, order_ok = _margins(lg, bias, cfg["topk"])
+    assert order_ok.all()
+    TL = synth.to_device(L, dev)
+    got = rt.grouped_prefill_from_logits(t16(x, dev), t16(lg, dev), TL, LIMIT, t16(bias, dev), cfg["topk"], 2.5)
+    ref = O.grouped_prefill(x, rid, rw, to_np_layer(L), LIMIT)
+    assert O.rel_l2(got.cpu().numpy(), ref) < 1e-4
+
+
 # ------------------------------------------------------------------------------------------- Hadamard passes
 @pytest.mark.parametrize("gather", [True, False])
 def test_row_had(dev, gather):

@@ -319,3 +319,27 @@ def test_tiny_golden_fixture():
         assert np.all(d <= np.abs(g[k].astype(np.float32)) * 2 ** -10 + 1e-6), k
     assert O.rel_l2(out, g["out"]) < 1e-5
     assert O.rel_l2(O.expert_loop(x, ids, w, layer, 10.0), g["loop"]) < 1e-5
+
+
+# ------------------------------------------------------------------------------------------- router top-k
+def test_route_topk_brute_force():
+    rng = np.random.default_rng(5)
+    T, E, k = 40, 37, 5
+    logits = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+    logits[3] = -5.0
+    logits[3, [20, 9, 4]] = 1.25                                   # exact ties: lower expert id first
+    bias = (rng.standard_normal(E) * 0.2).astype(np.float32)
+    bias[[4, 9, 20]] = 0
+    ids, w = O.route_topk(logits, bias, k, 2.5)
+    for t in range(T):
+        s = [1.0 / (1.0 + math.exp(-float(v))) for v in logits[t]]
+        sel = [float(np.float32(np.float32(s[e]) + bias[e])) for e in range(E)]
+        want = sorted(range(E), key=lambda e: (-sel[e], e))[:k]
+        assert ids[t].tolist() == want
+        sc = np.float32([s[e] for e in want])
+        assert abs(float(w[t].sum()) - 2.5) < 1e-5                     # renormalised un-biased scores
+        assert np.allclose(w[t], sc / sc.sum() * 2.5, rtol=1e-6)
+    assert ids[3, :3].tolist() == [4, 9, 20]
+    _, w_raw = O.route_topk(logits, bias, k, 2.5, renorm=False)
+    s_sel = 1.0 / (1.0 + np.exp(-np.take_along_axis(logits.astype(np.float64), ids, 1)))
+    assert np.allclose(w_raw, s_sel * 2.5, rtol=1e-6)                  # the bias only selects, never weighs
