@@ -219,6 +219,22 @@ def test_prefill_from_router_logits(dev):
     assert O.rel_l2(got.cpu().numpy(), ref) < 1e-4
 
 
+def test_checkpoint_tp_ranks_on_gpu(dev, tmp_path):
+    """A layer written in the EXL3 checkpoint layout, loaded for two tensor-parallel ranks straight onto the GPU:
+    the ranks' grouped_prefill outputs sum to the unsliced layer's (the all-reduce), and match the oracle."""
+    from exl3_grouped import checkpoint as C
+    L = synth.make_layer(E=8, H=512, I=512, bits=4, seed=21, svh_scale=1 / 16)
+    C.write_moe_layer(str(tmp_path), 5, L.w13_trellis, L.w13_suh, L.w13_svh, L.w2_trellis, L.w2_suh, L.w2_svh)
+    x = synth.make_x(256, 512, 21)
+    ids, w = synth.routing_softmax(256, 8, 4, 21)
+    xt, it, wt = t16(x, dev), t16(ids, dev), t16(w, dev)
+    full = rt.grouped_prefill(xt, it, wt, C.load_moe_layer(str(tmp_path), 5, device=dev), LIMIT)
+    parts = [rt.grouped_prefill(xt, it, wt, C.load_moe_layer(str(tmp_path), 5, tp_rank=r, tp=2, device=dev), LIMIT)
+             for r in range(2)]
+    assert O.rel_l2((parts[0] + parts[1]).cpu().numpy(), full.cpu().numpy()) < 1e-5
+    assert O.rel_l2(full.cpu().numpy(), O.expert_loop(x, ids, w, to_np_layer(L), LIMIT)) < 1e-3
+
+
 # ------------------------------------------------------------------------------------------- Hadamard passes
 @pytest.mark.parametrize("gather", [True, False])
 def test_row_had(dev, gather):
