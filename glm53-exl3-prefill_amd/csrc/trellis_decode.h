@@ -25,8 +25,8 @@ constexpr uint32_t MCG_MASK = 0x8FFF8FFFu;
 // gfx950 forwards a VALU result written through an SDWA destination select (a partial-register write) to the
 // next instruction stale: the consumer must be at least one instruction later. The compiler's hazard recognizer
 // cannot see inside an asm statement, so every SDWA result below is consumed only by a VALU instruction of the same
-// asm block at least one instruction later, and every register an asm block hands back is written by a plain
-// (non-SDWA) instruction, whatever the compiler places after the block. Inputs of these blocks must likewise not come
+// asm block at least one instruction later, and a block whose last writes are SDWA ends with an s_nop, so whatever the
+// compiler places after the block reads them at least one wait state later. Inputs of these blocks must likewise not come
 // from instructions with wait-state rules of their own (per-lane 64-bit shifts fed into them gave wrong results at
 // random): callers hand them 32-bit funnel shifts, loads and DPP moves.
 
@@ -51,20 +51,18 @@ __device__ __forceinline__ void mcg_mul2(uint32_t ra, uint32_t rb, uint32_t& x0,
 
 __device__ __forceinline__ uint32_t mcg_mask(uint32_t x) { return (x & MCG_MASK) ^ MCG_XOR; }
 
-// Two packed fp16 pairs: w0 = {fp16(ya.lo + ya.hi), fp16(yb.lo + yb.hi)}, w1 = {same for yc, yd}. Each sum goes to its
-// half of a zero-padded temporary by SDWA and the pairs are joined by full-register ORs, so no register the compiler
-// sees was last written through SDWA.
+// Two packed fp16 pairs: w0 = {fp16(ya.lo + ya.hi), fp16(yb.lo + yb.hi)}, w1 = {same for yc, yd}. The low halves are
+// written first (upper half zeroed), then the high halves with the low ones preserved -- each read-modify-write two
+// instructions after the write it reads -- and an s_nop guards the last partial write.
 __device__ __forceinline__ void add_halves_2pairs(uint32_t ya, uint32_t yb, uint32_t yc, uint32_t yd,
                                                   uint32_t& w0, uint32_t& w1)
 {
-    uint32_t a, b, c, d;
-    asm("v_add_f16_sdwa %2, %6, %6 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-        "v_add_f16_sdwa %3, %7, %7 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-        "v_add_f16_sdwa %4, %8, %8 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-        "v_add_f16_sdwa %5, %9, %9 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-        "v_or_b32 %0, %2, %3\n\t"
-        "v_or_b32 %1, %4, %5"
-        : "=&v"(w0), "=&v"(w1), "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d) : "v"(ya), "v"(yb), "v"(yc), "v"(yd));
+    asm("v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %1, %4, %4 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %0, %3, %3 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %1, %5, %5 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "s_nop 1"
+        : "=&v"(w0), "=&v"(w1) : "v"(ya), "v"(yb), "v"(yc), "v"(yd));
 }
 
 // Decoded chunk, as four packed fp16 pairs ordered for a [n][k] (k-contiguous) destination:
