@@ -12,6 +12,8 @@ average duration on the launch stream); cpu_baseline = the CPU oracle's expert l
 
   python bench.py [--steps K] [--warmup W] [--tokens T] [--bits B] [--routing R] [--no-cpu-baseline]
   python bench.py --sweep          (extra lines for T = 1024, 2048, 4096, 8192; not the driver's contract line)
+  python bench.py --decode         (the decode path, moe_decode, at small batches of the same layer: one line per
+                                    batch, eager and graph-replayed; not the driver's contract line)
 """
 import argparse
 import json
@@ -41,6 +43,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-seconds", type=float, default=20.0)
     ap.add_argument("--sweep", action="store_true")
+    ap.add_argument("--decode", action="store_true", help="time the decode path (moe_decode) at small batches")
+    ap.add_argument("--decode-tokens", default="1,4,16,32,64,128")
     ap.add_argument("--stages", action="store_true", help="print per-stage ms to stderr")
     ap.add_argument("--scatter", choices=["atomic", "combine"], default=None,
                     help="down-projection output method (default: the runtime's, EXL3_GROUPED_SCATTER or atomic)")
@@ -195,11 +199,73 @@ def cpu_baseline(inputs, seconds: float):
             "ms_per_layer_extrapolated": round(total / rows * counts.sum() * 1e3, 1)}
 
 
+def decode_bench(args):
+    """moe_decode on the config-3 layer (E=288, H=4096, I=768) at small batches with softmax top-8 routing: HIP-event
+    time per call, eager and replayed from a captured graph, beside the prefill path at the same batch. Its bound is
+    the trellis stream of the active experts (HBM) and their decode (VALU): bytes = active experts x 3 H I bits / 8
+    plus their sign / scale vectors, x and out."""
+    import numpy as np
+    import torch
+    import exl3_grouped as gp
+    import exl3_grouped_runtime as rt
+    from exl3_grouped import synth
+
+    dev = torch.device("cuda:0")
+    L, _, _, _, cfg = synth.make_config("layer1k", seed=args.seed, T=1, bits=args.bits)
+    TL = synth.to_device(L, dev)
+    E, H, I, k, bits = cfg["E"], cfg["H"], cfg["I"], cfg["topk"], cfg["bits"]
+    for T in [int(t) for t in args.decode_tokens.split(",")]:
+        ids_np, w_np = synth.make_routing("softmax", T, E, k, seed=args.seed + T)
+        x = torch.from_numpy(synth.make_x(T, H, args.seed + T)).to(dev).half()
+        ids = torch.from_numpy(ids_np).to(dev)
+        w = torch.from_numpy(w_np).to(dev)
+        out = torch.empty(T, H, dtype=torch.float32, device=dev)
+        ws = torch.empty(gp.moe_decode_workspace_bytes(T, k, E, H, I), dtype=torch.uint8, device=dev)
+
+        def call():
+            gp.moe_decode(x, ids, w, TL.w13_trellis, TL.w13_suh, TL.w13_svh, TL.w2_trellis, TL.w2_suh, TL.w2_svh,
+                          10.0, out=out, workspace=ws)
+
+        def timed(fn, n):
+            for _ in range(args.warmup):
+                fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(n):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) * 1e3 / n
+
+        n = max(args.steps, 20)
+        eager_us = timed(call, n)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            call()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            call()
+        graph_us = timed(g.replay, n)
+        prefill_us = timed(lambda: rt.grouped_prefill(x, ids, w, TL, 10.0), n)
+        active = int(np.unique(ids_np).size)
+        nbytes = active * (3 * H * I * bits // 8 + (H + 2 * I + I + H) * 2) + T * H * 2 + T * H * 4
+        print(json.dumps({"metric": "decode-path MoE us per layer", "tokens": T, "topk": k, "active_experts": active,
+                          "eager_us": round(eager_us, 2), "graph_us": round(graph_us, 2),
+                          "prefill_path_us": round(prefill_us, 2), "bytes": nbytes,
+                          "hbm_frac_graph": round(nbytes / (graph_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+                          "config": {"workload": f"layer1k weights: E={E} H={H} I={I} {bits}bpw top{k} softmax"}}),
+              flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path would shard "
-              "as TP (all-reduce) or EP (all-to-all) across GPUs, see DESIGN.md", file=sys.stderr)
+              "as TP (an all-reduce of the fp32 outputs) or EP (an all-to-all of routed rows) across GPUs",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
@@ -207,6 +273,9 @@ def main():
         sys.exit(1)
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.decode:
+        decode_bench(args)
         return
     if args.sweep:
         for T in (1024, 2048, 4096, 8192):

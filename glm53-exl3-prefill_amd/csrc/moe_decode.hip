@@ -1,0 +1,176 @@
+// Decode-path MoE: the whole routed-expert op for small batches (the `tokens <= cap` side of the reference's switch,
+// kernel/exl3_grouped_runtime.py:93-98, where the overlay calls exllamav3's fused exl3_moe,
+// kernel/tuned-fused-kernel-patch/exl3patch/exllamav3/exllamav3_ext/quant/exl3_moe.cu:133-345).
+//
+// Same stages and rounding points as the grouped prefill -- route sort, gather + input Hadamard, gate|up GEMM,
+// activation + Hadamard, down GEMM with scatter -- on a fixed launch sequence whose grids depend on the sizes only:
+//   * The row-tile table is bounded by min(E, R) + R / 128 entries (every expert with rows adds at most one partial
+//     tile), so a batch of a few tokens launches a few dozen row tiles instead of one per expert.
+//   * A batch of a few tokens has too few (row tile, column tile) pairs to fill the GPU, so both GEMMs split K into
+//     slices (chosen from the sizes so that about two workgroups per CU are resident) and add their partial sums
+//     with fp32 atomics: gate|up into an fp32 buffer (rounded to fp16 where act_had reads it, the reference's fp16
+//     gu), down straight into the output rows.
+//   * Everything lives in one caller-provided workspace; buffers that accumulate are cleared by a fill kernel (no
+//     memset nodes), and nothing is read back to the host, so a caller may capture the call in a HIP graph.
+#include <algorithm>
+
+#include "exl3_common.h"
+
+namespace exl3 {
+namespace {
+
+constexpr int DECODE_TILE_ROWS = 128;
+
+__global__ __launch_bounds__(256)
+void zero2_kernel(float4* __restrict__ a, int64_t na, float4* __restrict__ b, int64_t nb)
+{
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < na + nb; i += (int64_t) gridDim.x * 256)
+    {
+        if (i < na) a[i] = z;
+        else b[i - na] = z;
+    }
+}
+
+int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
+
+struct DecodeLayout
+{
+    int64_t sort_ws, token_sorted, weight_sorted, expert_of_row, counts, expert_row0, block_expert, block_row0, meta,
+        h13, gu, act, total;
+    int64_t sort_ws_bytes;
+    int max_blocks;
+};
+
+DecodeLayout decode_layout(int64_t tokens, int topk, int n_experts, int hidden, int inter)
+{
+    const int64_t R = tokens * topk;
+    const int64_t r16 = (R + 15) / 16 * 16;
+    DecodeLayout L{};
+    L.max_blocks = (int) (std::min<int64_t>(n_experts, R) + R / DECODE_TILE_ROWS);
+    L.sort_ws_bytes = (int64_t) exl3_sort_routes_workspace_bytes(tokens, topk, n_experts);
+    int64_t o = 0;
+    auto take = [&](int64_t bytes) { const int64_t at = o; o += align256(bytes); return at; };
+    L.sort_ws = take(L.sort_ws_bytes);
+    L.token_sorted = take(R * 8);
+    L.weight_sorted = take(R * 2);
+    L.expert_of_row = take(R * 4);
+    L.counts = take((int64_t) n_experts * 4);
+    L.expert_row0 = take((int64_t) n_experts * 4);
+    L.block_expert = take((int64_t) L.max_blocks * 4);
+    L.block_row0 = take((int64_t) L.max_blocks * 4);
+    L.meta = take(8);
+    L.h13 = take(r16 * hidden * 2);
+    L.gu = take(R * 2 * (int64_t) inter * 4);
+    L.act = take(r16 * inter * 2);
+    L.total = o;
+    return L;
+}
+
+// Workgroups a launch should put on the device: two resident 256-thread GEMM workgroups per CU.
+int target_workgroups(hipStream_t)
+{
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+    if (cus[dev] == 0)
+    {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return 2 * cus[dev];
+}
+
+// K slices for a launch of `wgs` workgroups over `stages` 32-wide K stages: enough to reach `target`, each slice at
+// least 2 stages.
+int k_split_for(int64_t wgs, int stages, int target)
+{
+    if (wgs <= 0) return 1;
+    int64_t s = (target + wgs - 1) / wgs;
+    s = std::max<int64_t>(1, std::min<int64_t>(s, stages / 2));
+    return (int) s;
+}
+
+}  // namespace
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" int64_t exl3_moe_decode_workspace_bytes(int64_t tokens, int topk, int n_experts, int hidden, int inter)
+{
+    if (tokens < 0 || topk <= 0 || n_experts <= 0 || n_experts > MAX_EXPERTS || hidden <= 0 || inter <= 0) return -1;
+    return decode_layout(tokens, topk, n_experts, hidden, inter).total;
+}
+
+extern "C" int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, const void* topk_ids, int ids_dtype,
+                               const void* topk_weights, int weights_dtype, int topk, int n_experts, int inter,
+                               int bits, const uint16_t* packed_gate, const uint16_t* packed_up,
+                               int64_t w13_expert_stride_words, const uint16_t* suh_gate, int64_t suh13_stride,
+                               const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh13_stride,
+                               const uint16_t* packed_down, int64_t w2_expert_stride_words, const uint16_t* suh_down,
+                               int64_t suh2_stride, const uint16_t* svh_down, int64_t svh2_stride, float limit,
+                               float* out, void* workspace, int64_t workspace_bytes, void* stream)
+{
+    EXL3_CHECK(tokens >= 0 && topk > 0, "bad routing shape");
+    EXL3_CHECK(hidden > 0 && hidden % 128 == 0 && inter > 0 && inter % 128 == 0,
+               "hidden and intermediate sizes must be multiples of 128");
+    EXL3_CHECK(n_experts > 0 && n_experts <= MAX_EXPERTS, "too many experts");
+    EXL3_CHECK(bits >= 2 && bits <= 4, "unsupported bits %d (2, 3 or 4)", bits);
+    EXL3_CHECK(tokens * topk < ((int64_t) 1 << 31), "too many routes");
+    if (tokens == 0) return EXL3_OK;
+    EXL3_CHECK(x && topk_ids && topk_weights && packed_gate && packed_up && suh_gate && svh_gate && svh_up &&
+               packed_down && suh_down && svh_down && out && workspace, "null pointer");
+    EXL3_CHECK((reinterpret_cast<uintptr_t>(out) & 15) == 0 && (reinterpret_cast<uintptr_t>(workspace) & 255) == 0,
+               "out must be 16-byte and the workspace 256-byte aligned");
+    const DecodeLayout L = decode_layout(tokens, topk, n_experts, hidden, inter);
+    EXL3_CHECK(workspace_bytes >= L.total, "decode workspace too small (%lld < %lld bytes)",
+               (long long) workspace_bytes, (long long) L.total);
+    hipStream_t s = as_stream(stream);
+    char* ws = reinterpret_cast<char*>(workspace);
+    auto at = [&](int64_t off) { return reinterpret_cast<void*>(ws + off); };
+    const int64_t R = tokens * topk;
+    auto* token_sorted = reinterpret_cast<int64_t*>(at(L.token_sorted));
+    auto* weight_sorted = reinterpret_cast<uint16_t*>(at(L.weight_sorted));
+    auto* expert_of_row = reinterpret_cast<int32_t*>(at(L.expert_of_row));
+    auto* counts = reinterpret_cast<int32_t*>(at(L.counts));
+    auto* expert_row0 = reinterpret_cast<int32_t*>(at(L.expert_row0));
+    auto* block_expert = reinterpret_cast<int32_t*>(at(L.block_expert));
+    auto* block_row0 = reinterpret_cast<int32_t*>(at(L.block_row0));
+    auto* meta = reinterpret_cast<int32_t*>(at(L.meta));
+    auto* h13 = reinterpret_cast<uint16_t*>(at(L.h13));
+    auto* gu = reinterpret_cast<float*>(at(L.gu));
+    auto* act = reinterpret_cast<uint16_t*>(at(L.act));
+
+    // accumulation targets: out [tokens, hidden] and gu [R, 2 inter], both whole float4s
+    const int64_t n_out4 = tokens * hidden / 4, n_gu4 = R * 2 * inter / 4;
+    const int64_t zgrid = std::min<int64_t>((n_out4 + n_gu4 + 255) / 256, 2048);
+    zero2_kernel<<<(unsigned) zgrid, 256, 0, s>>>(reinterpret_cast<float4*>(out), n_out4,
+                                                  reinterpret_cast<float4*>(gu), n_gu4);
+    int rc = hip_status("moe_decode zero");
+    if (rc) return rc;
+    rc = exl3_sort_routes(topk_ids, ids_dtype, topk_weights, weights_dtype, tokens, topk, n_experts, token_sorted,
+                          weight_sorted, expert_of_row, nullptr, counts, expert_row0, at(L.sort_ws),
+                          (size_t) L.sort_ws_bytes, stream);
+    if (rc) return rc;
+    rc = exl3_build_tiles(counts, n_experts, DECODE_TILE_ROWS, L.max_blocks, block_expert, block_row0, meta, stream);
+    if (rc) return rc;
+    rc = exl3_row_had_ex(x, h13, token_sorted, expert_of_row, suh_gate, suh13_stride, hidden, R, hidden, 1,
+                         EXL3_LAYOUT_T16, stream);
+    if (rc) return rc;
+    const int target = target_workgroups(s);
+    const int gu_split = k_split_for((int64_t) L.max_blocks * 2 * (inter / 128), hidden / 32, target);
+    rc = exl3_grouped_gemm_split(h13, R, hidden, EXL3_LAYOUT_T16, packed_gate, packed_up, w13_expert_stride_words,
+                                 hidden / 16, inter / 16, bits, svh_gate, svh_up, svh13_stride, block_expert,
+                                 block_row0, L.max_blocks, DECODE_TILE_ROWS, counts, expert_row0, n_experts,
+                                 token_sorted, weight_sorted, nullptr, gu, R, EXL3_GEMM_ATOMIC_F32, gu_split, stream);
+    if (rc) return rc;
+    rc = exl3_act_had_f32(gu, 2 * (int64_t) inter, act, expert_of_row, suh_down, suh2_stride, R, inter, limit, stream);
+    if (rc) return rc;
+    const int down_split = k_split_for((int64_t) L.max_blocks * (hidden / 128), inter / 32, target);
+    return exl3_grouped_gemm_split(act, R, inter, EXL3_LAYOUT_T16, packed_down, nullptr, w2_expert_stride_words,
+                                   inter / 16, hidden / 16, bits, svh_down, nullptr, svh2_stride, block_expert,
+                                   block_row0, L.max_blocks, DECODE_TILE_ROWS, counts, expert_row0, n_experts,
+                                   token_sorted, weight_sorted, nullptr, out, tokens, EXL3_GEMM_SCATTER_F32,
+                                   down_split, stream);
+}

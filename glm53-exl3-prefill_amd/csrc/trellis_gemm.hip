@@ -55,7 +55,10 @@ static_assert(UNROLL % 2 == 0 && UNROLL % RAW_DEPTH == 0 && UNROLL % ACT_DEPTH =
 
 // STORE_F16: fp16 rows (gate|up). SCATTER_F32: fp32 atomic add into out[token[r]]. STORE_F32: fp32 rows (fat GEMM).
 // STORE_ROUTE_F32: fp32 rows at out[route_index[r]] (per-route partials for the deterministic combine).
-enum { MODE_STORE_F16 = 0, MODE_SCATTER_F32 = 1, MODE_STORE_F32 = 2, MODE_STORE_ROUTE_F32 = 3 };
+// ATOMIC_F32: fp32 atomic add into out[r] (gate|up partial sums of a split-K launch).
+enum { MODE_STORE_F16 = 0, MODE_SCATTER_F32 = 1, MODE_STORE_F32 = 2, MODE_STORE_ROUTE_F32 = 3, MODE_ATOMIC_F32 = 4 };
+// Modes whose epilogue stages rows through LDS and adds them to the output with atomics.
+constexpr bool atomic_mode(int mode) { return mode == MODE_SCATTER_F32 || mode == MODE_ATOMIC_F32; }
 
 struct GemmParams
 {
@@ -78,6 +81,8 @@ struct GemmParams
     int n_groups;                  // row tiles (grouped: table entries; dense: ceil(m / tile_rows))
     int n_slots;                   // 128-col tiles over all tensors
     int n_tiles_each;              // 128-col tiles per tensor
+    int k_split;                   // K slices per output tile (0 or 1: none); slices add into the output atomically
+    int kb_per_split;              // TILE_K stages per slice (even)
     int64_t m;                     // dense rows
     const int64_t* token;          // scatter destination row per sorted row
     const uint16_t* route_weight;  // fp16 per sorted row
@@ -138,14 +143,27 @@ __device__ __forceinline__ void static_for(F&& f) { static_for_from<0, N>(f); }
 struct Tile
 {
     int e, row0, rows_valid, which, nt;
+    int kb0, num_kb;               // the workgroup's K slice: TILE_K stages kb0 .. kb0 + num_kb - 1
     const uint32_t* packed;        // the tensor's trellis for expert e
     const uint16_t* svh;           // svh of the tile's 128 output columns
 };
 
+// `slot` runs over n_slots x k_split: the column tile, then the K slice.
 template <bool DENSE>
 __device__ __forceinline__ bool resolve_tile(const GemmParams& p, int group, int slot, Tile& t)
 {
     if (group >= p.n_groups) return false;
+    const int total_kb = p.size_k / TILE_K;
+    t.kb0 = 0;
+    t.num_kb = total_kb;
+    if (p.k_split > 1)
+    {
+        const int ks = slot / p.n_slots;
+        slot -= ks * p.n_slots;
+        t.kb0 = ks * p.kb_per_split;
+        t.num_kb = min(p.kb_per_split, total_kb - t.kb0);
+        if (t.num_kb <= 0) return false;
+    }
     if constexpr (DENSE)
     {
         t.e = 0;
@@ -193,7 +211,7 @@ struct Decoder
         const int kt = dw >> 1;
         const int nt8 = 4 * (dw & 1) + (lane >> 4);
         stage_bytes = 2 * p.tiles_n * NDW * 4;
-        const int64_t first = ((int64_t) kt * p.tiles_n + t.nt * 8 + 4 * (dw & 1)) * NDW;
+        const int64_t first = ((int64_t) (2 * t.kb0 + kt) * p.tiles_n + t.nt * 8 + 4 * (dw & 1)) * NDW;
         raw = buffer_rsrc(t.packed + first, ((int64_t) (p.size_k >> 4) * p.tiles_n * NDW - first) * 4);
         last_kb = num_kb - 1;
         const int tile_off = (lane >> 4) * NDW;
@@ -287,7 +305,7 @@ struct Decoder1
         const int kt = dw >> 2;
         const int nt8 = 2 * (dw & 3) + (lane >> 5);
         stage_bytes = 2 * p.tiles_n * NDW * 4;
-        const int64_t first = ((int64_t) kt * p.tiles_n + t.nt * 8 + 2 * (dw & 3)) * NDW;
+        const int64_t first = ((int64_t) (2 * t.kb0 + kt) * p.tiles_n + t.nt * 8 + 2 * (dw & 3)) * NDW;
         raw = buffer_rsrc(t.packed + first, ((int64_t) (p.size_k >> 4) * p.tiles_n * NDW - first) * 4);
         last_kb = num_kb - 1;
         const int b0 = 8 * c * BITS + BITS - 16;              // first window bit, >= -15
@@ -346,7 +364,8 @@ struct Mma
         const int tok = lane & 15, kq = lane >> 4;
         a_step = p.a_t16 ? 4 * 128 * 2 : TILE_K * 2;          // bytes per stage
         const int g0 = t.row0 >> 4;
-        const int64_t base_el = p.a_t16 ? (int64_t) g0 * (p.size_k >> 3) * 128 : (int64_t) t.row0 * p.size_k;
+        const int64_t base_el = (p.a_t16 ? (int64_t) g0 * (p.size_k >> 3) * 128 : (int64_t) t.row0 * p.size_k) +
+                                (int64_t) t.kb0 * (a_step / 2);       // the slice's first stage
         const int64_t total_el = (p.a_t16 ? (p.a_rows + 15) / 16 * 16 : p.a_rows) * p.size_k;
         a_rsrc = buffer_rsrc(p.a + base_el, (total_el - base_el) * 2);
         #pragma unroll
@@ -438,7 +457,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
             float v[4];
             #pragma unroll
             for (int r = 0; r < 4; ++r) v[r] = x[4 * nb + r] * sv[4 * nb + r] * rw;
-            if constexpr (MODE == MODE_SCATTER_F32)
+            if constexpr (atomic_mode(MODE))
             {
                 *reinterpret_cast<float4*>(stage + tok * SC_ROW + col) = make_float4(v[0], v[1], v[2], v[3]);
                 continue;
@@ -458,10 +477,11 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
                 *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
             }
         }
-        if constexpr (MODE == MODE_SCATTER_F32)
+        if constexpr (atomic_mode(MODE))
         {
             // LDS accesses of one wave complete in order: the reads below see the writes above, and the next
-            // group's writes land after these reads. Lane t (< 16) holds row t's destination token.
+            // group's writes land after these reads. Lane t (< 16) holds row t's destination row (token, or the
+            // sorted row itself in ATOMIC_F32).
             const int nrows = min(16, rows_w - 16 * mb);
             const uint32_t tok_lo = (uint32_t) orow, tok_hi = (uint32_t) ((uint64_t) orow >> 32);
             float* outp = reinterpret_cast<float*>(p.out) + out_col0 + lane;
@@ -490,17 +510,17 @@ __global__ __launch_bounds__(256, 2)
 void trellis_gemm_kernel(const GemmParams p)
 {
     constexpr int SCB = lds_scatter_bytes<4>();
-    constexpr int LDS_BYTES = (MODE == MODE_SCATTER_F32 && SCB > LDS_MAIN_BYTES) ? SCB : LDS_MAIN_BYTES;
+    constexpr int LDS_BYTES = (atomic_mode(MODE) && SCB > LDS_MAIN_BYTES) ? SCB : LDS_MAIN_BYTES;
     __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
     uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
 
     int group, slot;
-    xcd_group_slot((int) blockIdx.x, p.n_slots, group, slot);
+    xcd_group_slot((int) blockIdx.x, p.k_split > 1 ? p.n_slots * p.k_split : p.n_slots, group, slot);
     Tile t;
     if (!resolve_tile<DENSE>(p, group, slot, t)) return;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int num_kb = p.size_k / TILE_K;
+    const int num_kb = t.num_kb;
     using Dec = Decoder<BITS>;
     constexpr int NR = Dec::NR;
     const Dec dec(p, t, wave, lane, num_kb);
@@ -568,7 +588,7 @@ void trellis_gemm_kernel(const GemmParams p)
     else if (rows_w > 0) mainloop(std::integral_constant<int, 1>{});
     else mainloop(std::integral_constant<int, 0>{});
 
-    if constexpr (MODE == MODE_SCATTER_F32) __syncthreads();     // decoded tiles are dead; LDS becomes staging
+    if constexpr (atomic_mode(MODE)) __syncthreads();            // decoded tiles are dead; LDS becomes staging
     if (rows_w <= 0) return;
     epilogue<MODE>(p, t, wave, lane, acc, reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW));
 }
@@ -587,18 +607,18 @@ __global__ __launch_bounds__(512, 1)
 void trellis_gemm_pp_kernel(const GemmParams p)
 {
     constexpr int SCB = lds_scatter_bytes<8>();
-    constexpr int LDS_BYTES = (MODE == MODE_SCATTER_F32 && SCB > LDS_MAIN_BYTES) ? SCB : LDS_MAIN_BYTES;
+    constexpr int LDS_BYTES = (atomic_mode(MODE) && SCB > LDS_MAIN_BYTES) ? SCB : LDS_MAIN_BYTES;
     __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
     uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
 
     int group, slot;
-    xcd_group_slot((int) blockIdx.x, p.n_slots, group, slot);
+    xcd_group_slot((int) blockIdx.x, p.k_split > 1 ? p.n_slots * p.k_split : p.n_slots, group, slot);
     Tile t;
     if (!resolve_tile<DENSE>(p, group, slot, t)) return;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = wave >> 2;
-    const int num_kb = p.size_k / TILE_K;
+    const int num_kb = t.num_kb;
     using Dec = Decoder1<BITS>;
     const Dec dec(p, t, wave, lane, num_kb);
     const Mma mm(p, t, wave, lane, num_kb);
@@ -786,18 +806,25 @@ __global__ void decode_states_kernel(const uint32_t* __restrict__ states, uint32
     if (i + 1 < n2) out[i + 1] = wb;
 }
 
-// 512-row tiles run the 8-wave ping-pong kernel, 128- and 256-row tiles the 4-wave one.
+// 512-row tiles run the 8-wave ping-pong kernel, 128- and 256-row tiles the 4-wave one (the only one built for
+// ATOMIC_F32, whose split-K launches serve small batches).
 template <int BITS, int MODE, bool DENSE>
 int launch_gemm(const GemmParams& p, hipStream_t s)
 {
     const int groups8 = (p.n_groups + 7) / 8 * 8;
-    const int64_t grid = (int64_t) groups8 * p.n_slots;
+    const int64_t grid = (int64_t) groups8 * p.n_slots * (p.k_split > 1 ? p.k_split : 1);
     if (grid == 0) return EXL3_OK;
     if (grid > 0x7FFFFFFF) return fail("grid too large");
-    if (p.tile_rows > 256)
+    if constexpr (MODE == MODE_ATOMIC_F32)
+    {
+        if (p.tile_rows > 256) return fail("mode 3 (fp32 atomic rows) takes row tiles of at most 256 rows");
+    }
+    else if (p.tile_rows > 256)
+    {
         trellis_gemm_pp_kernel<BITS, MODE, DENSE><<<(unsigned) grid, 512, 0, s>>>(p);
-    else
-        trellis_gemm_kernel<BITS, MODE, DENSE><<<(unsigned) grid, 256, 0, s>>>(p);
+        return EXL3_OK;
+    }
+    trellis_gemm_kernel<BITS, MODE, DENSE><<<(unsigned) grid, 256, 0, s>>>(p);
     return EXL3_OK;
 }
 
@@ -820,15 +847,15 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15)
 
 using namespace exl3;
 
-extern "C" int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,
-                                    const uint16_t* packed_gate, const uint16_t* packed_up,
-                                    int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
-                                    const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
-                                    const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
-                                    int tile_rows, const int32_t* counts, const int32_t* expert_row0,
-                                    int n_experts, const int64_t* token_sorted, const uint16_t* route_weight,
-                                    const int32_t* route_index, void* out, int64_t out_rows, int mode,
-                                    void* stream)
+extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,
+                                       const uint16_t* packed_gate, const uint16_t* packed_up,
+                                       int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
+                                       const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                                       const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
+                                       int tile_rows, const int32_t* counts, const int32_t* expert_row0,
+                                       int n_experts, const int64_t* token_sorted, const uint16_t* route_weight,
+                                       const int32_t* route_index, void* out, int64_t out_rows, int mode,
+                                       int k_split, void* stream)
 {
     EXL3_CHECK(tile_rows == 128 || tile_rows == 256 || tile_rows == 512, "tile_rows must be 128, 256 or 512");
     EXL3_CHECK(a_layout == EXL3_LAYOUT_ROWS || a_layout == EXL3_LAYOUT_T16, "unknown layout");
@@ -858,6 +885,13 @@ extern "C" int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_
     p.tile_rows = tile_rows; p.n_groups = max_blocks; p.n_tiles_each = size_n_each / TILE_N;
     p.n_slots = n_tensors * p.n_tiles_each;
     p.token = token_sorted; p.route_weight = route_weight; p.route_index = route_index; p.out = out;
+    // K slices of an even number of stages each (the main loop runs stages in pairs)
+    const int total_kb = size_k / TILE_K;
+    EXL3_CHECK(k_split >= 1 && k_split <= total_kb / 2, "k_split must be in [1, K / 64]");
+    EXL3_CHECK(k_split == 1 || mode == EXL3_GEMM_SCATTER_F32 || mode == EXL3_GEMM_ATOMIC_F32,
+               "k_split > 1 needs an accumulating mode (1: fp32 atomic scatter, 3: fp32 atomic rows)");
+    p.kb_per_split = ((total_kb + k_split - 1) / k_split + 1) / 2 * 2;
+    p.k_split = (total_kb + p.kb_per_split - 1) / p.kb_per_split;
     hipStream_t s = as_stream(stream);
     int rc;
     if (mode == EXL3_GEMM_STORE_F16)
@@ -882,10 +916,35 @@ extern "C" int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_
         p.out_ld = size_n_each;
         rc = launch_bits<MODE_STORE_ROUTE_F32, false>(bits, p, s);
     }
+    else if (mode == EXL3_GEMM_ATOMIC_F32)
+    {
+        EXL3_CHECK(out_rows >= a_rows, "mode 3: out fp32 [rows, n_tensors*N]");
+        EXL3_CHECK(tile_rows <= 256, "mode 3 takes row tiles of 128 or 256 rows");
+        EXL3_CHECK((reinterpret_cast<uintptr_t>(out) & 3) == 0, "out must be 4-byte aligned");
+        p.out_ld = (int64_t) n_tensors * size_n_each;
+        rc = launch_bits<MODE_ATOMIC_F32, false>(bits, p, s);
+    }
     else
-        return fail("mode must be 0 (fp16 store), 1 (fp32 atomic scatter) or 2 (fp32 per-route store)");
+        return fail("mode must be 0 (fp16 store), 1 (fp32 atomic scatter), 2 (fp32 per-route store) or 3 (fp32 atomic "
+                    "rows)");
     if (rc != EXL3_OK) return rc;
     return hip_status("grouped_gemm");
+}
+
+extern "C" int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,
+                                    const uint16_t* packed_gate, const uint16_t* packed_up,
+                                    int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
+                                    const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                                    const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
+                                    int tile_rows, const int32_t* counts, const int32_t* expert_row0,
+                                    int n_experts, const int64_t* token_sorted, const uint16_t* route_weight,
+                                    const int32_t* route_index, void* out, int64_t out_rows, int mode,
+                                    void* stream)
+{
+    return exl3_grouped_gemm_split(a, a_rows, size_k, a_layout, packed_gate, packed_up, expert_stride_words, tiles_k,
+                                   tiles_n, bits, svh_gate, svh_up, svh_stride, block_expert, block_row0, max_blocks,
+                                   tile_rows, counts, expert_row0, n_experts, token_sorted, route_weight, route_index,
+                                   out, out_rows, mode, 1, stream);
 }
 
 extern "C" int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,

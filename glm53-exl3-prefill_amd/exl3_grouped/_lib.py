@@ -36,10 +36,13 @@ SIGNATURES = {
     "exl3_row_had_ex": (I32, [P, P, P, P, P, I64, I64, I64, I32, I32, I32, P]),
     "exl3_act_had": (I32, [P, I64, P, P, P, I64, I64, I32, F32, P]),
     "exl3_act_had_ex": (I32, [P, I64, P, P, P, I64, I64, I32, F32, I32, P]),
+    "exl3_act_had_f32": (I32, [P, I64, P, P, P, I64, I64, I32, F32, P]),
     "exl3_grouped_gemm": (I32, [P, I64, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, P, P, I32, P, P,
                                 P, P, I64, I32, P]),
     "exl3_grouped_gemm_ex": (I32, [P, I64, I32, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, I32, P, P,
                                    I32, P, P, P, P, I64, I32, P]),
+    "exl3_grouped_gemm_split": (I32, [P, I64, I32, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, I32, P, P,
+                                      I32, P, P, P, P, I64, I32, I32, P]),
     "exl3_combine_routes": (I32, [P, P, P, I32, I32, I64, I32, I64, P]),
     "exl3_fat_gemm": (I32, [P, I64, I32, P, I32, I32, I32, P, I64, P, I64, I32, I32, I32, I32, P]),
     "exl3_fat_gemm_scatter": (I32, [P, I64, I32, P, I32, I32, I32, P, I64, P, I64, P, P, I32, I32, I32, I32, P]),
@@ -49,9 +52,12 @@ SIGNATURES = {
     "exl3_linear": (I32, [P, I64, I32, P, I32, I32, I32, P, P, P, P, I32, P]),
     "exl3_reconstruct": (I32, [P, P, I32, I32, I32, I32, I32, P]),
     "exl3_decode_states": (I32, [P, P, I64, P]),
+    "exl3_moe_decode_workspace_bytes": (I64, [I64, I32, I32, I32, I32]),
+    "exl3_moe_decode": (I32, [P, I64, I32, P, I32, P, I32, I32, I32, I32, I32, P, P, I64, P, I64, P, P, I64, P, I64,
+                              P, I64, P, I64, F32, P, P, I64, P]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib = None
 _path = None

@@ -189,7 +189,8 @@ def row_had(src: torch.Tensor, dst: torch.Tensor, token_sorted: Optional[torch.T
 def act_had(gu: torch.Tensor, act: torch.Tensor, expert_of_row: torch.Tensor, suh_down: torch.Tensor,
             limit: float, dst_layout: int = 0) -> None:
     """kernel/exl3_grouped_prefill.cu:313-322. dst_layout (new): 0 row-major act [rows, I]; 1 T16 (rows = gu rows,
-    act holds t16_rows(rows) rows)."""
+    act holds t16_rows(rows) rows). gu may be fp32 (new; the partial sums of a split-K gate|up, grouped_gemm mode 3),
+    rounded to fp16 on load, with dst_layout 1."""
     I = act.shape[1]
     if dst_layout == 0:
         rows = act.shape[0]
@@ -197,15 +198,20 @@ def act_had(gu: torch.Tensor, act: torch.Tensor, expert_of_row: torch.Tensor, su
         rows = gu.shape[0]
         _check(dst_layout == 1 and act.shape[0] >= t16_rows(rows), "T16 act needs t16_rows(rows) rows")
     _check(gu.size(1) == 2 * I and I % 128 == 0, "gate|up width must be 2I, I multiple of 128")
-    _check(gu.dtype == torch.float16 and act.dtype == torch.float16 and suh_down.dtype == torch.float16,
-           "fp16 tensors")
+    _check(gu.dtype in (torch.float16, torch.float32) and act.dtype == torch.float16 and
+           suh_down.dtype == torch.float16, "fp16 tensors (gu fp16 or fp32)")
+    _check(gu.dtype == torch.float16 or dst_layout == 1, "fp32 gu writes the T16 layout")
     _check(gu.is_contiguous() and act.is_contiguous() and gu.size(0) >= rows, "gu / act must be contiguous")
     _check(suh_down.dim() == 2 and suh_down.size(1) == I and suh_down.stride(1) == 1, "suh_down must be [E, I]")
     _check(expert_of_row.dtype == torch.int32 and expert_of_row.numel() >= rows, "expert_of_row int32 [rows]")
     dev = _require_cuda(gu, act, expert_of_row, suh_down)
     with _On(dev) as s:
-        _lib.call("exl3_act_had_ex", _p(gu), gu.size(1), _p(act), _p(expert_of_row), _p(suh_down),
-                  suh_down.stride(0), rows, I, float(limit), int(dst_layout), s)
+        if gu.dtype == torch.float32:
+            _lib.call("exl3_act_had_f32", _p(gu), gu.size(1), _p(act), _p(expert_of_row), _p(suh_down),
+                      suh_down.stride(0), rows, I, float(limit), s)
+        else:
+            _lib.call("exl3_act_had_ex", _p(gu), gu.size(1), _p(act), _p(expert_of_row), _p(suh_down),
+                      suh_down.stride(0), rows, I, float(limit), int(dst_layout), s)
 
 
 # ------------------------------------------------------------------------------------------- grouped GEMM
@@ -214,14 +220,18 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
                  block_row0: torch.Tensor, counts: torch.Tensor, expert_row0: torch.Tensor,
                  token_sorted: Optional[torch.Tensor], route_weight: Optional[torch.Tensor], out: torch.Tensor,
                  mode: int, route_index: Optional[torch.Tensor] = None, tile_rows: int = 128, a_layout: int = 0,
-                 a_rows: Optional[int] = None) -> None:
+                 a_rows: Optional[int] = None, k_split: int = 1) -> None:
     """kernel/exl3_grouped_prefill.cu:326-378. mode 0: fp16 store; mode 1: fp32 atomic scatter into
     out[token_sorted[r]]; mode 2 (new): fp32 store of the weighted row into out[route_index[r]] (out [T*topk, N]),
-    summed per token by combine_routes in a fixed order. tile_rows (new): rows per block-table entry, 128 for
+    summed per token by combine_routes in a fixed order; mode 3 (new): fp32 atomic add of the unweighted row into
+    out[r] (out [rows, n_tensors*N], caller-zeroed). tile_rows (new): rows per block-table entry, 128 for
     build_blocks' table (the reference's), 256 or 512 for a build_tiles(..., 256 | 512) table (512 runs the 8-wave
     kernel). a_layout (new): 0 row-major a,
-    1 T16 (a from row_had / act_had with dst_layout=1; a_rows gives its logical rows)."""
+    1 T16 (a from row_had / act_had with dst_layout=1; a_rows gives its logical rows). k_split (new): slices of K
+    whose partial products are added into out (modes 1 and 3 only)."""
     _check(int(tile_rows) in (128, 256, 512), "tile_rows must be 128, 256 or 512")
+    _check(int(k_split) >= 1 and int(k_split) <= a.size(1) // 64, "k_split must be in [1, K / 64]")
+    _check(int(k_split) == 1 or mode in (1, 3), "k_split > 1 needs mode 1 or 3")
     _check(a_layout in (0, 1), "unknown layout")
     if a_rows is None:
         a_rows = a.size(0)
@@ -265,18 +275,23 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
                out.is_contiguous(), "mode 2: out fp32 [routes, N], single tensor")
         _check(route_index is not None and route_weight is not None and route_index.dtype == torch.int32 and
                route_weight.dtype == torch.float16, "mode 2 needs route_index (int32) and route_weight (fp16)")
+    elif mode == 3:
+        _check(out.dtype == torch.float32 and out.dim() == 2 and out.size(1) == n_tensors * size_n_each and
+               out.is_contiguous() and out.size(0) >= a_rows, "mode 3: out fp32 [rows, n_tensors*N]")
+        _check(int(tile_rows) <= 256, "mode 3 takes row tiles of 128 or 256 rows")
     else:
-        raise RuntimeError("mode must be 0, 1 or 2")
+        raise RuntimeError("mode must be 0, 1, 2 or 3")
+    weighted = mode in (1, 2)
     dev = _require_cuda(a, packed_gate, packed_up, svh_gate, svh_up, block_expert, block_row0, counts,
-                        expert_row0, out, token_sorted if mode == 1 else None, route_weight if mode else None,
+                        expert_row0, out, token_sorted if mode == 1 else None, route_weight if weighted else None,
                         route_index if mode == 2 else None)
     with _On(dev) as s:
-        _lib.call("exl3_grouped_gemm_ex", _p(a), int(a_rows), size_k, int(a_layout), _p(packed_gate), _p(packed_up),
-                  expert_stride, tiles_k, tiles_n, bits, _p(svh_gate), _p(svh_up), svh_stride, _p(block_expert),
-                  _p(block_row0), max_blocks, int(tile_rows), _p(counts), _p(expert_row0), E,
+        _lib.call("exl3_grouped_gemm_split", _p(a), int(a_rows), size_k, int(a_layout), _p(packed_gate),
+                  _p(packed_up), expert_stride, tiles_k, tiles_n, bits, _p(svh_gate), _p(svh_up), svh_stride,
+                  _p(block_expert), _p(block_row0), max_blocks, int(tile_rows), _p(counts), _p(expert_row0), E,
                   _p(token_sorted) if mode == 1 else None,
-                  _p(route_weight) if mode else None, _p(route_index) if mode == 2 else None, _p(out), out.size(0),
-                  mode, s)
+                  _p(route_weight) if weighted else None, _p(route_index) if mode == 2 else None, _p(out),
+                  out.size(0), mode, int(k_split), s)
 
 
 def combine_routes(partial: torch.Tensor, out: torch.Tensor, topk: int, topk_ids: Optional[torch.Tensor] = None,
@@ -380,6 +395,72 @@ def linear_exl3(x: torch.Tensor, packed: torch.Tensor, suh: torch.Tensor, svh: t
     with _On(dev) as s:
         _lib.call("exl3_linear", _p(x), M, k, _p(packed), packed.size(0), packed.size(1), int(K), _p(suh), _p(svh),
                   _p(work), _p(out), 0 if out_dtype == torch.float32 else 1, s)
+    return out
+
+
+# ------------------------------------------------------------------------------------------- decode path
+def moe_decode_workspace_bytes(tokens: int, topk: int, n_experts: int, hidden: int, inter: int) -> int:
+    """Bytes of the workspace moe_decode needs (sorted routes, tile table, the Hadamard'd rows, fp32 gate|up sums)."""
+    v = int(_lib.load().exl3_moe_decode_workspace_bytes(int(tokens), int(topk), int(n_experts), int(hidden),
+                                                         int(inter)))
+    _check(v >= 0, "bad decode sizes")
+    return v
+
+
+def moe_decode(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, w13_trellis: torch.Tensor,
+               w13_suh: torch.Tensor, w13_svh: torch.Tensor, w2_trellis: torch.Tensor, w2_suh: torch.Tensor,
+               w2_svh: torch.Tensor, limit: float, out: Optional[torch.Tensor] = None,
+               workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode-path MoE (new; replaces the overlay's fused exl3_moe call on the `tokens <= cap` side of
+    kernel/exl3_grouped_runtime.py:93-98): x fp16 [T, H], topk_ids [T, topk] int64/int32, topk_weights [T, topk]
+    fp32/fp16/bf16, the stacked layer tensors (w13_trellis [E, 2, H/16, I/16, 16*bits], w13_suh [E, 2, H] with
+    gate == up, w13_svh [E, 2, I], w2_trellis [E, I/16, H/16, 16*bits], w2_suh [E, I], w2_svh [E, H]) -> out fp32
+    [T, H]. One fixed launch sequence that allocates nothing when `out` and `workspace` (uint8, at least
+    moe_decode_workspace_bytes(...) bytes, 256-byte aligned) are given, so the call can be captured in a graph."""
+    _check(x.dim() == 2 and x.dtype == torch.float16 and x.is_contiguous(), "x must be contiguous fp16 [T, H]")
+    T, H = x.shape
+    _check(topk_ids.dim() == 2 and topk_ids.size(0) == T and topk_weights.shape == topk_ids.shape,
+           "topk_ids / topk_weights must be [T, topk]")
+    _check(topk_ids.dtype in (torch.int64, torch.int32) and topk_ids.is_contiguous(), "topk_ids int64/int32")
+    _check(topk_weights.dtype in (torch.float32, torch.float16, torch.bfloat16) and topk_weights.is_contiguous(),
+           "topk_weights fp32/fp16/bf16")
+    topk = topk_ids.size(1)
+    _check(w13_trellis.dim() == 5 and w13_trellis.size(1) == 2 and w13_trellis.dtype in (torch.int16, torch.uint16),
+           "w13_trellis must be [E, 2, H/16, I/16, 16*bits] int16")
+    E = w13_trellis.size(0)
+    words = w13_trellis.size(4)
+    _check(words in (32, 48, 64), "trellis tile width must be 16*bits words, bits in {2, 3, 4}")
+    bits = words // 16
+    _check(w13_trellis.size(2) * 16 == H, "w13_trellis K must match x")
+    inter = w13_trellis.size(3) * 16
+    g, u = w13_trellis[:, 0], w13_trellis[:, 1]
+    for t in (g, u):
+        _check(t.stride(3) == 1 and t.stride(2) == words and t.stride(1) == t.size(2) * words,
+               "w13_trellis inner dims must be contiguous")
+    _check(w2_trellis.dim() == 4 and w2_trellis.shape == (E, inter // 16, H // 16, words) and
+           w2_trellis.dtype == w13_trellis.dtype and w2_trellis.stride(3) == 1 and w2_trellis.stride(2) == words and
+           w2_trellis.stride(1) == w2_trellis.size(2) * words, "w2_trellis must be [E, I/16, H/16, 16*bits]")
+    _check(w13_suh.shape == (E, 2, H) and w13_svh.shape == (E, 2, inter) and w2_suh.shape == (E, inter) and
+           w2_svh.shape == (E, H), "sign / scale vector shapes")
+    for t in (w13_suh, w13_svh, w2_suh, w2_svh):
+        _check(t.dtype == torch.float16 and t.stride(-1) == 1, "suh / svh must be fp16 with contiguous rows")
+    _check(w13_svh[:, 0].stride() == w13_svh[:, 1].stride(), "gate / up svh strides must match")
+    if out is None:
+        out = torch.empty(T, H, dtype=torch.float32, device=x.device)
+    _check(out.dtype == torch.float32 and tuple(out.shape) == (T, H) and out.is_contiguous(), "out must be fp32 [T, H]")
+    need = moe_decode_workspace_bytes(T, topk, E, H, inter)
+    if workspace is None:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+    _check(workspace.is_contiguous() and workspace.numel() * workspace.element_size() >= need,
+           "decode workspace too small")
+    dev = _require_cuda(x, topk_ids, topk_weights, w13_trellis, w13_suh, w13_svh, w2_trellis, w2_suh, w2_svh, out,
+                        workspace)
+    with _On(dev) as s:
+        _lib.call("exl3_moe_decode", _p(x), T, H, _p(topk_ids), _DT[topk_ids.dtype], _p(topk_weights),
+                  _DT[topk_weights.dtype], topk, E, inter, bits, _p(g), _p(u), g.stride(0), _p(w13_suh[:, 0]),
+                  w13_suh.stride(0), _p(w13_svh[:, 0]), _p(w13_svh[:, 1]), w13_svh.stride(0), _p(w2_trellis),
+                  w2_trellis.stride(0), _p(w2_suh), w2_suh.stride(0), _p(w2_svh), w2_svh.stride(0), float(limit),
+                  _p(out), _p(workspace), workspace.numel() * workspace.element_size(), s)
     return out
 
 

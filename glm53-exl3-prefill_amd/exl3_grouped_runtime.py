@@ -2,12 +2,15 @@
 kernel/exl3_grouped_runtime.py, whose functions and behaviour this module mirrors).
 
 Installed into vLLM's exl3 overlay module by patch_exl3_grouped.py when EXL3_GROUPED_PREFILL != "0".
-Prefill calls (tokens > the fused kernel's row cap) go through one launch per stage over all experts;
-decode calls (tokens <= cap), expert-parallel calls (layer.expert_map set) and layers without w13_trellis keep
-the original path untouched (kernel/exl3_grouped_runtime.py:93-98).
+Prefill calls (tokens > the fused kernel's row cap) go through one launch per stage over all experts
+(kernel/exl3_grouped_runtime.py:93-98). Decode calls (tokens <= cap), which the reference leaves to the overlay's
+fused exl3_moe (a CUDA kernel with no build on this GPU), go to moe_decode: the same stages with split-K GEMMs and a
+per-layer workspace, one fixed launch sequence that a HIP graph can capture. Expert-parallel calls (layer.expert_map
+set) and layers without w13_trellis keep the original path untouched.
 
 Env:
   EXL3_GROUPED_PREFILL=1     enable (read by the hook)
+  EXL3_GROUPED_DECODE=0      leave decode calls (tokens <= cap) to the original path (default: moe_decode)
   EXL3_GROUPED_SCATTER=...   down-projection output: "atomic" (fp32 atomic scatter by token, the reference's
                              method) or "combine" (per-route fp32 rows + a fixed-order sum per token: deterministic)
   EXL3_GROUPED_LIB=<path>    prebuilt libexl3_grouped.so (default: exl3_grouped/libexl3_grouped.so beside this file)
@@ -155,6 +158,32 @@ def grouped_prefill_from_logits(x2d: torch.Tensor, router_logits: torch.Tensor, 
     return grouped_prefill(x2d, ids, weights, layer, limit, scatter=scatter)
 
 
+def decode_enabled() -> bool:
+    return os.environ.get("EXL3_GROUPED_DECODE", "1") != "0"
+
+
+def moe_decode(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, layer, limit: float,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode-path MoE for a small batch: x2d [T, H] (any float dtype), ids [T, topk], weights [T, topk] -> out fp32
+    [T, H]. The workspace lives on the layer (layer._exl3_decode_ws), grown to the largest batch seen and reused, so
+    a call after the first allocates nothing when `out` is given (the first call of each size should run before a
+    graph capture)."""
+    gp = _load_ext()
+    T, H = x2d.shape
+    topk = ids.shape[1]
+    E = int(layer.w13_trellis.shape[0])
+    I = int(layer._exl3_intermediate_local)
+    need = gp.moe_decode_workspace_bytes(T, topk, E, H, I)
+    ws = getattr(layer, "_exl3_decode_ws", None)
+    if ws is None or ws.numel() < need or ws.device != x2d.device:
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=x2d.device)
+        layer._exl3_decode_ws = ws
+    x16 = x2d if x2d.dtype == torch.float16 and x2d.is_contiguous() else x2d.to(torch.float16).contiguous()
+    return gp.moe_decode(x16, ids.contiguous(), weights.contiguous(), layer.w13_trellis, layer.w13_suh,
+                         layer.w13_svh, layer.w2_trellis, layer.w2_suh, layer.w2_svh, float(limit), out=out,
+                         workspace=ws)
+
+
 def install(ov):
     """Wrap ov.apply_exl3_experts: prefill-sized calls use the grouped path; everything else is untouched
     (kernel/exl3_grouped_runtime.py:86-112)."""
@@ -167,11 +196,15 @@ def install(ov):
         temps = getattr(layer, "_exl3_fused_temps", None)
         cap = int(temps[0].shape[1]) if temps else 0
         expert_map = getattr(layer, "expert_map", None)
-        if tokens <= cap or expert_map is not None or not hasattr(layer, "w13_trellis"):
+        if expert_map is not None or not hasattr(layer, "w13_trellis") or (tokens <= cap and not decode_enabled()):
             return original(x, topk_ids, topk_weights, layer, limit=limit, fused=fused)
         x2d = x.reshape(tokens, x.shape[-1])
         ids = topk_ids.reshape(tokens, -1).to(torch.long)
         weights = topk_weights.reshape(tokens, -1)
+        if tokens <= cap:
+            out = moe_decode(x2d, ids, weights, layer, float(limit))
+            layer._exl3_last_apply = "decode"
+            return out.to(dtype=x.dtype)
         out = grouped_prefill(x2d, ids, weights, layer, float(limit))
         layer._exl3_last_apply = "grouped"
         if not _logged:

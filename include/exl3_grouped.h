@@ -45,6 +45,7 @@ extern "C" {
 #define EXL3_GEMM_STORE_F16 0      /* grouped_gemm mode 0: fp16 store into [rows, n_tensors*N] */
 #define EXL3_GEMM_SCATTER_F32 1    /* grouped_gemm mode 1: fp32 atomic add into out[token_sorted[r]] * w[r] */
 #define EXL3_GEMM_STORE_ROUTE_F32 2 /* grouped_gemm mode 2: fp32 store of w[r] * y[r] into out[route_index[r]] */
+#define EXL3_GEMM_ATOMIC_F32 3      /* grouped_gemm mode 3: fp32 atomic add of y[r] into out[r] (split-K gate|up) */
 
 /* Message for the calling thread's last failing call ("" if none). */
 const char* exl3_last_error(void);
@@ -131,6 +132,10 @@ int exl3_act_had(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int3
 int exl3_act_had_ex(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
                     const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, int dst_layout,
                     void* stream);
+/* exl3_act_had_ex(..., EXL3_LAYOUT_T16) reading gate|up as fp32 partial sums (grouped GEMM mode 3), each rounded to
+ * fp16 first -- the reference's fp16 gu -- so the result is what the fp16 gu of the same sums would give. New. */
+int exl3_act_had_f32(const float* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
+                     const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, void* stream);
 
 /*
  * Grouped weight-stationary trellis GEMM over all experts (pybind op grouped_gemm,
@@ -174,6 +179,24 @@ int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_k, int a_la
                          const int32_t* counts, const int32_t* expert_row0, int n_experts,
                          const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
                          void* out, int64_t out_rows, int mode, void* stream);
+
+/*
+ * exl3_grouped_gemm_ex with K split into k_split slices of whole 64-column pairs of stages (new; the decode path's
+ * launches, which have too few output tiles to fill the GPU otherwise). Each slice runs the full epilogue on its
+ * partial product and adds it to the output, so k_split > 1 needs an accumulating mode: EXL3_GEMM_SCATTER_F32, or
+ * EXL3_GEMM_ATOMIC_F32 -- out fp32 [a_rows, n_tensors*N_each], caller-zeroed,
+ *        out[r, which*N_each + n] += H128_n(a[r] @ W'_e,which) / sqrt(128) * svh_e,which[n]
+ * (valid with k_split == 1 too; tile_rows 128 or 256). 1 <= k_split <= size_k / 64; the slice count used is
+ * ceil(K_stages / per_slice) with per_slice = ceil(K_stages / k_split) rounded up to even (K_stages = size_k / 32).
+ */
+int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,
+                            const uint16_t* packed_gate, const uint16_t* packed_up, int64_t expert_stride_words,
+                            int tiles_k, int tiles_n, int bits,
+                            const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                            const int32_t* block_expert, const int32_t* block_row0, int max_blocks, int tile_rows,
+                            const int32_t* counts, const int32_t* expert_row0, int n_experts,
+                            const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
+                            void* out, int64_t out_rows, int mode, int k_split, void* stream);
 
 /*
  * Deterministic route combine (new; pairs with grouped_gemm mode 2): out[t, :] = sum_{j < topk} partial[t*topk + j, :]
@@ -230,6 +253,32 @@ int exl3_reconstruct(uint16_t* out, const uint16_t* packed, int tiles_k, int til
  * over all 65536 states. n must be even.
  */
 int exl3_decode_states(const uint16_t* states, uint16_t* out, int64_t n, void* stream);
+
+/*
+ * Decode-path MoE: the whole routed-expert op for small batches, the `tokens <= cap` side of the reference wrapper's
+ * switch (kernel/exl3_grouped_runtime.py:93-98), where the overlay calls exllamav3's fused exl3_moe
+ * (kernel/tuned-fused-kernel-patch/exl3patch/exllamav3/exllamav3_ext/quant/exl3_moe.cu:133-345). Same result as
+ * the grouped prefill on the same inputs (route sort, gather + H128(x * suh_gate), gate|up, fp16 gu, SwiGLU with limit,
+ * H128(act * suh_down), down, scatter by token with the fp16 route weight), with both GEMMs split over K for batches
+ * too small to fill the GPU. Graph-capture-safe: a fixed launch sequence for given sizes, no allocation, no memset
+ * (fill kernels clear what accumulates), no host reads.
+ *   x fp16 [tokens, hidden] row-major; topk_ids [tokens, topk] int64 / int32 (ids outside [0, n_experts) are dropped);
+ *   topk_weights [tokens, topk] fp32 / fp16 / bf16 (rounded to fp16).
+ *   packed_gate / packed_up: trellis [hidden/16, inter/16, 16*bits] of expert e at + e*w13_expert_stride_words
+ *   (the [E, 2, ...] stacked views); suh_gate fp16 [E, hidden] at suh13_stride (gate and up share it);
+ *   svh_gate / svh_up fp16 [E, inter] at svh13_stride; packed_down [inter/16, hidden/16, 16*bits] at
+ *   w2_expert_stride_words; suh_down fp16 [E, inter] at suh2_stride; svh_down fp16 [E, hidden] at svh2_stride.
+ *   out fp32 [tokens, hidden], overwritten (16-byte aligned). workspace: exl3_moe_decode_workspace_bytes(...) bytes,
+ *   256-byte aligned, caller-owned. Calls that share a workspace must not overlap. New.
+ */
+int64_t exl3_moe_decode_workspace_bytes(int64_t tokens, int topk, int n_experts, int hidden, int inter);
+int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, const void* topk_ids, int ids_dtype,
+                    const void* topk_weights, int weights_dtype, int topk, int n_experts, int inter, int bits,
+                    const uint16_t* packed_gate, const uint16_t* packed_up, int64_t w13_expert_stride_words,
+                    const uint16_t* suh_gate, int64_t suh13_stride, const uint16_t* svh_gate, const uint16_t* svh_up,
+                    int64_t svh13_stride, const uint16_t* packed_down, int64_t w2_expert_stride_words,
+                    const uint16_t* suh_down, int64_t suh2_stride, const uint16_t* svh_down, int64_t svh2_stride,
+                    float limit, float* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -76,7 +76,8 @@ def test_grouped_gemm_contract():
     assert "too many experts" in _gemm(E=2000)[1]
     assert "single tensor" in _gemm(pu=FAKE, su=FAKE)[1]
     assert "gate/up strides must match" in _gemm(pu=FAKE, su=None)[1]
-    assert "mode" in _gemm(mode=3)[1]
+    assert "mode must be" in _gemm(mode=4)[1]
+    assert "mode 3: out fp32" in _gemm(mode=3)[1]                       # out_rows < a_rows
     assert "route_index" in _gemm(mode=2)[1]
     assert "combine" in rc_and_msg("exl3_combine_routes", FAKE, FAKE, None, 4, 8, 10, 8, 6, None)[1]
     a = dict(a=FAKE, a_rows=256, size_k=512, a_layout=0, pg=FAKE, pu=None, es=32 * 16 * 64, tk=32, tn=16, bits=4,
@@ -213,3 +214,85 @@ def test_route_topk_contract():
     assert rc == _lib.EXL3_ERR_ARG and msg == "null pointer"
     rc, msg = call(T=0, logits=None)
     assert rc == _lib.EXL3_OK
+
+
+def test_split_gemm_contract():
+    args = dict(a=FAKE, a_rows=256, size_k=512, a_layout=1, pg=FAKE, pu=None, es=32 * 16 * 64, tk=32, tn=16, bits=4,
+                sg=FAKE, su=None, ss=256, be=FAKE, br=FAKE, mb=10, tile_rows=128, counts=FAKE, row0=FAKE, E=8,
+                tok=FAKE, rw=FAKE, ri=None, out=FAKE, out_rows=256, mode=1, k_split=2)
+
+    def call(**kw):
+        a = dict(args)
+        a.update(kw)
+        return rc_and_msg("exl3_grouped_gemm_split", *a.values(), None)
+
+    for ks in (0, 9):                                    # K = 512: 16 stages, at most 8 slices of 2
+        rc, msg = call(k_split=ks)
+        assert rc == _lib.EXL3_ERR_ARG and "k_split" in msg
+    rc, msg = call(mode=0, k_split=2)
+    assert rc == _lib.EXL3_ERR_ARG and "accumulating mode" in msg
+    rc, msg = call(mode=3, tile_rows=512)
+    assert rc == _lib.EXL3_ERR_ARG and "mode 3" in msg
+    rc, msg = call(mode=5, k_split=1)
+    assert rc == _lib.EXL3_ERR_ARG and "mode must be" in msg
+    rc, msg = rc_and_msg("exl3_act_had_f32", FAKE, 300, FAKE, FAKE, FAKE, 128, 4, 128, ctypes.c_float(10.0), None)
+    assert rc == _lib.EXL3_ERR_ARG and "2I" in msg
+
+
+DECODE_ARGS = dict(x=FAKE, tokens=4, hidden=4096, ids=FAKE, ids_dt=4, w=FAKE, w_dt=0, topk=8, E=288, inter=768,
+                   bits=4, pg=FAKE, pu=FAKE, es13=2 * 256 * 48 * 64, suh=FAKE, suh_s=8192, svg=FAKE, svu=FAKE,
+                   sv_s=1536, pd=FAKE, es2=48 * 256 * 64, suhd=FAKE, suhd_s=768, svd=FAKE, svd_s=4096,
+                   limit=ctypes.c_float(10.0), out=ctypes.c_void_p(0x2000), ws=ctypes.c_void_p(0x10000), ws_bytes=0)
+
+
+def decode_call(**kw):
+    a = dict(DECODE_ARGS)
+    a.update(kw)
+    return rc_and_msg("exl3_moe_decode", *a.values(), None)
+
+
+def test_moe_decode_contract():
+    lib = _lib.load()
+    need = lib.exl3_moe_decode_workspace_bytes(4, 8, 288, 4096, 768)
+    R, r16 = 32, 32
+    regions = [R * 8, R * 2, R * 4, 288 * 4, 288 * 4, (32 + 0) * 4, (32 + 0) * 4, 8, r16 * 4096 * 2, R * 1536 * 4,
+               r16 * 768 * 2]
+    assert need % 256 == 0 and need >= sum(regions) + lib.exl3_sort_routes_workspace_bytes(4, 8, 288)
+    assert lib.exl3_moe_decode_workspace_bytes(8, 8, 288, 4096, 768) > need
+    assert lib.exl3_moe_decode_workspace_bytes(-1, 8, 288, 4096, 768) == -1
+    assert lib.exl3_moe_decode_workspace_bytes(4, 8, 2000, 4096, 768) == -1
+    rc, msg = decode_call(hidden=4000)
+    assert rc == _lib.EXL3_ERR_ARG and "multiples of 128" in msg
+    rc, msg = decode_call(bits=5)
+    assert rc == _lib.EXL3_ERR_ARG and "bits" in msg
+    rc, msg = decode_call(E=2000)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "too many experts"
+    rc, msg = decode_call(x=None)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "null pointer"
+    rc, msg = decode_call(out=ctypes.c_void_p(0x2004))
+    assert rc == _lib.EXL3_ERR_ARG and "aligned" in msg
+    rc, msg = decode_call(ws_bytes=need - 1)
+    assert rc == _lib.EXL3_ERR_ARG and "workspace too small" in msg
+    rc, msg = decode_call(tokens=0, x=None, ids=None, w=None, out=None, ws=None)
+    assert rc == _lib.EXL3_OK                            # nothing to do: no pointer is needed
+
+
+def test_shim_moe_decode_messages():
+    x = torch.zeros(4, 512, dtype=torch.float16)
+    ids = torch.zeros(4, 2, dtype=torch.int64)
+    w = torch.zeros(4, 2)
+    w13 = torch.zeros(8, 2, 32, 16, 64, dtype=torch.int16)
+    w2 = torch.zeros(8, 16, 32, 64, dtype=torch.int16)
+    s13, v13 = torch.zeros(8, 2, 512, dtype=torch.float16), torch.zeros(8, 2, 256, dtype=torch.float16)
+    s2, v2 = torch.zeros(8, 256, dtype=torch.float16), torch.zeros(8, 512, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="contiguous fp16"):
+        gp.moe_decode(x.float(), ids, w, w13, s13, v13, w2, s2, v2, 10.0)
+    with pytest.raises(RuntimeError, match="topk_ids"):
+        gp.moe_decode(x, ids[:3], w, w13, s13, v13, w2, s2, v2, 10.0)
+    with pytest.raises(RuntimeError, match="w2_trellis"):
+        gp.moe_decode(x, ids, w, w13, s13, v13, w2[:, :8], s2, v2, 10.0)
+    with pytest.raises(RuntimeError, match="shapes"):
+        gp.moe_decode(x, ids, w, w13, s13, v13, w2, s2[:, :128], v2, 10.0)
+    with pytest.raises(RuntimeError, match="tensors must be CUDA"):
+        gp.moe_decode(x, ids, w, w13, s13, v13, w2, s2, v2, 10.0,
+                      workspace=torch.empty(gp.moe_decode_workspace_bytes(4, 2, 8, 512, 256), dtype=torch.uint8))

@@ -1,0 +1,309 @@
+"""GPU parity of the decode path: moe_decode (the `tokens <= cap` side of kernel/exl3_grouped_runtime.py:93-98,
+where the reference calls the overlay's fused exl3_moe) and its building blocks, the split-K grouped GEMM and the
+fp32-input act_had.
+
+Bars: the north-star rel L2 <= 1e-3 against the oracle expert loop (harness/proto_fp8.py:123-134 restated in
+oracle/exl3_oracle.py); exact equality where the arithmetic is the same (fp32 act_had input rounded to fp16, a
+one-slice mode-3 GEMM against the fp16 store); fp32 accumulation-order bounds where only the order of additions
+differs (K slices, atomics). Graph capture: replays with fresh inputs against eager calls.
+"""
+import functools
+
+import numpy as np
+import pytest
+import torch
+
+import exl3_grouped as gp
+import exl3_grouped_runtime as rt
+import exl3_oracle as O
+from exl3_grouped import synth
+
+pytestmark = pytest.mark.gpu
+LIMIT = 10.0
+
+
+def to_np_layer(L):
+    return O.Layer(L.w13_trellis, L.w13_suh, L.w13_svh, L.w2_trellis, L.w2_suh, L.w2_svh)
+
+
+def dt(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@functools.lru_cache(maxsize=6)
+def layer_case(name, bits=None, svh_scale=1.0, seed=0):
+    """A layer of config `name` (weights only) on the host and on the GPU."""
+    L, _, _, _, cfg = synth.make_config(name, seed=seed, T=1, bits=bits, svh_scale=svh_scale)
+    return L, cfg
+
+
+@functools.lru_cache(maxsize=6)
+def device_layer(name, bits=None, svh_scale=1.0, seed=0):
+    L, cfg = layer_case(name, bits, svh_scale, seed)
+    return synth.to_device(L, torch.device("cuda:0"))
+
+
+def inputs(cfg, T, seed, routing="softmax"):
+    x = synth.make_x(T, cfg["H"], seed)
+    ids, w = synth.make_routing(routing, T, cfg["E"], cfg["topk"], seed=seed)
+    return x, ids, w
+
+
+def decode(TL, x, ids, w, dev, **kw):
+    out = gp.moe_decode(dt(x, dev).to(torch.float16), dt(ids, dev), dt(w, dev), TL.w13_trellis, TL.w13_suh,
+                        TL.w13_svh, TL.w2_trellis, TL.w2_suh, TL.w2_svh, LIMIT, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+# ------------------------------------------------------------------------------------------- building blocks
+def test_act_had_f32_equals_fp16_input(dev):
+    rng = np.random.default_rng(3)
+    R, I, E = 77, 768, 5
+    gu32 = torch.from_numpy((rng.standard_normal((R, 2 * I)) * 6).astype(np.float32)).to(dev)
+    eor = dt(rng.integers(0, E, R).astype(np.int32), dev)
+    suh = dt(np.where(rng.random((E, I)) < 0.5, -1.0, 1.0).astype(np.float16), dev)
+    a32 = torch.full((gp.t16_rows(R), I), float("nan"), dtype=torch.float16, device=dev)
+    a16 = torch.full_like(a32, float("nan"))
+    gp.act_had(gu32, a32, eor, suh, LIMIT, dst_layout=1)
+    gp.act_had(gu32.half(), a16, eor, suh, LIMIT, dst_layout=1)
+    assert torch.equal(a32.view(torch.int16), a16.view(torch.int16))      # bitwise; unwritten T16 padding is NaN
+
+
+def sorted_case(cfg, T, seed, dev, tile_rows=128, routing="softmax"):
+    x, ids, w = inputs(cfg, T, seed, routing)
+    E = cfg["E"]
+    ts, ws, eor, counts, row0 = O.sort_routes(ids, w, E)
+    R = ids.size
+    mb = min(E, R) + R // tile_rows
+    be = torch.empty(mb, dtype=torch.int32, device=dev)
+    br = torch.empty(mb, dtype=torch.int32, device=dev)
+    meta = torch.zeros(2, dtype=torch.int32, device=dev)
+    gp.build_tiles(dt(counts, dev), be, br, meta, tile_rows)
+    return x, ids, w, (dt(ts, dev), dt(ws, dev), dt(eor, dev), dt(counts, dev), dt(row0, dev)), be, br
+
+
+@pytest.mark.parametrize("tile_rows", [128, 256])
+@pytest.mark.parametrize("T", [1, 16, 300])
+def test_split_gate_up_matches_store(dev, T, tile_rows):
+    L, cfg = layer_case("layer1k")
+    TL = device_layer("layer1k")
+    x, ids, w, (ts, ws, eor, counts, row0), be, br = sorted_case(cfg, T, 11, dev, tile_rows)
+    R, I, H = ids.size, cfg["I"], cfg["H"]
+    h13 = torch.empty(gp.t16_rows(R), H, dtype=torch.float16, device=dev)
+    gp.row_had(dt(x, dev).half(), h13, ts, eor, TL.w13_suh[:, 0], True, dst_layout=1, rows=R)
+    args = (h13, TL.w13_trellis[:, 0], TL.w13_trellis[:, 1], TL.w13_svh[:, 0], TL.w13_svh[:, 1], be, br, counts, row0,
+            None, None)
+    gu16 = torch.empty(R, 2 * I, dtype=torch.float16, device=dev)
+    gp.grouped_gemm(*args, gu16, 0, tile_rows=tile_rows, a_layout=1, a_rows=R)
+    one = torch.zeros(R, 2 * I, dtype=torch.float32, device=dev)
+    gp.grouped_gemm(*args, one, 3, tile_rows=tile_rows, a_layout=1, a_rows=R, k_split=1)
+    torch.cuda.synchronize()
+    # One slice: 0 + y is y, so the fp32 rows hold the store path's products before its fp16 rounding. The store path
+    # may round the exact product once (mixed-precision multiply) where one.half() rounds the fp32 product again:
+    # exact fp16 ties then go one step apart, nothing else.
+    g = gu16.float()
+    assert ((one - g).abs() <= g.abs() * 2.0 ** -11 + 2.0 ** -24).all()
+    assert (one.half() != gu16).float().mean().item() < 1e-3
+    for ks in (2, 5, 64):
+        acc = torch.zeros_like(one)
+        gp.grouped_gemm(*args, acc, 3, tile_rows=tile_rows, a_layout=1, a_rows=R, k_split=ks)
+        torch.cuda.synchronize()
+        assert ((acc - one).norm() / one.norm()).item() < 1e-6, ks      # fp32 sums in another order
+
+
+@pytest.mark.parametrize("T", [1, 40])
+def test_split_down_scatter_matches_unsplit(dev, T):
+    L, cfg = layer_case("layer1k")
+    TL = device_layer("layer1k")
+    x, ids, w, (ts, ws, eor, counts, row0), be, br = sorted_case(cfg, T, 12, dev)
+    R, I, H = ids.size, cfg["I"], cfg["H"]
+    rng = np.random.default_rng(5)
+    act = dt((rng.standard_normal((gp.t16_rows(R), I)) * 3).astype(np.float16), dev)
+    outs = []
+    for ks in (1, 2, 12):
+        out = torch.zeros(T, H, dtype=torch.float32, device=dev)
+        gp.grouped_gemm(act, TL.w2_trellis, None, TL.w2_svh, None, be, br, counts, row0, ts, ws, out, 1,
+                        a_layout=1, a_rows=R, k_split=ks)
+        torch.cuda.synchronize()
+        outs.append(out)
+    for o in outs[1:]:
+        assert ((o - outs[0]).norm() / outs[0].norm()).item() < 1e-6
+
+
+def test_split_rejections(dev):
+    L, cfg = layer_case("tiny")
+    TL = device_layer("tiny")
+    x, ids, w, (ts, ws, eor, counts, row0), be, br = sorted_case(cfg, 4, 1, dev)
+    R, I, H = ids.size, cfg["I"], cfg["H"]
+    a = torch.zeros(gp.t16_rows(R), H, dtype=torch.float16, device=dev)
+    args = (a, TL.w13_trellis[:, 0], TL.w13_trellis[:, 1], TL.w13_svh[:, 0], TL.w13_svh[:, 1], be, br, counts, row0,
+            None, None)
+    with pytest.raises(RuntimeError, match="k_split"):
+        gp.grouped_gemm(*args, torch.zeros(R, 2 * I, dtype=torch.float16, device=dev), 0, a_layout=1, a_rows=R,
+                        k_split=2)                                # a storing mode cannot take slices
+    with pytest.raises(RuntimeError, match="k_split"):
+        gp.grouped_gemm(*args, torch.zeros(R, 2 * I, device=dev), 3, a_layout=1, a_rows=R, k_split=H // 64 + 1)
+    with pytest.raises(RuntimeError, match="mode 3"):
+        gp.grouped_gemm(*args, torch.zeros(R, 2 * I, device=dev), 3, a_layout=1, a_rows=R, tile_rows=512)
+
+
+# ------------------------------------------------------------------------------------------- the decode op
+@pytest.mark.parametrize("T", [1, 2, 7, 16, 24])
+def test_decode_vs_expert_loop_layer1k(dev, T):
+    L, cfg = layer_case("layer1k", svh_scale=1 / 64)
+    TL = device_layer("layer1k", svh_scale=1 / 64)
+    x, ids, w = inputs(cfg, T, 100 + T)
+    got = decode(TL, x, ids, w, dev).cpu().numpy()
+    ref = O.expert_loop(x, ids, w, to_np_layer(L), LIMIT)
+    assert O.rel_l2(got, ref) < 1e-3
+    prefill = rt.grouped_prefill(dt(x, dev), dt(ids, dev), dt(w, dev), TL, LIMIT).cpu().numpy()
+    assert O.rel_l2(got, prefill) < 1e-3
+
+
+@pytest.mark.parametrize("svh_scale", [1.0, 1 / 64])
+@pytest.mark.parametrize("T", [1, 128])
+def test_decode_vs_expert_loop_tiny(dev, T, svh_scale):
+    L, cfg = layer_case("tiny", svh_scale=svh_scale)
+    TL = device_layer("tiny", svh_scale=svh_scale)
+    x, ids, w = inputs(cfg, T, 7)
+    got = decode(TL, x, ids, w, dev).cpu().numpy()
+    ref = O.expert_loop(x, ids, w, to_np_layer(L), LIMIT)
+    assert O.rel_l2(got, ref) < 1e-3
+
+
+@pytest.mark.parametrize("bits", [3, 2])
+def test_decode_low_bits(dev, bits):
+    L, cfg = layer_case("layer1k", bits=bits, svh_scale=1 / 64)
+    TL = device_layer("layer1k", bits=bits, svh_scale=1 / 64)
+    x, ids, w = inputs(cfg, 4, 20 + bits)
+    got = decode(TL, x, ids, w, dev).cpu().numpy()
+    assert O.rel_l2(got, O.expert_loop(x, ids, w, to_np_layer(L), LIMIT)) < 1e-3
+
+
+def test_decode_skewed_rows_span_tiles(dev):
+    """Every token on the same 8 experts: 200 rows per expert, two 128-row tiles each."""
+    L, cfg = layer_case("layer1k", svh_scale=1 / 64)
+    TL = device_layer("layer1k", svh_scale=1 / 64)
+    T = 200
+    x = synth.make_x(T, cfg["H"], 3)
+    ids = np.tile(np.array([5, 77, 140, 141, 200, 3, 9, 287], np.int64), (T, 1))
+    w = np.random.default_rng(2).random((T, 8)).astype(np.float32)
+    w /= w.sum(1, keepdims=True)
+    got = decode(TL, x, ids, w, dev).cpu().numpy()
+    tokens = np.random.default_rng(4).choice(T, 12, replace=False)
+    ref = O.expert_loop(x[tokens], ids[tokens], w[tokens], to_np_layer(L), LIMIT)
+    assert O.rel_l2(got[tokens], ref) < 1e-3
+    prefill = rt.grouped_prefill(dt(x, dev), dt(ids, dev), dt(w, dev), TL, LIMIT).cpu().numpy()
+    assert O.rel_l2(got, prefill) < 1e-3
+
+
+def test_decode_dropped_ids_and_dtypes(dev):
+    L, cfg = layer_case("tiny")
+    TL = device_layer("tiny")
+    x, ids, w = inputs(cfg, 24, 9)
+    ids = ids.copy()
+    ids[3, 1] = -1
+    ids[10, 0] = cfg["E"] + 4                                       # outside [0, E): dropped like the reference loop
+    wb = torch.from_numpy(w).to(torch.bfloat16)
+    got = gp.moe_decode(dt(x, dev).half(), dt(ids, dev).to(torch.int32), wb.to(dev), TL.w13_trellis, TL.w13_suh,
+                        TL.w13_svh, TL.w2_trellis, TL.w2_suh, TL.w2_svh, LIMIT).cpu().numpy()
+    ref = O.expert_loop(x, ids, wb.float().numpy(), to_np_layer(L), LIMIT)
+    assert O.rel_l2(got, ref) < 1e-3
+
+
+def test_decode_empty_and_workspace_checks(dev):
+    L, cfg = layer_case("tiny")
+    TL = device_layer("tiny")
+    H = cfg["H"]
+    out = gp.moe_decode(torch.zeros(0, H, dtype=torch.float16, device=dev), torch.zeros(0, 2, dtype=torch.int64,
+                        device=dev), torch.zeros(0, 2, device=dev), TL.w13_trellis, TL.w13_suh, TL.w13_svh,
+                        TL.w2_trellis, TL.w2_suh, TL.w2_svh, LIMIT)
+    assert out.shape == (0, H)
+    x, ids, w = inputs(cfg, 3, 1)
+    small = torch.empty(256, dtype=torch.uint8, device=dev)
+    with pytest.raises(RuntimeError, match="workspace"):
+        gp.moe_decode(dt(x, dev).half(), dt(ids, dev), dt(w, dev), TL.w13_trellis, TL.w13_suh, TL.w13_svh,
+                      TL.w2_trellis, TL.w2_suh, TL.w2_svh, LIMIT, workspace=small)
+
+
+def test_decode_reuses_workspace_and_overwrites_out(dev):
+    """Calls of different sizes on one workspace, and an out buffer holding garbage: every call starts clean."""
+    L, cfg = layer_case("layer1k", svh_scale=1 / 64)
+    TL = device_layer("layer1k", svh_scale=1 / 64)
+    ws = torch.empty(gp.moe_decode_workspace_bytes(64, 8, cfg["E"], cfg["H"], cfg["I"]), dtype=torch.uint8,
+                     device=dev)
+    for T, seed in ((64, 1), (3, 2), (64, 1)):
+        x, ids, w = inputs(cfg, T, seed)
+        out = torch.full((T, cfg["H"]), 1e30, dtype=torch.float32, device=dev)
+        got = decode(TL, x, ids, w, dev, out=out, workspace=ws)
+        fresh = decode(TL, x, ids, w, dev)
+        assert got.data_ptr() == out.data_ptr()
+        assert ((got - fresh).norm() / fresh.norm()).item() < 1e-6
+
+
+def test_decode_graph_capture_replays(dev):
+    """Capture one decode call in a graph; replay it on new inputs copied into the captured buffers, with eager calls
+    in between, and compare every replay with an eager call on the same inputs."""
+    L, cfg = layer_case("layer1k", svh_scale=1 / 64)
+    TL = device_layer("layer1k", svh_scale=1 / 64)
+    T, k, H = 8, cfg["topk"], cfg["H"]
+    sx = torch.empty(T, H, dtype=torch.float16, device=dev)
+    sids = torch.empty(T, k, dtype=torch.int64, device=dev)
+    sw = torch.empty(T, k, dtype=torch.float32, device=dev)
+    sout = torch.empty(T, H, dtype=torch.float32, device=dev)
+    ws = torch.empty(gp.moe_decode_workspace_bytes(T, k, cfg["E"], H, cfg["I"]), dtype=torch.uint8, device=dev)
+
+    def load(seed):
+        x, ids, w = inputs(cfg, T, seed)
+        sx.copy_(dt(x, dev).half())
+        sids.copy_(dt(ids, dev))
+        sw.copy_(dt(w, dev))
+        return x, ids, w
+
+    def call():
+        gp.moe_decode(sx, sids, sw, TL.w13_trellis, TL.w13_suh, TL.w13_svh, TL.w2_trellis, TL.w2_suh, TL.w2_svh,
+                      LIMIT, out=sout, workspace=ws)
+
+    load(1)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call()                                                    # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for seed in (2, 3, 1, 2):
+        x, ids, w = load(seed)
+        g.replay()
+        torch.cuda.synchronize()
+        replay = sout.clone()
+        eager = decode(TL, x, ids, w, dev)
+        assert ((replay - eager).norm() / eager.norm()).item() < 1e-6, seed
+    ref = O.expert_loop(x, ids, w, to_np_layer(L), LIMIT)
+    assert O.rel_l2(replay.cpu().numpy(), ref) < 1e-3
+
+
+def test_install_routes_decode_calls(dev, monkeypatch):
+    L, cfg = layer_case("tiny")
+    TL = device_layer("tiny")
+
+    class Ov:
+        SWIGLU_LIMIT_DEFAULT = LIMIT
+
+        @staticmethod
+        def apply_exl3_experts(*a, **k):
+            return "original"
+
+    rt.install(Ov)
+    TL._exl3_fused_temps = [torch.zeros(1, 64)]
+    x, ids, w = inputs(cfg, 48, 5)
+    xb = dt(x, dev).to(torch.bfloat16)
+    got = Ov.apply_exl3_experts(xb, dt(ids, dev), dt(w, dev), TL, limit=LIMIT)
+    assert got.dtype == torch.bfloat16 and TL._exl3_last_apply == "decode"
+    ref = rt.grouped_prefill(xb, dt(ids, dev), dt(w, dev), TL, LIMIT)
+    assert O.rel_l2(got.float().cpu().numpy(), ref.to(torch.bfloat16).float().cpu().numpy()) < 1e-2
+    monkeypatch.setenv("EXL3_GROUPED_DECODE", "0")
+    assert Ov.apply_exl3_experts(xb, dt(ids, dev), dt(w, dev), TL) == "original"

@@ -27,18 +27,30 @@ def fake_overlay():
     return ov, calls
 
 
-def test_install_passes_through_decode_ep_and_non_trellis_layers():
+def test_install_passes_through_decode_ep_and_non_trellis_layers(monkeypatch):
     ov, calls = fake_overlay()
     rt.install(ov)
     assert ov.apply_exl3_experts is not None and ov.apply_exl3_experts.__name__ == "apply_exl3_experts_grouped"
     x = torch.zeros(64, 512, dtype=torch.float16)
     ids = torch.zeros(64, 8, dtype=torch.long)
     w = torch.zeros(64, 8)
-    # decode-sized call: tokens <= cap (cap = layer._exl3_fused_temps[0].shape[1])
+    # decode-sized call: tokens <= cap (cap = layer._exl3_fused_temps[0].shape[1]) goes to moe_decode, or to the
+    # original path with EXL3_GROUPED_DECODE=0
     layer = FakeLayer()
     layer.w13_trellis = torch.zeros(4, 2, 32, 16, 64, dtype=torch.int16)
     layer._exl3_fused_temps = [torch.zeros(1, 128)]
     layer.expert_map = None
+    decoded = []
+
+    def fake_decode(x2d, ids2d, w2d, lay, limit, out=None):
+        decoded.append((tuple(x2d.shape), ids2d.dtype, limit))
+        return torch.ones(x2d.shape, dtype=torch.float32)
+
+    monkeypatch.setattr(rt, "moe_decode", fake_decode)
+    got = ov.apply_exl3_experts(x, ids.to(torch.int32), w, layer, limit=7.0, fused="f")
+    assert got.dtype == torch.float16 and decoded == [((64, 512), torch.int64, 7.0)]
+    assert layer._exl3_last_apply == "decode" and not calls
+    monkeypatch.setenv("EXL3_GROUPED_DECODE", "0")
     assert ov.apply_exl3_experts(x, ids, w, layer, limit=7.0, fused="f") == "original"
     assert calls[-1] == dict(tokens=64, limit=7.0, fused="f")
     # expert-parallel layer
