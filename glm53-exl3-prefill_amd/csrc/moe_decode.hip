@@ -20,6 +20,7 @@ namespace exl3 {
 namespace {
 
 constexpr int DECODE_TILE_ROWS = 128;
+constexpr int SMALL_ROUTES = 2048;                   // routes exl3_route_prep_small sorts in one workgroup
 
 __global__ __launch_bounds__(256)
 void zero2_kernel(float4* __restrict__ a, int64_t na, float4* __restrict__ b, int64_t nb)
@@ -82,13 +83,12 @@ int target_workgroups(hipStream_t)
     return 2 * cus[dev];
 }
 
-// K slices for a launch of `wgs` workgroups over `stages` 32-wide K stages: enough to reach `target`, each slice at
-// least 2 stages.
+// K slices for a launch of `wgs` workgroups over `stages` 32-wide K stages: as many as fit in one round of `target`
+// resident workgroups (a partial second round would double the launch's time), each slice at least 2 stages.
 int k_split_for(int64_t wgs, int stages, int target)
 {
     if (wgs <= 0) return 1;
-    int64_t s = (target + wgs - 1) / wgs;
-    s = std::max<int64_t>(1, std::min<int64_t>(s, stages / 2));
+    const int64_t s = std::max<int64_t>(1, std::min<int64_t>(target / wgs, stages / 2));
     return (int) s;
 }
 
@@ -143,18 +143,31 @@ extern "C" int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, co
     auto* act = reinterpret_cast<uint16_t*>(at(L.act));
 
     // accumulation targets: out [tokens, hidden] and gu [R, 2 inter], both whole float4s
-    const int64_t n_out4 = tokens * hidden / 4, n_gu4 = R * 2 * inter / 4;
-    const int64_t zgrid = std::min<int64_t>((n_out4 + n_gu4 + 255) / 256, 2048);
-    zero2_kernel<<<(unsigned) zgrid, 256, 0, s>>>(reinterpret_cast<float4*>(out), n_out4,
-                                                  reinterpret_cast<float4*>(gu), n_gu4);
-    int rc = hip_status("moe_decode zero");
-    if (rc) return rc;
-    rc = exl3_sort_routes(topk_ids, ids_dtype, topk_weights, weights_dtype, tokens, topk, n_experts, token_sorted,
-                          weight_sorted, expert_of_row, nullptr, counts, expert_row0, at(L.sort_ws),
-                          (size_t) L.sort_ws_bytes, stream);
-    if (rc) return rc;
-    rc = exl3_build_tiles(counts, n_experts, DECODE_TILE_ROWS, L.max_blocks, block_expert, block_row0, meta, stream);
-    if (rc) return rc;
+    const int64_t n_out = tokens * hidden, n_gu = R * 2 * inter;
+    int rc;
+    if (R <= SMALL_ROUTES)
+    {
+        // sort, tile table and both clears in one launch
+        rc = exl3_route_prep_small(topk_ids, ids_dtype, topk_weights, weights_dtype, tokens, topk, n_experts,
+                                   DECODE_TILE_ROWS, L.max_blocks, token_sorted, weight_sorted, expert_of_row, counts,
+                                   expert_row0, block_expert, block_row0, meta, out, n_out, gu, n_gu, stream);
+        if (rc) return rc;
+    }
+    else
+    {
+        const int64_t zgrid = std::min<int64_t>((n_out / 4 + n_gu / 4 + 255) / 256, 2048);
+        zero2_kernel<<<(unsigned) zgrid, 256, 0, s>>>(reinterpret_cast<float4*>(out), n_out / 4,
+                                                      reinterpret_cast<float4*>(gu), n_gu / 4);
+        rc = hip_status("moe_decode zero");
+        if (rc) return rc;
+        rc = exl3_sort_routes(topk_ids, ids_dtype, topk_weights, weights_dtype, tokens, topk, n_experts, token_sorted,
+                              weight_sorted, expert_of_row, nullptr, counts, expert_row0, at(L.sort_ws),
+                              (size_t) L.sort_ws_bytes, stream);
+        if (rc) return rc;
+        rc = exl3_build_tiles(counts, n_experts, DECODE_TILE_ROWS, L.max_blocks, block_expert, block_row0, meta,
+                              stream);
+        if (rc) return rc;
+    }
     rc = exl3_row_had_ex(x, h13, token_sorted, expert_of_row, suh_gate, suh13_stride, hidden, R, hidden, 1,
                          EXL3_LAYOUT_T16, stream);
     if (rc) return rc;

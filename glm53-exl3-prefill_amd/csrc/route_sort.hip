@@ -13,6 +13,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 namespace exl3 {
 namespace {
 
@@ -129,22 +131,17 @@ __device__ __forceinline__ uint64_t match_lanes(int key, bool valid)
     return peers;
 }
 
-__global__ __launch_bounds__(SORT_THREADS)
-void sort_scatter_kernel(const void* __restrict__ ids, int ids_dtype, const void* __restrict__ weights, int w_dtype,
-                         int64_t R, int topk, int n_experts, const int32_t* __restrict__ cursor0,
-                         int64_t* __restrict__ token_sorted, uint16_t* __restrict__ weight_sorted,
-                         int32_t* __restrict__ expert_of_row, int32_t* __restrict__ route_index)
+// Writes the routes of chunk [base, base + CHUNK) to their sorted rows, in index order: s_cursor[e] holds the chunk's
+// first row for expert e (advanced here), s_wave_cnt is zero on entry and on exit. Called by all SORT_THREADS
+// threads of the workgroup.
+__device__ __forceinline__ void scatter_chunk(const void* __restrict__ ids, int ids_dtype,
+                                              const void* __restrict__ weights, int w_dtype, int64_t R, int topk,
+                                              int n_experts, int64_t base, int32_t* s_cursor,
+                                              int32_t (*s_wave_cnt)[MAX_EXPERTS], int64_t* __restrict__ token_sorted,
+                                              uint16_t* __restrict__ weight_sorted,
+                                              int32_t* __restrict__ expert_of_row, int32_t* __restrict__ route_index)
 {
-    __shared__ int32_t s_cursor[MAX_EXPERTS];
-    __shared__ int32_t s_wave_cnt[SORT_WAVES][MAX_EXPERTS];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    for (int e = t; e < n_experts; e += SORT_THREADS)
-    {
-        s_cursor[e] = cursor0[(int64_t) blockIdx.x * n_experts + e];
-        for (int w = 0; w < SORT_WAVES; ++w) s_wave_cnt[w][e] = 0;
-    }
-    __syncthreads();
-    const int64_t base = (int64_t) blockIdx.x * CHUNK;
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     for (int k = 0; k < ROUTES_PER_THREAD; ++k)
     {
@@ -173,6 +170,119 @@ void sort_scatter_kernel(const void* __restrict__ ids, int ids_dtype, const void
         }
         __syncthreads();
     }
+}
+
+__global__ __launch_bounds__(SORT_THREADS)
+void sort_scatter_kernel(const void* __restrict__ ids, int ids_dtype, const void* __restrict__ weights, int w_dtype,
+                         int64_t R, int topk, int n_experts, const int32_t* __restrict__ cursor0,
+                         int64_t* __restrict__ token_sorted, uint16_t* __restrict__ weight_sorted,
+                         int32_t* __restrict__ expert_of_row, int32_t* __restrict__ route_index)
+{
+    __shared__ int32_t s_cursor[MAX_EXPERTS];
+    __shared__ int32_t s_wave_cnt[SORT_WAVES][MAX_EXPERTS];
+    const int t = threadIdx.x;
+    for (int e = t; e < n_experts; e += SORT_THREADS)
+    {
+        s_cursor[e] = cursor0[(int64_t) blockIdx.x * n_experts + e];
+        for (int w = 0; w < SORT_WAVES; ++w) s_wave_cnt[w][e] = 0;
+    }
+    __syncthreads();
+    scatter_chunk(ids, ids_dtype, weights, w_dtype, R, topk, n_experts, (int64_t) blockIdx.x * CHUNK, s_cursor,
+                  s_wave_cnt, token_sorted, weight_sorted, expert_of_row, route_index);
+}
+
+// The decode path's route preparation in one launch, for R <= CHUNK routes. Workgroup 0 sorts: expert histogram in
+// LDS, exclusive scans of rows and tiles over the experts (thread t owns experts 4t .. 4t + 3), counts / expert_row0,
+// the tile table of build_blocks_kernel, the tail rows of sort_fill_tail_kernel, then the stable scatter of
+// sort_scatter_kernel from the scanned cursors -- the same rows the three-pass sort writes. Workgroups 1.. clear two
+// fp32 buffers (float4 counts na, nb).
+__global__ __launch_bounds__(SORT_THREADS)
+void route_prep_small_kernel(const void* __restrict__ ids, int ids_dtype, const void* __restrict__ weights,
+                             int w_dtype, int64_t R, int topk, int n_experts, int tile_rows, int max_tiles,
+                             int64_t* __restrict__ token_sorted, uint16_t* __restrict__ weight_sorted,
+                             int32_t* __restrict__ expert_of_row, int32_t* __restrict__ counts,
+                             int32_t* __restrict__ expert_row0, int32_t* __restrict__ tile_expert,
+                             int32_t* __restrict__ tile_row0, int32_t* __restrict__ meta, float4* __restrict__ zero_a,
+                             int64_t na, float4* __restrict__ zero_b, int64_t nb)
+{
+    const int t = threadIdx.x;
+    if (blockIdx.x > 0)
+    {
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int64_t i = (int64_t) (blockIdx.x - 1) * SORT_THREADS + t; i < na + nb;
+             i += (int64_t) (gridDim.x - 1) * SORT_THREADS)
+        {
+            if (i < na) zero_a[i] = z;
+            else zero_b[i - na] = z;
+        }
+        return;
+    }
+    static_assert(MAX_EXPERTS == 4 * SORT_THREADS, "four experts per thread in the scans");
+    __shared__ int32_t s_cursor[MAX_EXPERTS];
+    __shared__ int32_t s_wave_cnt[SORT_WAVES][MAX_EXPERTS];
+    __shared__ int32_t s_rows[SORT_THREADS], s_tiles[SORT_THREADS];
+    for (int e = t; e < MAX_EXPERTS; e += SORT_THREADS)
+    {
+        s_cursor[e] = 0;
+        for (int w = 0; w < SORT_WAVES; ++w) s_wave_cnt[w][e] = 0;
+    }
+    __syncthreads();
+    for (int k = 0; k < ROUTES_PER_THREAD; ++k)
+    {
+        const int64_t i = (int64_t) k * SORT_THREADS + t;
+        const int e = (i < R) ? route_id(ids, ids_dtype, i, n_experts) : -1;
+        if (e >= 0) atomicAdd(&s_cursor[e], 1);
+    }
+    __syncthreads();
+    int c[4], nbk[4], my_rows = 0, my_tiles = 0;
+    #pragma unroll
+    for (int j = 0; j < 4; ++j)
+    {
+        c[j] = s_cursor[4 * t + j];                     // zero past n_experts
+        nbk[j] = (c[j] + tile_rows - 1) / tile_rows;
+        my_rows += c[j];
+        my_tiles += nbk[j];
+    }
+    s_rows[t] = my_rows;
+    s_tiles[t] = my_tiles;
+    __syncthreads();
+    for (int d = 1; d < SORT_THREADS; d <<= 1)         // inclusive scans over the threads
+    {
+        const int vr = (t >= d) ? s_rows[t - d] : 0;
+        const int vt = (t >= d) ? s_tiles[t - d] : 0;
+        __syncthreads();
+        s_rows[t] += vr;
+        s_tiles[t] += vt;
+        __syncthreads();
+    }
+    int row = s_rows[t] - my_rows, tile = s_tiles[t] - my_tiles;
+    const int n_rows = s_rows[SORT_THREADS - 1], n_tiles = s_tiles[SORT_THREADS - 1];
+    #pragma unroll
+    for (int j = 0; j < 4; ++j)
+    {
+        const int e = 4 * t + j;
+        if (e < n_experts)
+        {
+            counts[e] = c[j];
+            expert_row0[e] = row;
+            for (int q = 0; q < nbk[j]; ++q)
+                if (tile + q < max_tiles) { tile_expert[tile + q] = e; tile_row0[tile + q] = row + q * tile_rows; }
+        }
+        s_cursor[e] = row;                              // every slot was read into c[] before the scans' barriers
+        row += c[j];
+        tile += nbk[j];
+    }
+    if (t == 0) { meta[0] = n_tiles; meta[1] = n_rows; }
+    for (int b = n_tiles + t; b < max_tiles; b += SORT_THREADS) tile_expert[b] = -1;
+    for (int64_t r = n_rows + t; r < R; r += SORT_THREADS)
+    {
+        token_sorted[r] = 0;
+        weight_sorted[r] = 0;
+        expert_of_row[r] = 0;
+    }
+    __syncthreads();
+    scatter_chunk(ids, ids_dtype, weights, w_dtype, R, topk, n_experts, 0, s_cursor, s_wave_cnt, token_sorted,
+                  weight_sorted, expert_of_row, nullptr);
 }
 
 // Rows past sum(counts) (only present when routes were dropped): token 0, weight 0, expert 0, route 0.
@@ -351,6 +461,38 @@ extern "C" int exl3_sort_routes(const void* topk_ids, int ids_dtype, const void*
                                                  expert_of_row, route_index);
     }
     return hip_status("sort_routes");
+}
+
+extern "C" int exl3_route_prep_small(const void* topk_ids, int ids_dtype, const void* topk_weights, int weights_dtype,
+                                     int64_t tokens, int topk, int n_experts, int tile_rows, int max_tiles,
+                                     int64_t* token_sorted, uint16_t* weight_sorted, int32_t* expert_of_row,
+                                     int32_t* counts, int32_t* expert_row0, int32_t* tile_expert, int32_t* tile_row0,
+                                     int32_t* meta, float* zero_a, int64_t zero_a_floats, float* zero_b,
+                                     int64_t zero_b_floats, void* stream)
+{
+    EXL3_CHECK(ids_dtype == EXL3_DTYPE_I64 || ids_dtype == EXL3_DTYPE_I32, "topk_ids must be int64 or int32");
+    EXL3_CHECK(weights_dtype == EXL3_DTYPE_F32 || weights_dtype == EXL3_DTYPE_F16 || weights_dtype == EXL3_DTYPE_BF16,
+               "topk_weights must be float32, float16 or bfloat16");
+    EXL3_CHECK(tokens >= 0 && topk > 0, "bad routing shape");
+    EXL3_CHECK(n_experts > 0 && n_experts <= MAX_EXPERTS, "too many experts");
+    EXL3_CHECK(tokens * topk <= CHUNK, "route_prep_small takes at most %d routes", CHUNK);
+    EXL3_CHECK(tile_rows == 64 || tile_rows == 128 || tile_rows == 256 || tile_rows == 512,
+               "tile_rows must be 64, 128, 256 or 512");
+    EXL3_CHECK(max_tiles >= 0 && zero_a_floats >= 0 && zero_b_floats >= 0 && zero_a_floats % 4 == 0 &&
+               zero_b_floats % 4 == 0, "bad sizes (zero-fill lengths are whole float4s)");
+    const int64_t R = tokens * topk;
+    EXL3_CHECK(counts && expert_row0 && meta && (max_tiles == 0 || (tile_expert && tile_row0)), "null pointer");
+    EXL3_CHECK(R == 0 || (topk_ids && topk_weights && token_sorted && weight_sorted && expert_of_row), "null pointer");
+    EXL3_CHECK((zero_a_floats == 0 || zero_a) && (zero_b_floats == 0 || zero_b) &&
+               ((reinterpret_cast<uintptr_t>(zero_a) | reinterpret_cast<uintptr_t>(zero_b)) & 15) == 0,
+               "zero-fill buffers must be 16-byte aligned");
+    const int64_t n4 = zero_a_floats / 4 + zero_b_floats / 4;
+    const int64_t zwgs = std::min<int64_t>((n4 + SORT_THREADS - 1) / SORT_THREADS, 1024);
+    route_prep_small_kernel<<<(unsigned) (1 + zwgs), SORT_THREADS, 0, as_stream(stream)>>>(
+        topk_ids, ids_dtype, topk_weights, weights_dtype, R, topk, n_experts, tile_rows, max_tiles, token_sorted,
+        weight_sorted, expert_of_row, counts, expert_row0, tile_expert, tile_row0, meta,
+        reinterpret_cast<float4*>(zero_a), zero_a_floats / 4, reinterpret_cast<float4*>(zero_b), zero_b_floats / 4);
+    return hip_status("route_prep_small");
 }
 
 extern "C" int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_rows, int max_tiles,

@@ -52,6 +52,8 @@ SIGNATURES = {
     "exl3_linear": (I32, [P, I64, I32, P, I32, I32, I32, P, P, P, P, I32, P]),
     "exl3_reconstruct": (I32, [P, P, I32, I32, I32, I32, I32, P]),
     "exl3_decode_states": (I32, [P, P, I64, P]),
+    "exl3_route_prep_small": (I32, [P, I32, P, I32, I64, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P, I64, P, I64,
+                                    P]),
     "exl3_moe_decode_workspace_bytes": (I64, [I64, I32, I32, I32, I32]),
     "exl3_moe_decode": (I32, [P, I64, I32, P, I32, P, I32, I32, I32, I32, I32, P, P, I64, P, I64, P, P, I64, P, I64,
                               P, I64, P, I64, F32, P, P, I64, P]),

@@ -399,6 +399,42 @@ def linear_exl3(x: torch.Tensor, packed: torch.Tensor, suh: torch.Tensor, svh: t
 
 
 # ------------------------------------------------------------------------------------------- decode path
+SMALL_ROUTES = 2048
+
+
+def route_prep_small(topk_ids: torch.Tensor, topk_weights: torch.Tensor, n_experts: int, token_sorted: torch.Tensor,
+                     weight_sorted: torch.Tensor, expert_of_row: torch.Tensor, counts: torch.Tensor,
+                     expert_row0: torch.Tensor, tile_expert: torch.Tensor, tile_row0: torch.Tensor,
+                     meta: torch.Tensor, tile_rows: int = 128, zero: tuple = ()) -> None:
+    """The decode path's route preparation in one launch (new): sort_routes + build_tiles for at most 2048 routes,
+    and a zero fill of up to two contiguous fp32 tensors in `zero`."""
+    _check(topk_ids.dim() == 2 and topk_weights.shape == topk_ids.shape, "topk_ids / topk_weights must be [T, topk]")
+    _check(topk_ids.dtype in (torch.int64, torch.int32) and topk_ids.is_contiguous(), "topk_ids int64/int32")
+    _check(topk_weights.dtype in (torch.float32, torch.float16, torch.bfloat16) and topk_weights.is_contiguous(),
+           "topk_weights fp32/fp16/bf16")
+    T, k = topk_ids.shape
+    R = T * k
+    _check(R <= SMALL_ROUTES, f"route_prep_small takes at most {SMALL_ROUTES} routes")
+    _check(token_sorted.dtype == torch.int64 and weight_sorted.dtype == torch.float16 and
+           expert_of_row.dtype == torch.int32 and min(token_sorted.numel(), weight_sorted.numel(),
+                                                      expert_of_row.numel()) >= R, "sorted outputs [R]")
+    _check(counts.dtype == torch.int32 and expert_row0.dtype == torch.int32 and counts.numel() >= n_experts and
+           expert_row0.numel() >= n_experts, "counts / expert_row0 int32 [E]")
+    _check(tile_expert.dtype == torch.int32 and tile_row0.dtype == torch.int32 and meta.dtype == torch.int32 and
+           tile_row0.numel() >= tile_expert.numel() and meta.numel() >= 2, "int32 tile table")
+    _check(len(zero) <= 2 and all(z.dtype == torch.float32 and z.is_contiguous() and z.numel() % 4 == 0
+                                  for z in zero), "zero: up to two contiguous fp32 tensors of whole float4s")
+    z = list(zero) + [None] * (2 - len(zero))
+    dev = _require_cuda(topk_ids, topk_weights, token_sorted, weight_sorted, expert_of_row, counts, expert_row0,
+                        tile_expert, tile_row0, meta, *zero)
+    with _On(dev) as s:
+        _lib.call("exl3_route_prep_small", _p(topk_ids), _DT[topk_ids.dtype], _p(topk_weights),
+                  _DT[topk_weights.dtype], T, k, int(n_experts), int(tile_rows), tile_expert.numel(),
+                  _p(token_sorted), _p(weight_sorted), _p(expert_of_row), _p(counts), _p(expert_row0),
+                  _p(tile_expert), _p(tile_row0), _p(meta), _p(z[0]), 0 if z[0] is None else z[0].numel(), _p(z[1]),
+                  0 if z[1] is None else z[1].numel(), s)
+
+
 def moe_decode_workspace_bytes(tokens: int, topk: int, n_experts: int, hidden: int, inter: int) -> int:
     """Bytes of the workspace moe_decode needs (sorted routes, tile table, the Hadamard'd rows, fp32 gate|up sums)."""
     v = int(_lib.load().exl3_moe_decode_workspace_bytes(int(tokens), int(topk), int(n_experts), int(hidden),

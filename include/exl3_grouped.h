@@ -271,6 +271,18 @@ int exl3_decode_states(const uint16_t* states, uint16_t* out, int64_t n, void* s
  *   out fp32 [tokens, hidden], overwritten (16-byte aligned). workspace: exl3_moe_decode_workspace_bytes(...) bytes,
  *   256-byte aligned, caller-owned. Calls that share a workspace must not overlap. New.
  */
+/*
+ * The decode path's route preparation in one launch (new): for tokens*topk <= 2048 routes, the stable sort of
+ * exl3_sort_routes (same token_sorted / weight_sorted / expert_of_row / counts / expert_row0, no route_index, no
+ * workspace) and the tile table of exl3_build_tiles(counts, n_experts, tile_rows, max_tiles, ...) including meta,
+ * plus a zero fill of two optional fp32 buffers (16-byte aligned, lengths multiples of 4 floats).
+ */
+int exl3_route_prep_small(const void* topk_ids, int ids_dtype, const void* topk_weights, int weights_dtype,
+                          int64_t tokens, int topk, int n_experts, int tile_rows, int max_tiles,
+                          int64_t* token_sorted, uint16_t* weight_sorted, int32_t* expert_of_row, int32_t* counts,
+                          int32_t* expert_row0, int32_t* tile_expert, int32_t* tile_row0, int32_t* meta,
+                          float* zero_a, int64_t zero_a_floats, float* zero_b, int64_t zero_b_floats, void* stream);
+
 int64_t exl3_moe_decode_workspace_bytes(int64_t tokens, int topk, int n_experts, int hidden, int inter);
 int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, const void* topk_ids, int ids_dtype,
                     const void* topk_weights, int weights_dtype, int topk, int n_experts, int inter, int bits,

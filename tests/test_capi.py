@@ -296,3 +296,21 @@ def test_shim_moe_decode_messages():
     with pytest.raises(RuntimeError, match="tensors must be CUDA"):
         gp.moe_decode(x, ids, w, w13, s13, v13, w2, s2, v2, 10.0,
                       workspace=torch.empty(gp.moe_decode_workspace_bytes(4, 2, 8, 512, 256), dtype=torch.uint8))
+
+
+def test_route_prep_small_contract():
+    def call(T=4, k=8, E=288, tr=128, mt=40, za=None, na=0, ids=FAKE):
+        return rc_and_msg("exl3_route_prep_small", ids, 4, FAKE, 0, T, k, E, tr, mt, FAKE, FAKE, FAKE, FAKE, FAKE,
+                          FAKE, FAKE, FAKE, za, na, None, 0, None)
+    rc, msg = call(T=257)
+    assert rc == _lib.EXL3_ERR_ARG and "at most 2048 routes" in msg
+    rc, msg = call(tr=100)
+    assert rc == _lib.EXL3_ERR_ARG and "tile_rows" in msg
+    rc, msg = call(E=1025)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "too many experts"
+    rc, msg = call(za=FAKE, na=6)
+    assert rc == _lib.EXL3_ERR_ARG and "float4" in msg
+    rc, msg = call(za=ctypes.c_void_p(0x1004), na=8)
+    assert rc == _lib.EXL3_ERR_ARG and "aligned" in msg
+    rc, msg = call(ids=None)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "null pointer"

@@ -70,6 +70,64 @@ def test_act_had_f32_equals_fp16_input(dev):
     assert torch.equal(a32.view(torch.int16), a16.view(torch.int16))      # bitwise; unwritten T16 padding is NaN
 
 
+def closed_form_sort(ids, w, E):
+    """Stable sort of routes by expert with out-of-range ids moved to the tail as (token 0, weight 0, expert 0): the
+    semantics of the route sort, restated with numpy (checked against the oracle's sort where no id is dropped)."""
+    flat = ids.reshape(-1)
+    R, k = flat.size, ids.shape[1]
+    valid = (flat >= 0) & (flat < E)
+    order = np.argsort(np.where(valid, flat, E), kind="stable")
+    live = np.arange(R) < valid.sum()
+    ts = np.where(live, order // k, 0).astype(np.int64)
+    ws = np.where(live, w.reshape(-1).astype(np.float16)[order], np.float16(0)).astype(np.float16)
+    eor = np.where(live, flat[order], 0).astype(np.int32)
+    counts = np.bincount(flat[valid], minlength=E).astype(np.int32)
+    return ts, ws, eor, counts, (np.cumsum(counts) - counts).astype(np.int32)
+
+
+@pytest.mark.parametrize("kind,T,E,k,tile_rows", [("softmax", 1, 288, 8, 128), ("softmax", 16, 288, 8, 128),
+                                                  ("skewed", 256, 288, 8, 128), ("softmax", 200, 1024, 6, 64),
+                                                  ("zipf", 128, 288, 8, 256), ("softmax", 2048, 8, 1, 512)])
+def test_route_prep_small_bit_exact(dev, kind, T, E, k, tile_rows):
+    """One launch against the stable sort and block table (kernel/exl3_grouped_prefill.cu:63-96,
+    kernel/exl3_grouped_runtime.py:59-68), with int32 ids, dropped ids and bf16 weights on the side."""
+    ids, w = synth.make_routing(kind, T, E, k, seed=T + E)
+    wf = w.astype(np.float16).astype(np.float32)
+    for g, r in zip(closed_form_sort(ids, wf, E), O.sort_routes(ids, wf, E)):
+        assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(r).view(np.uint8))
+    cases = [(ids, torch.int64, torch.float32)]
+    if T > 3:
+        dropped = ids.copy()
+        dropped[3, 0] = -1
+        dropped[T - 1, k - 1] = E + 3
+        cases.append((dropped, torch.int32, torch.bfloat16))
+    for ids_c, ids_dt, w_dt in cases:
+        wt = torch.from_numpy(w).to(w_dt)
+        ref = closed_form_sort(ids_c, wt.float().numpy(), E)
+        R = ids_c.size
+        mb = min(E, R) + R // tile_rows
+        rbe, rbr, rmeta = O.build_blocks(ref[3], mb, init=-7, tile_rows=tile_rows)
+        ts = torch.full((R,), -5, dtype=torch.int64, device=dev)
+        ws = torch.full((R,), 7, dtype=torch.int16, device=dev).view(torch.float16)
+        eor = torch.full((R,), -5, dtype=torch.int32, device=dev)
+        counts = torch.full((E,), -5, dtype=torch.int32, device=dev)
+        row0 = torch.full((E,), -5, dtype=torch.int32, device=dev)
+        be = torch.full((mb,), -7, dtype=torch.int32, device=dev)
+        br = torch.full((mb,), -7, dtype=torch.int32, device=dev)
+        meta = torch.full((2,), -5, dtype=torch.int32, device=dev)
+        za = torch.full((1000,), 3.0, device=dev)
+        zb = torch.full((36,), 3.0, device=dev)
+        gp.route_prep_small(dt(ids_c, dev).to(ids_dt), wt.to(dev), E, ts, ws, eor, counts, row0, be, br, meta,
+                            tile_rows=tile_rows, zero=(za, zb))
+        torch.cuda.synchronize()
+        for g, r in zip((ts, ws, eor, counts, row0), ref):
+            assert np.array_equal(g.cpu().numpy().view(np.uint8), np.asarray(r).view(np.uint8))
+        n = int(rmeta[0])
+        assert meta.tolist() == [int(v) for v in rmeta]
+        assert np.array_equal(be.cpu().numpy(), rbe) and np.array_equal(br.cpu().numpy()[:n], rbr[:n])
+        assert not za.any() and not zb.any()
+
+
 def sorted_case(cfg, T, seed, dev, tile_rows=128, routing="softmax"):
     x, ids, w = inputs(cfg, T, seed, routing)
     E = cfg["E"]
