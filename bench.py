@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--decode", action="store_true", help="time the decode path (moe_decode) at small batches")
     ap.add_argument("--decode-tokens", default="1,4,16,32,64,128")
+    ap.add_argument("--decode-no-compare", action="store_true",
+                    help="with --decode: skip the prefill-path comparison (clean kernel traces of the decode path)")
     ap.add_argument("--stages", action="store_true", help="print per-stage ms to stderr")
     ap.add_argument("--scatter", choices=["atomic", "combine"], default=None,
                     help="down-projection output method (default: the runtime's, EXL3_GROUPED_SCATTER or atomic)")
@@ -249,12 +251,13 @@ def decode_bench(args):
         with torch.cuda.graph(g):
             call()
         graph_us = timed(g.replay, n)
-        prefill_us = timed(lambda: rt.grouped_prefill(x, ids, w, TL, 10.0), n)
+        prefill_us = None if args.decode_no_compare else round(timed(lambda: rt.grouped_prefill(x, ids, w, TL, 10.0),
+                                                                         n), 2)
         active = int(np.unique(ids_np).size)
         nbytes = active * (3 * H * I * bits // 8 + (H + 2 * I + I + H) * 2) + T * H * 2 + T * H * 4
         print(json.dumps({"metric": "decode-path MoE us per layer", "tokens": T, "topk": k, "active_experts": active,
                           "eager_us": round(eager_us, 2), "graph_us": round(graph_us, 2),
-                          "prefill_path_us": round(prefill_us, 2), "bytes": nbytes,
+                          "prefill_path_us": prefill_us, "bytes": nbytes,
                           "hbm_frac_graph": round(nbytes / (graph_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
                           "config": {"workload": f"layer1k weights: E={E} H={H} I={I} {bits}bpw top{k} softmax"}}),
               flush=True)

@@ -9,8 +9,8 @@
 //
 // gfx950 cost per weight: the 32-bit multiply by a 16-bit state is split into a 16x16 low-half multiply whose
 // result lands in the upper word (SDWA) plus a 16x16+32 multiply-add that picks the state's half by op_sel,
-// so no state ever needs shifting out of its dword; v_bitop3 does mask-and-xor in one op, SDWA fp16 adds put each
-// sum in its half of a temporary and an OR joins a pair. About 4.9 VALU ops per weight at 4 bits.
+// so no state ever needs shifting out of its dword; v_bitop3 does mask-and-xor in one op, and SDWA fp16 adds write
+// each sum into its half of the packed output pair in place. About 4.4 VALU ops per weight at 4 bits.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>

@@ -504,7 +504,7 @@ def test_thin_config_all_bits(dev, bits):
     assert O.rel_l2(out[tokens], sampled_loop(L, x, ids, w, tokens)) < 1e-3
 
 
-def test_install_engages_grouped_path(dev):
+def test_install_engages_grouped_path(dev, monkeypatch):
     L, x, ids, w, cfg = synth.make_config("tiny", seed=5)
     ov = Fake()
     ov.SWIGLU_LIMIT_DEFAULT = LIMIT
@@ -517,4 +517,7 @@ def test_install_engages_grouped_path(dev):
     assert got.dtype == torch.bfloat16 and TL._exl3_last_apply == "grouped"
     ref = rt.grouped_prefill(xb, t16(ids, dev), t16(w, dev), TL, LIMIT)
     assert torch.allclose(got.float(), ref.to(torch.bfloat16).float())
+    small = ov.apply_exl3_experts(xb[:64], t16(ids, dev)[:64], t16(w, dev)[:64], TL)   # tokens <= cap: decode path
+    assert small.dtype == torch.bfloat16 and TL._exl3_last_apply == "decode"
+    monkeypatch.setenv("EXL3_GROUPED_DECODE", "0")
     assert ov.apply_exl3_experts(xb[:64], t16(ids, dev)[:64], t16(w, dev)[:64], TL) == "original"
