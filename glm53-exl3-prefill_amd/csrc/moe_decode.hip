@@ -4,7 +4,9 @@
 //
 // Same stages and rounding points as the grouped prefill -- route sort, gather + input Hadamard, gate|up GEMM,
 // activation + Hadamard, down GEMM with scatter -- on a fixed launch sequence whose grids depend on the sizes only:
-//   * The row-tile table is bounded by min(E, R) + R / 128 entries (every expert with rows adds at most one partial
+//   * 64-row tiles on the thin GEMM kernel (16 rows per wave, a quarter of the accumulators, four workgroups per CU):
+//     most waves of a small batch only decode, and the extra resident waves hide the trellis loads' latency.
+//   * The row-tile table is bounded by min(E, R) + R / 64 entries (every expert with rows adds at most one partial
 //     tile), so a batch of a few tokens launches a few dozen row tiles instead of one per expert.
 //   * A batch of a few tokens has too few (row tile, column tile) pairs to fill the GPU, so both GEMMs split K into
 //     slices (chosen from the sizes so that about two workgroups per CU are resident) and add their partial sums
@@ -19,7 +21,7 @@
 namespace exl3 {
 namespace {
 
-constexpr int DECODE_TILE_ROWS = 128;
+constexpr int DECODE_TILE_ROWS = 64;                 // the thin GEMM kernel: 16 rows per wave, four workgroups per CU
 constexpr int SMALL_ROUTES = 2048;                   // routes exl3_route_prep_small sorts in one workgroup
 
 __global__ __launch_bounds__(256)
@@ -68,19 +70,19 @@ DecodeLayout decode_layout(int64_t tokens, int topk, int n_experts, int hidden, 
     return L;
 }
 
-// Workgroups a launch should put on the device: two resident 256-thread GEMM workgroups per CU.
+// Workgroups a launch should put on the device: four resident thin-kernel workgroups per CU.
 int target_workgroups(hipStream_t)
 {
     static int cus[64] = {};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
     if (cus[dev] == 0)
     {
         int n = 0;
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
         cus[dev] = n;
     }
-    return 2 * cus[dev];
+    return 4 * cus[dev];
 }
 
 // K slices for a launch of `wgs` workgroups over `stages` 32-wide K stages: as many as fit in one round of `target`

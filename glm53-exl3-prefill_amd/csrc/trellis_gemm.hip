@@ -359,7 +359,7 @@ struct Mma
     uint32_t a_off[4];
     int a_step, wread, last_kb;
 
-    __device__ __forceinline__ Mma(const GemmParams& p, const Tile& t, int mw, int lane, int num_kb)
+    __device__ __forceinline__ Mma(const GemmParams& p, const Tile& t, int mw, int lane, int num_kb, int rpw)
     {
         const int tok = lane & 15, kq = lane >> 4;
         a_step = p.a_t16 ? 4 * 128 * 2 : TILE_K * 2;          // bytes per stage
@@ -371,16 +371,17 @@ struct Mma
         #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
         {
-            const int row = t.row0 + min(64 * mw + 16 * mb + tok, t.rows_valid - 1);
+            const int row = t.row0 + min(rpw * mw + 16 * mb + tok, t.rows_valid - 1);
             a_off[mb] = p.a_t16 ? (uint32_t) ((((row >> 4) - g0) * (p.size_k >> 3) + kq) * 256 + (row & 15) * 16)
                                 : (uint32_t) ((row - t.row0) * p.size_k * 2 + 16 * kq);
         }
         wread = tok * LDS_ROW + 8 * kq;
         last_kb = num_kb - 1;
     }
-    template <int MBA>
-    __device__ __forceinline__ void load_act(int kb, half8_t (&a)[4]) const
+    template <int MBA, int N>
+    __device__ __forceinline__ void load_act(int kb, half8_t (&a)[N]) const
     {
+        static_assert(MBA <= N, "activation groups");
         const int so = min(kb, last_kb) * a_step;
         #pragma unroll
         for (int mb = 0; mb < MBA; ++mb)
@@ -391,9 +392,10 @@ struct Mma
         #pragma unroll
         for (int nb = 0; nb < 8; ++nb) w[nb] = *reinterpret_cast<const half8_t*>(lds + nb * LDS_BLK + wread);
     }
-    template <int MBA>
-    __device__ __forceinline__ static void mfma(const half8_t (&w)[8], const half8_t (&a)[4], floatx4 (&acc)[4][8])
+    template <int MBA, int MBN>
+    __device__ __forceinline__ static void mfma(const half8_t (&w)[8], const half8_t (&a)[MBN], floatx4 (&acc)[MBN][8])
     {
+        static_assert(MBA <= MBN, "row groups");
         #pragma unroll
         for (int nb = 0; nb < 8; ++nb)
             #pragma unroll
@@ -403,17 +405,17 @@ struct Mma
 };
 
 // ------------------------------------------------------------------------------------------- epilogue
-// Per 16-row group of multiplying wave mw: H128 over the 128 columns of each row (lane l holds columns
+// Per 16-row group of multiplying wave mw (16 MBN rows per wave): H128 over the 128 columns of each row (lane l holds columns
 // 16 nb + 4 (l >> 4) + r: 5 butterfly stages in registers, column bit 2 across lanes l ^ 16, bit 3 across l ^ 32),
 // scale by svh / sqrt(128) (and the route weight), then store / scatter. The scatter stages each group through LDS
 // (`stage`: 16 rows x SC_ROW floats of this wave) so that every atomic instruction covers 64 consecutive floats of
 // one output row.
-template <int MODE>
-__device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int mw, int lane, floatx4 (&acc)[4][8],
+template <int MODE, int MBN>
+__device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int mw, int lane, floatx4 (&acc)[MBN][8],
                                          float* stage)
 {
     const int tok = lane & 15, kq = lane >> 4;
-    const int rows_w = t.rows_valid - 64 * mw;
+    const int rows_w = t.rows_valid - 16 * MBN * mw;
     const int out_col0 = t.which * p.n_tiles_each * TILE_N + t.nt * TILE_N;
     float sv[32];
     #pragma unroll
@@ -426,7 +428,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
         sv[4 * nb + 3] = h2f(v.y >> 16) * HAD_SCALE;
     }
     #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < MBN; ++mb)
     {
         if (16 * mb >= rows_w) break;                           // uniform over the wave
         float x[32];
@@ -440,7 +442,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
         #pragma unroll
         for (int i = 0; i < 32; i += 2) pair_butterfly32(x[i], x[i + 1]);
 
-        const int r_local = 64 * mw + 16 * mb + tok;           // this lane's row within the tile
+        const int r_local = 16 * MBN * mw + 16 * mb + tok;     // this lane's row within the tile
         const bool row_ok = r_local < t.rows_valid;
         const int64_t srow = (int64_t) t.row0 + min(r_local, t.rows_valid - 1);
         float rw = 1.0f;
@@ -505,8 +507,10 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
 // write stage s+1 into the other of two LDS buffers; issue loads for later stages.
 template <int WAVES> constexpr int lds_scatter_bytes() { return WAVES * 16 * SC_ROW * 4; }
 
-template <int BITS, int MODE, bool DENSE>
-__global__ __launch_bounds__(256, 2)
+// MBN: 16-row groups per wave. 4 (the default): 256-row tiles, two workgroups per CU. 1 (thin): 64-row tiles of small
+// batches, where most waves only decode; a quarter of the accumulators lets four workgroups share a CU.
+template <int BITS, int MODE, bool DENSE, int MBN = 4>
+__global__ __launch_bounds__(256, MBN == 4 ? 2 : 4)
 void trellis_gemm_kernel(const GemmParams p)
 {
     constexpr int SCB = lds_scatter_bytes<4>();
@@ -524,22 +528,22 @@ void trellis_gemm_kernel(const GemmParams p)
     using Dec = Decoder<BITS>;
     constexpr int NR = Dec::NR;
     const Dec dec(p, t, wave, lane, num_kb);
-    const Mma mm(p, t, wave, lane, num_kb);
-    const int rows_w = t.rows_valid - 64 * wave;          // valid rows of this wave (uniform)
+    const Mma mm(p, t, wave, lane, num_kb, 16 * MBN);
+    const int rows_w = t.rows_valid - 16 * MBN * wave;    // valid rows of this wave (uniform)
 
-    floatx4 acc[4][8];
+    floatx4 acc[MBN][8];
     #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < MBN; ++mb)
         #pragma unroll
         for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = {};
 
     // Main loop, specialised on the number of 16-row groups a wave multiplies (MBA: 0 = decode only, 1 for a wave with
-    // <= 16 valid rows, else 4). Every variant runs the same barriers. Loads past the last stage are clamped to it, so
+    // <= 16 valid rows, else MBN). Every variant runs the same barriers. Loads past the last stage are clamped to it, so
     // every path keeps the same loads in flight.
     auto mainloop = [&](auto mba_tag) {
         constexpr int MBA = decltype(mba_tag)::value;
         uint32_t raw[RAW_DEPTH][NR];
-        half8_t act[ACT_DEPTH][4];
+        half8_t act[ACT_DEPTH][MBN];
         {
             uint32_t r0[NR];
             dec.load(0, r0);
@@ -584,7 +588,7 @@ void trellis_gemm_kernel(const GemmParams p)
         }
         if (s0 < num_kb) trip(s0, std::integral_constant<int, 2>{});
     };
-    if (rows_w > 16) mainloop(std::integral_constant<int, 4>{});
+    if (MBN > 1 && rows_w > 16) mainloop(std::integral_constant<int, MBN>{});
     else if (rows_w > 0) mainloop(std::integral_constant<int, 1>{});
     else mainloop(std::integral_constant<int, 0>{});
 
@@ -621,7 +625,7 @@ void trellis_gemm_pp_kernel(const GemmParams p)
     const int num_kb = t.num_kb;
     using Dec = Decoder1<BITS>;
     const Dec dec(p, t, wave, lane, num_kb);
-    const Mma mm(p, t, wave, lane, num_kb);
+    const Mma mm(p, t, wave, lane, num_kb, 64);
     const int rows_w = t.rows_valid - 64 * wave;          // valid rows of this wave (uniform)
 
     floatx4 acc[4][8];
@@ -807,7 +811,8 @@ __global__ void decode_states_kernel(const uint32_t* __restrict__ states, uint32
 }
 
 // 512-row tiles run the 8-wave ping-pong kernel, 128- and 256-row tiles the 4-wave one (the only one built for
-// ATOMIC_F32, whose split-K launches serve small batches).
+// ATOMIC_F32, whose split-K launches serve small batches), 64-row tiles of the accumulating grouped modes the thin
+// 4-wave one.
 template <int BITS, int MODE, bool DENSE>
 int launch_gemm(const GemmParams& p, hipStream_t s)
 {
@@ -815,6 +820,14 @@ int launch_gemm(const GemmParams& p, hipStream_t s)
     const int64_t grid = (int64_t) groups8 * p.n_slots * (p.k_split > 1 ? p.k_split : 1);
     if (grid == 0) return EXL3_OK;
     if (grid > 0x7FFFFFFF) return fail("grid too large");
+    if constexpr (atomic_mode(MODE) && !DENSE)
+    {
+        if (p.tile_rows == 64)
+        {
+            trellis_gemm_kernel<BITS, MODE, DENSE, 1><<<(unsigned) grid, 256, 0, s>>>(p);
+            return EXL3_OK;
+        }
+    }
     if constexpr (MODE == MODE_ATOMIC_F32)
     {
         if (p.tile_rows > 256) return fail("mode 3 (fp32 atomic rows) takes row tiles of at most 256 rows");
@@ -857,7 +870,9 @@ extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int si
                                        const int32_t* route_index, void* out, int64_t out_rows, int mode,
                                        int k_split, void* stream)
 {
-    EXL3_CHECK(tile_rows == 128 || tile_rows == 256 || tile_rows == 512, "tile_rows must be 128, 256 or 512");
+    EXL3_CHECK(tile_rows == 128 || tile_rows == 256 || tile_rows == 512 ||
+               (tile_rows == 64 && (mode == EXL3_GEMM_SCATTER_F32 || mode == EXL3_GEMM_ATOMIC_F32)),
+               "tile_rows must be 128, 256 or 512 (or 64 in modes 1 and 3)");
     EXL3_CHECK(a_layout == EXL3_LAYOUT_ROWS || a_layout == EXL3_LAYOUT_T16, "unknown layout");
     EXL3_CHECK(bits >= 2 && bits <= 4, "unsupported bits %d (2, 3 or 4)", bits);
     EXL3_CHECK(size_k == tiles_k * 16 && size_k % 64 == 0 && size_k > 0, "K mismatch");
@@ -919,7 +934,7 @@ extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int si
     else if (mode == EXL3_GEMM_ATOMIC_F32)
     {
         EXL3_CHECK(out_rows >= a_rows, "mode 3: out fp32 [rows, n_tensors*N]");
-        EXL3_CHECK(tile_rows <= 256, "mode 3 takes row tiles of 128 or 256 rows");
+        EXL3_CHECK(tile_rows <= 256, "mode 3 takes row tiles of 64, 128 or 256 rows");
         EXL3_CHECK((reinterpret_cast<uintptr_t>(out) & 3) == 0, "out must be 4-byte aligned");
         p.out_ld = (int64_t) n_tensors * size_n_each;
         rc = launch_bits<MODE_ATOMIC_F32, false>(bits, p, s);

@@ -226,10 +226,11 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
     summed per token by combine_routes in a fixed order; mode 3 (new): fp32 atomic add of the unweighted row into
     out[r] (out [rows, n_tensors*N], caller-zeroed). tile_rows (new): rows per block-table entry, 128 for
     build_blocks' table (the reference's), 256 or 512 for a build_tiles(..., 256 | 512) table (512 runs the 8-wave
-    kernel). a_layout (new): 0 row-major a,
+    kernel), 64 in modes 1 and 3 (a thin kernel for small batches, 16 rows per wave). a_layout (new): 0 row-major a,
     1 T16 (a from row_had / act_had with dst_layout=1; a_rows gives its logical rows). k_split (new): slices of K
     whose partial products are added into out (modes 1 and 3 only)."""
-    _check(int(tile_rows) in (128, 256, 512), "tile_rows must be 128, 256 or 512")
+    _check(int(tile_rows) in (128, 256, 512) or (int(tile_rows) == 64 and mode in (1, 3)),
+           "tile_rows must be 128, 256 or 512 (or 64 in modes 1 and 3)")
     _check(int(k_split) >= 1 and int(k_split) <= a.size(1) // 64, "k_split must be in [1, K / 64]")
     _check(int(k_split) == 1 or mode in (1, 3), "k_split > 1 needs mode 1 or 3")
     _check(a_layout in (0, 1), "unknown layout")
@@ -278,7 +279,7 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
     elif mode == 3:
         _check(out.dtype == torch.float32 and out.dim() == 2 and out.size(1) == n_tensors * size_n_each and
                out.is_contiguous() and out.size(0) >= a_rows, "mode 3: out fp32 [rows, n_tensors*N]")
-        _check(int(tile_rows) <= 256, "mode 3 takes row tiles of 128 or 256 rows")
+        _check(int(tile_rows) <= 256, "mode 3 takes row tiles of 64, 128 or 256 rows")
     else:
         raise RuntimeError("mode must be 0, 1, 2 or 3")
     weighted = mode in (1, 2)

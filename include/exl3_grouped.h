@@ -186,7 +186,9 @@ int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_k, int a_la
  * partial product and adds it to the output, so k_split > 1 needs an accumulating mode: EXL3_GEMM_SCATTER_F32, or
  * EXL3_GEMM_ATOMIC_F32 -- out fp32 [a_rows, n_tensors*N_each], caller-zeroed,
  *        out[r, which*N_each + n] += H128_n(a[r] @ W'_e,which) / sqrt(128) * svh_e,which[n]
- * (valid with k_split == 1 too; tile_rows 128 or 256). 1 <= k_split <= size_k / 64; the slice count used is
+ * (valid with k_split == 1 too; tile_rows 128 or 256). Modes 1 and 3 also take tile_rows 64: a table from
+ * exl3_build_tiles(..., 64, ...), run by a thin kernel (16 rows per wave, four workgroups per CU) for small batches.
+ * 1 <= k_split <= size_k / 64; the slice count used is
  * ceil(K_stages / per_slice) with per_slice = ceil(K_stages / k_split) rounded up to even (K_stages = size_k / 32).
  */
 int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,

@@ -81,9 +81,12 @@ def test_grouped_gemm_contract():
     assert "route_index" in _gemm(mode=2)[1]
     assert "combine" in rc_and_msg("exl3_combine_routes", FAKE, FAKE, None, 4, 8, 10, 8, 6, None)[1]
     a = dict(a=FAKE, a_rows=256, size_k=512, a_layout=0, pg=FAKE, pu=None, es=32 * 16 * 64, tk=32, tn=16, bits=4,
-             sg=FAKE, su=None, ss=256, be=FAKE, br=FAKE, mb=10, tile_rows=64, counts=FAKE, row0=FAKE, E=8, tok=FAKE,
+             sg=FAKE, su=None, ss=256, be=FAKE, br=FAKE, mb=10, tile_rows=96, counts=FAKE, row0=FAKE, E=8, tok=FAKE,
              rw=FAKE, ri=None, out=FAKE, out_rows=64, mode=1)
     assert "tile_rows" in rc_and_msg("exl3_grouped_gemm_ex", *a.values(), None)[1]
+    a.update(tile_rows=64, mode=0)                                      # 64-row tiles only in the accumulating modes
+    assert "tile_rows" in rc_and_msg("exl3_grouped_gemm_ex", *a.values(), None)[1]
+    a.update(mode=1)
     a.update(tile_rows=256, a_layout=2)
     assert "layout" in rc_and_msg("exl3_grouped_gemm_ex", *a.values(), None)[1]
     assert "layout" in rc_and_msg("exl3_row_had_ex", FAKE, FAKE, FAKE, FAKE, FAKE, 256, 256, 4, 256, 1, 5, None)[1]

@@ -20,6 +20,10 @@ from exl3_grouped import synth
 
 pytestmark = pytest.mark.gpu
 LIMIT = 10.0
+# Two runs of the decode op on the same inputs: the K slices add into gate|up with fp32 atomics in a varying order, so
+# an fp16 rounding of gu can land one step apart between runs (like the reference's atomic scatter, the op is not
+# bit-reproducible); the outputs then differ by ~1e-5 relative.
+RERUN_TOL = 1e-4
 
 
 def to_np_layer(L):
@@ -141,19 +145,21 @@ def sorted_case(cfg, T, seed, dev, tile_rows=128, routing="softmax"):
     return x, ids, w, (dt(ts, dev), dt(ws, dev), dt(eor, dev), dt(counts, dev), dt(row0, dev)), be, br
 
 
-@pytest.mark.parametrize("tile_rows", [128, 256])
+@pytest.mark.parametrize("tile_rows", [64, 128, 256])
 @pytest.mark.parametrize("T", [1, 16, 300])
 def test_split_gate_up_matches_store(dev, T, tile_rows):
+    """Mode 3 (64-row tiles: the thin kernel) against the fp16 store of mode 0 on a 128-row table."""
     L, cfg = layer_case("layer1k")
     TL = device_layer("layer1k")
     x, ids, w, (ts, ws, eor, counts, row0), be, br = sorted_case(cfg, T, 11, dev, tile_rows)
+    _, _, _, _, be128, br128 = sorted_case(cfg, T, 11, dev, 128)
     R, I, H = ids.size, cfg["I"], cfg["H"]
     h13 = torch.empty(gp.t16_rows(R), H, dtype=torch.float16, device=dev)
     gp.row_had(dt(x, dev).half(), h13, ts, eor, TL.w13_suh[:, 0], True, dst_layout=1, rows=R)
-    args = (h13, TL.w13_trellis[:, 0], TL.w13_trellis[:, 1], TL.w13_svh[:, 0], TL.w13_svh[:, 1], be, br, counts, row0,
-            None, None)
+    weights = (TL.w13_trellis[:, 0], TL.w13_trellis[:, 1], TL.w13_svh[:, 0], TL.w13_svh[:, 1])
+    args = (h13, *weights, be, br, counts, row0, None, None)
     gu16 = torch.empty(R, 2 * I, dtype=torch.float16, device=dev)
-    gp.grouped_gemm(*args, gu16, 0, tile_rows=tile_rows, a_layout=1, a_rows=R)
+    gp.grouped_gemm(h13, *weights, be128, br128, counts, row0, None, None, gu16, 0, tile_rows=128, a_layout=1, a_rows=R)
     one = torch.zeros(R, 2 * I, dtype=torch.float32, device=dev)
     gp.grouped_gemm(*args, one, 3, tile_rows=tile_rows, a_layout=1, a_rows=R, k_split=1)
     torch.cuda.synchronize()
@@ -170,11 +176,12 @@ def test_split_gate_up_matches_store(dev, T, tile_rows):
         assert ((acc - one).norm() / one.norm()).item() < 1e-6, ks      # fp32 sums in another order
 
 
+@pytest.mark.parametrize("tile_rows", [64, 128])
 @pytest.mark.parametrize("T", [1, 40])
-def test_split_down_scatter_matches_unsplit(dev, T):
+def test_split_down_scatter_matches_unsplit(dev, T, tile_rows):
     L, cfg = layer_case("layer1k")
     TL = device_layer("layer1k")
-    x, ids, w, (ts, ws, eor, counts, row0), be, br = sorted_case(cfg, T, 12, dev)
+    x, ids, w, (ts, ws, eor, counts, row0), be, br = sorted_case(cfg, T, 12, dev, tile_rows)
     R, I, H = ids.size, cfg["I"], cfg["H"]
     rng = np.random.default_rng(5)
     act = dt((rng.standard_normal((gp.t16_rows(R), I)) * 3).astype(np.float16), dev)
@@ -182,7 +189,7 @@ def test_split_down_scatter_matches_unsplit(dev, T):
     for ks in (1, 2, 12):
         out = torch.zeros(T, H, dtype=torch.float32, device=dev)
         gp.grouped_gemm(act, TL.w2_trellis, None, TL.w2_svh, None, be, br, counts, row0, ts, ws, out, 1,
-                        a_layout=1, a_rows=R, k_split=ks)
+                        a_layout=1, a_rows=R, k_split=ks, tile_rows=tile_rows)
         torch.cuda.synchronize()
         outs.append(out)
     for o in outs[1:]:
@@ -204,6 +211,9 @@ def test_split_rejections(dev):
         gp.grouped_gemm(*args, torch.zeros(R, 2 * I, device=dev), 3, a_layout=1, a_rows=R, k_split=H // 64 + 1)
     with pytest.raises(RuntimeError, match="mode 3"):
         gp.grouped_gemm(*args, torch.zeros(R, 2 * I, device=dev), 3, a_layout=1, a_rows=R, tile_rows=512)
+    with pytest.raises(RuntimeError, match="64 in modes 1 and 3"):
+        gp.grouped_gemm(*args, torch.zeros(R, 2 * I, dtype=torch.float16, device=dev), 0, a_layout=1, a_rows=R,
+                        tile_rows=64)
 
 
 # ------------------------------------------------------------------------------------------- the decode op
@@ -297,7 +307,7 @@ def test_decode_reuses_workspace_and_overwrites_out(dev):
         got = decode(TL, x, ids, w, dev, out=out, workspace=ws)
         fresh = decode(TL, x, ids, w, dev)
         assert got.data_ptr() == out.data_ptr()
-        assert ((got - fresh).norm() / fresh.norm()).item() < 1e-6
+        assert ((got - fresh).norm() / fresh.norm()).item() < RERUN_TOL
 
 
 def test_decode_graph_capture_replays(dev):
@@ -339,7 +349,7 @@ def test_decode_graph_capture_replays(dev):
         torch.cuda.synchronize()
         replay = sout.clone()
         eager = decode(TL, x, ids, w, dev)
-        assert ((replay - eager).norm() / eager.norm()).item() < 1e-6, seed
+        assert ((replay - eager).norm() / eager.norm()).item() < RERUN_TOL, seed
     ref = O.expert_loop(x, ids, w, to_np_layer(L), LIMIT)
     assert O.rel_l2(replay.cpu().numpy(), ref) < 1e-3
 
