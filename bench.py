@@ -28,7 +28,7 @@ sys.path[:0] = [os.path.join(ROOT, "glm53-exl3-prefill_amd")]
 MFMA_F16_PEAK_TFLOPS = 2500.0      # MI355X dense fp16 (no sparsity)
 HBM_PEAK_GBS = 8000.0
 # the dominant kernel's name as rocprofv3 reports it (key of the committed traffic summary)
-GATE_UP_KERNEL = "trellis_gemm_kernel<{bits}, 0, false>(GemmParams)"
+GATE_UP_KERNEL = "trellis_gemm_kernel<{bits}, 0, false, 4>(GemmParams)"
 
 
 def parse():
