@@ -337,6 +337,52 @@ void build_blocks_kernel(const int32_t* __restrict__ counts, int n_experts, int 
     for (int b = n_blocks + e; b < max_blocks; b += 1024) block_expert[b] = -1;
 }
 
+// Two tables over the same rows: `tile_rows`-row tiles, except that an expert's last tile goes to a second table of
+// `thin_rows`-row tiles when it holds at most thin_rows rows (the thin GEMM kernel runs those at twice the occupancy).
+// meta = {full tiles, rows, thin tiles}. Single workgroup of 1024 threads; thread e owns expert e.
+__global__ __launch_bounds__(1024)
+void build_tiles_split_kernel(const int32_t* __restrict__ counts, int n_experts, int tile_rows, int thin_rows,
+                              int max_full, int max_thin, int32_t* __restrict__ full_expert,
+                              int32_t* __restrict__ full_row0, int32_t* __restrict__ thin_expert,
+                              int32_t* __restrict__ thin_row0, int32_t* __restrict__ meta)
+{
+    __shared__ int32_t s_rows[1024];
+    __shared__ int32_t s_full[1024];
+    __shared__ int32_t s_thin[1024];
+    const int e = threadIdx.x;
+    const int c = (e < n_experts) ? counts[e] : 0;
+    const int rem = c % tile_rows;
+    const int nthin = (rem > 0 && rem <= thin_rows) ? 1 : 0;
+    const int nfull = c / tile_rows + ((rem > thin_rows) ? 1 : 0);
+    s_rows[e] = c;
+    s_full[e] = nfull;
+    s_thin[e] = nthin;
+    __syncthreads();
+    for (int d = 1; d < 1024; d <<= 1)
+    {
+        const int vr = (e >= d) ? s_rows[e - d] : 0;
+        const int vf = (e >= d) ? s_full[e - d] : 0;
+        const int vt = (e >= d) ? s_thin[e - d] : 0;
+        __syncthreads();
+        s_rows[e] += vr;
+        s_full[e] += vf;
+        s_thin[e] += vt;
+        __syncthreads();
+    }
+    const int row0 = s_rows[e] - c;
+    const int f0 = s_full[e] - nfull, t0 = s_thin[e] - nthin;
+    if (e < n_experts)
+    {
+        for (int i = 0; i < nfull; ++i)
+            if (f0 + i < max_full) { full_expert[f0 + i] = e; full_row0[f0 + i] = row0 + i * tile_rows; }
+        if (nthin && t0 < max_thin) { thin_expert[t0] = e; thin_row0[t0] = row0 + (c / tile_rows) * tile_rows; }
+    }
+    const int n_full = s_full[1023], n_thin = s_thin[1023];
+    if (e == 0) { meta[0] = n_full; meta[1] = s_rows[1023]; meta[2] = n_thin; }
+    for (int b = n_full + e; b < max_full; b += 1024) full_expert[b] = -1;
+    for (int b = n_thin + e; b < max_thin; b += 1024) thin_expert[b] = -1;
+}
+
 // ------------------------------------------------------------------------------------------- router top-k
 constexpr int ROUTER_VPL = MAX_EXPERTS / 64;           // scores per lane (expert e = lane + 64 i)
 constexpr int ROUTER_MAX_TOPK = 16;
@@ -506,6 +552,22 @@ extern "C" int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_r
     build_blocks_kernel<<<1, 1024, 0, as_stream(stream)>>>(counts, n_experts, tile_rows, max_tiles, tile_expert,
                                                            tile_row0, meta);
     return hip_status("build_blocks");
+}
+
+extern "C" int exl3_build_tiles_split(const int32_t* counts, int n_experts, int tile_rows, int thin_rows,
+                                      int max_full, int max_thin, int32_t* full_expert, int32_t* full_row0,
+                                      int32_t* thin_expert, int32_t* thin_row0, int32_t* meta, void* stream)
+{
+    EXL3_CHECK(n_experts >= 0 && n_experts <= MAX_EXPERTS, "too many experts");
+    EXL3_CHECK((tile_rows == 128 || tile_rows == 256 || tile_rows == 512) && thin_rows == 64,
+               "tile_rows must be 128, 256 or 512 and thin_rows 64");
+    EXL3_CHECK(max_full >= 0 && max_thin >= 0, "bad table sizes");
+    EXL3_CHECK(counts && meta && (max_full == 0 || (full_expert && full_row0)) &&
+               (max_thin == 0 || (thin_expert && thin_row0)), "null pointer");
+    build_tiles_split_kernel<<<1, 1024, 0, as_stream(stream)>>>(counts, n_experts, tile_rows, thin_rows, max_full,
+                                                                max_thin, full_expert, full_row0, thin_expert,
+                                                                thin_row0, meta);
+    return hip_status("build_tiles_split");
 }
 
 extern "C" int exl3_build_blocks(const int32_t* counts, int n_experts, int max_blocks,

@@ -811,8 +811,8 @@ __global__ void decode_states_kernel(const uint32_t* __restrict__ states, uint32
 }
 
 // 512-row tiles run the 8-wave ping-pong kernel, 128- and 256-row tiles the 4-wave one (the only one built for
-// ATOMIC_F32, whose split-K launches serve small batches), 64-row tiles of the accumulating grouped modes the thin
-// 4-wave one.
+// ATOMIC_F32, whose split-K launches serve small batches), 64-row tiles of grouped modes 0, 1 and 3 the thin 4-wave
+// one.
 template <int BITS, int MODE, bool DENSE>
 int launch_gemm(const GemmParams& p, hipStream_t s)
 {
@@ -820,7 +820,7 @@ int launch_gemm(const GemmParams& p, hipStream_t s)
     const int64_t grid = (int64_t) groups8 * p.n_slots * (p.k_split > 1 ? p.k_split : 1);
     if (grid == 0) return EXL3_OK;
     if (grid > 0x7FFFFFFF) return fail("grid too large");
-    if constexpr (atomic_mode(MODE) && !DENSE)
+    if constexpr (MODE != MODE_STORE_ROUTE_F32 && !DENSE)
     {
         if (p.tile_rows == 64)
         {
@@ -871,8 +871,8 @@ extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int si
                                        int k_split, void* stream)
 {
     EXL3_CHECK(tile_rows == 128 || tile_rows == 256 || tile_rows == 512 ||
-               (tile_rows == 64 && (mode == EXL3_GEMM_SCATTER_F32 || mode == EXL3_GEMM_ATOMIC_F32)),
-               "tile_rows must be 128, 256 or 512 (or 64 in modes 1 and 3)");
+               (tile_rows == 64 && mode != EXL3_GEMM_STORE_ROUTE_F32),
+               "tile_rows must be 128, 256 or 512 (or 64 in modes 0, 1 and 3)");
     EXL3_CHECK(a_layout == EXL3_LAYOUT_ROWS || a_layout == EXL3_LAYOUT_T16, "unknown layout");
     EXL3_CHECK(bits >= 2 && bits <= 4, "unsupported bits %d (2, 3 or 4)", bits);
     EXL3_CHECK(size_k == tiles_k * 16 && size_k % 64 == 0 && size_k > 0, "K mismatch");

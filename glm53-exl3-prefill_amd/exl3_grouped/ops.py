@@ -153,6 +153,22 @@ def build_tiles(counts: torch.Tensor, tile_expert: torch.Tensor, tile_row0: torc
 
 
 # ------------------------------------------------------------------------------------------- Hadamard passes
+def build_tiles_split(counts: torch.Tensor, full_expert: torch.Tensor, full_row0: torch.Tensor,
+                      thin_expert: torch.Tensor, thin_row0: torch.Tensor, meta: torch.Tensor, tile_rows: int = 256,
+                      thin_rows: int = 64) -> None:
+    """Two tile tables (new): `tile_rows`-row tiles with each expert's small last tile (<= thin_rows rows) moved to a
+    `thin_rows`-row table for the grouped GEMM's thin kernel. meta int32[3] = {full tiles, rows, thin tiles}."""
+    for t in (counts, full_expert, full_row0, thin_expert, thin_row0, meta):
+        _check(t.dtype == torch.int32 and t.is_contiguous(), "int32 contiguous tensors")
+    _check(full_row0.numel() >= full_expert.numel() and thin_row0.numel() >= thin_expert.numel() and
+           meta.numel() >= 3, "tables: row0 at least as long as expert, meta int32[3]")
+    dev = _require_cuda(counts, full_expert, full_row0, thin_expert, thin_row0, meta)
+    with _On(dev) as s:
+        _lib.call("exl3_build_tiles_split", _p(counts), counts.numel(), int(tile_rows), int(thin_rows),
+                  full_expert.numel(), thin_expert.numel(), _p(full_expert), _p(full_row0), _p(thin_expert),
+                  _p(thin_row0), _p(meta), s)
+
+
 def t16_rows(rows: int) -> int:
     """Rows a T16-layout buffer of `rows` logical rows holds (whole 16-row groups)."""
     return (rows + 15) // 16 * 16
@@ -226,11 +242,11 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
     summed per token by combine_routes in a fixed order; mode 3 (new): fp32 atomic add of the unweighted row into
     out[r] (out [rows, n_tensors*N], caller-zeroed). tile_rows (new): rows per block-table entry, 128 for
     build_blocks' table (the reference's), 256 or 512 for a build_tiles(..., 256 | 512) table (512 runs the 8-wave
-    kernel), 64 in modes 1 and 3 (a thin kernel for small batches, 16 rows per wave). a_layout (new): 0 row-major a,
+    kernel), 64 in modes 0, 1 and 3 (a thin kernel for small tiles, 16 rows per wave). a_layout (new): 0 row-major a,
     1 T16 (a from row_had / act_had with dst_layout=1; a_rows gives its logical rows). k_split (new): slices of K
     whose partial products are added into out (modes 1 and 3 only)."""
-    _check(int(tile_rows) in (128, 256, 512) or (int(tile_rows) == 64 and mode in (1, 3)),
-           "tile_rows must be 128, 256 or 512 (or 64 in modes 1 and 3)")
+    _check(int(tile_rows) in (128, 256, 512) or (int(tile_rows) == 64 and mode in (0, 1, 3)),
+           "tile_rows must be 128, 256 or 512 (or 64 in modes 0, 1 and 3)")
     _check(int(k_split) >= 1 and int(k_split) <= a.size(1) // 64, "k_split must be in [1, K / 64]")
     _check(int(k_split) == 1 or mode in (1, 3), "k_split > 1 needs mode 1 or 3")
     _check(a_layout in (0, 1), "unknown layout")

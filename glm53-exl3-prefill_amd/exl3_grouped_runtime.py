@@ -11,6 +11,8 @@ set) and layers without w13_trellis keep the original path untouched.
 Env:
   EXL3_GROUPED_PREFILL=1     enable (read by the hook)
   EXL3_GROUPED_DECODE=0      leave decode calls (tokens <= cap) to the original path (default: moe_decode)
+  EXL3_GROUPED_THIN=0        run every expert tile on the main GEMM kernel (default: an expert's last tile of <= 64
+                             rows runs on the thin kernel, four workgroups per CU, in a second launch; atomic scatter)
   EXL3_GROUPED_SCATTER=...   down-projection output: "atomic" (fp32 atomic scatter by token, the reference's
                              method) or "combine" (per-route fp32 rows + a fixed-order sum per token: deterministic)
   EXL3_GROUPED_LIB=<path>    prebuilt libexl3_grouped.so (default: exl3_grouped/libexl3_grouped.so beside this file)
@@ -68,14 +70,23 @@ def tile_rows() -> int:
     return int(v)
 
 
+def thin_tiles_enabled() -> bool:
+    return os.environ.get("EXL3_GROUPED_THIN", "1") != "0"
+
+
+THIN_ROWS = 64
+
+
 def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, layer, limit: float,
                     stage_events: list | None = None, scatter: str | None = None,
-                    rows_per_tile: int | None = None) -> torch.Tensor:
+                    rows_per_tile: int | None = None, thin_tiles: bool | None = None) -> torch.Tensor:
     """x2d [T, K] (any float dtype), ids [T, topk] (int64 or int32), weights [T, topk] -> out [T, K] fp32.
     Restates kernel/exl3_grouped_runtime.py:50-83 with the route sort on the GPU (sort_routes).
     stage_events: if a list is given, a timing event recorded on the current stream after each stage is appended
     as (stage name, event), after a leading ("start", event).
-    scatter: "atomic" or "combine" (default: EXL3_GROUPED_SCATTER, else "atomic")."""
+    scatter: "atomic" or "combine" (default: EXL3_GROUPED_SCATTER, else "atomic").
+    thin_tiles: run each expert's last tile of <= 64 rows on the thin GEMM kernel (default: EXL3_GROUPED_THIN, else
+    on; atomic scatter only). Same arithmetic per row, so the same result."""
     gp = _load_ext()
     scatter = scatter or scatter_mode()
 
@@ -112,17 +123,28 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     max_blocks = R // tr + E
     block_expert = torch.empty(max_blocks, dtype=torch.int32, device=dev)
     block_row0 = torch.empty_like(block_expert)
-    meta = torch.zeros(2, dtype=torch.int32, device=dev)
-    gp.build_tiles(counts, block_expert, block_row0, meta, tr)
+    thin = (thin_tiles_enabled() if thin_tiles is None else thin_tiles) and scatter == "atomic"
+    if thin:
+        # each expert's last tile of <= 64 rows goes to a second table, run by the thin kernel
+        thin_expert = torch.empty(min(E, R), dtype=torch.int32, device=dev)
+        thin_row0 = torch.empty_like(thin_expert)
+        meta = torch.zeros(3, dtype=torch.int32, device=dev)
+        gp.build_tiles_split(counts, block_expert, block_row0, thin_expert, thin_row0, meta, tr, THIN_ROWS)
+    else:
+        meta = torch.zeros(2, dtype=torch.int32, device=dev)
+        gp.build_tiles(counts, block_expert, block_row0, meta, tr)
     mark("build_blocks")
     # the GEMMs' activation operands (h13, act) are written in the T16 layout, which makes their loads contiguous
     h13 = torch.empty(gp.t16_rows(R), K, dtype=torch.float16, device=dev)
     gp.row_had(x16, h13, token_sorted, expert_of_row, layer.w13_suh[:, 0], True, dst_layout=1, rows=R)
     mark("row_had")
     gu = torch.empty(R, 2 * I, dtype=torch.float16, device=dev)
-    gp.grouped_gemm(h13, layer.w13_trellis[:, 0], layer.w13_trellis[:, 1], layer.w13_svh[:, 0], layer.w13_svh[:, 1],
-                    block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 0,
+    w13 = (layer.w13_trellis[:, 0], layer.w13_trellis[:, 1], layer.w13_svh[:, 0], layer.w13_svh[:, 1])
+    gp.grouped_gemm(h13, *w13, block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 0,
                     tile_rows=tr, a_layout=1, a_rows=R)
+    if thin:
+        gp.grouped_gemm(h13, *w13, thin_expert, thin_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 0,
+                        tile_rows=THIN_ROWS, a_layout=1, a_rows=R)
     mark("gemm_gate_up")
     act = torch.empty(gp.t16_rows(R), I, dtype=torch.float16, device=dev)
     gp.act_had(gu, act, expert_of_row, layer.w2_suh, float(limit), dst_layout=1)
@@ -133,6 +155,10 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
         gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
                         block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, out, 1,
                         tile_rows=tr, a_layout=1, a_rows=R)
+        if thin:
+            gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
+                            thin_expert, thin_row0, counts, expert_row0, token_sorted, weight_sorted, out, 1,
+                            tile_rows=THIN_ROWS, a_layout=1, a_rows=R)
         mark("gemm_down_scatter")
         return out
     partial = torch.empty(R, K, dtype=torch.float32, device=dev)

@@ -100,6 +100,16 @@ int exl3_build_blocks(const int32_t* counts, int n_experts, int max_blocks,
  * reference counterpart): the grouped GEMM amortises each decoded trellis tile over up to 256 (512) rows of one
  * expert when given a 256-row (512-row) table (max_tiles >= R/tile_rows + n_experts).
  */
+/*
+ * Two row-tile tables for one launch pair (new): tile_rows-row tiles (128, 256 or 512), except that each expert's
+ * last tile goes to a second table of thin_rows-row tiles (64) when it holds at most thin_rows rows;
+ * the grouped GEMM runs the second table on its thin kernel (modes 0, 1, 3 with tile_rows 64). Tails are -1 as in
+ * exl3_build_tiles; meta int32[3] = {full tiles, rows, thin tiles}. Bounds: max_full >= R/tile_rows + n_experts,
+ * max_thin >= min(n_experts, R).
+ */
+int exl3_build_tiles_split(const int32_t* counts, int n_experts, int tile_rows, int thin_rows, int max_full,
+                           int max_thin, int32_t* full_expert, int32_t* full_row0, int32_t* thin_expert,
+                           int32_t* thin_row0, int32_t* meta, void* stream);
 int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_rows, int max_tiles,
                      int32_t* tile_expert, int32_t* tile_row0, int32_t* meta, void* stream);
 
@@ -186,8 +196,8 @@ int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_k, int a_la
  * partial product and adds it to the output, so k_split > 1 needs an accumulating mode: EXL3_GEMM_SCATTER_F32, or
  * EXL3_GEMM_ATOMIC_F32 -- out fp32 [a_rows, n_tensors*N_each], caller-zeroed,
  *        out[r, which*N_each + n] += H128_n(a[r] @ W'_e,which) / sqrt(128) * svh_e,which[n]
- * (valid with k_split == 1 too; tile_rows 128 or 256). Modes 1 and 3 also take tile_rows 64: a table from
- * exl3_build_tiles(..., 64, ...), run by a thin kernel (16 rows per wave, four workgroups per CU) for small batches.
+ * (valid with k_split == 1 too; tile_rows 128 or 256). Modes 0, 1 and 3 also take tile_rows 64: a table from
+ * exl3_build_tiles(..., 64, ...), run by a thin kernel (16 rows per wave, four workgroups per CU) for small tiles.
  * 1 <= k_split <= size_k / 64; the slice count used is
  * ceil(K_stages / per_slice) with per_slice = ceil(K_stages / k_split) rounded up to even (K_stages = size_k / 32).
  */

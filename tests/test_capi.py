@@ -84,7 +84,7 @@ def test_grouped_gemm_contract():
              sg=FAKE, su=None, ss=256, be=FAKE, br=FAKE, mb=10, tile_rows=96, counts=FAKE, row0=FAKE, E=8, tok=FAKE,
              rw=FAKE, ri=None, out=FAKE, out_rows=64, mode=1)
     assert "tile_rows" in rc_and_msg("exl3_grouped_gemm_ex", *a.values(), None)[1]
-    a.update(tile_rows=64, mode=0)                                      # 64-row tiles only in the accumulating modes
+    a.update(tile_rows=64, mode=2)                                      # no 64-row tiles for per-route rows
     assert "tile_rows" in rc_and_msg("exl3_grouped_gemm_ex", *a.values(), None)[1]
     a.update(mode=1)
     a.update(tile_rows=256, a_layout=2)
@@ -316,4 +316,15 @@ def test_route_prep_small_contract():
     rc, msg = call(za=ctypes.c_void_p(0x1004), na=8)
     assert rc == _lib.EXL3_ERR_ARG and "aligned" in msg
     rc, msg = call(ids=None)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "null pointer"
+
+
+def test_build_tiles_split_contract():
+    rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 8, 256, 128, 10, 8, FAKE, FAKE, FAKE, FAKE, FAKE, None)
+    assert rc == _lib.EXL3_ERR_ARG and "thin_rows 64" in msg
+    rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 8, 64, 64, 10, 8, FAKE, FAKE, FAKE, FAKE, FAKE, None)
+    assert rc == _lib.EXL3_ERR_ARG and "tile_rows" in msg
+    rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 1025, 256, 64, 10, 8, FAKE, FAKE, FAKE, FAKE, FAKE, None)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "too many experts"
+    rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 8, 256, 64, 10, 8, FAKE, FAKE, None, FAKE, FAKE, None)
     assert rc == _lib.EXL3_ERR_ARG and msg == "null pointer"

@@ -144,6 +144,55 @@ def test_build_blocks_bit_exact(dev, kind, T, E, k, tile_rows):
 
 
 # ------------------------------------------------------------------------------------------- router top-k
+def split_tables(counts, tile_rows, thin_rows=64):
+    """Closed form of exl3_build_tiles_split: tile_rows-row tiles, an expert's last tile of <= thin_rows rows in a
+    second table."""
+    full, thin, row = [], [], 0
+    for e, c in enumerate(counts.tolist()):
+        nf, rem = divmod(c, tile_rows)
+        full += [(e, row + i * tile_rows) for i in range(nf)]
+        if rem > thin_rows:
+            full.append((e, row + nf * tile_rows))
+        elif rem > 0:
+            thin.append((e, row + nf * tile_rows))
+        row += c
+    return full, thin, row
+
+
+@pytest.mark.parametrize("tile_rows", [128, 256, 512])
+@pytest.mark.parametrize("kind,T,E,k", ROUTINGS)
+def test_build_tiles_split_bit_exact(dev, kind, T, E, k, tile_rows):
+    ids, w = synth.make_routing(kind, T, E, k, seed=T + 2)
+    counts = np.bincount(ids.ravel(), minlength=E).astype(np.int32)
+    R = ids.size
+    mf, mt = R // tile_rows + E, min(E, R)
+    full, thin, rows = split_tables(counts, tile_rows)
+    # the two tables hold exactly the tiles of the one-table schedule (oracle build_blocks), small last tiles moved
+    rbe, rbr, rmeta = O.build_blocks(counts, mf, init=-7, tile_rows=tile_rows)
+    n = int(rmeta[0])
+    assert sorted(full + thin) == sorted(zip(rbe[:n].tolist(), rbr[:n].tolist()))
+    t = [torch.full((m,), -7, dtype=torch.int32, device=dev) for m in (mf, mf, mt, mt)]
+    meta = torch.full((3,), -5, dtype=torch.int32, device=dev)
+    gp.build_tiles_split(t16(counts, dev), *t, meta, tile_rows, 64)
+    fe, fr, te, tr_ = (x.cpu().numpy() for x in t)
+    assert meta.tolist() == [len(full), rows, len(thin)]
+    assert list(zip(fe[:len(full)].tolist(), fr[:len(full)].tolist())) == full
+    assert list(zip(te[:len(thin)].tolist(), tr_[:len(thin)].tolist())) == thin
+    assert (fe[len(full):] == -1).all() and (te[len(thin):] == -1).all()
+
+
+def test_prefill_thin_tiles_match_one_table(dev):
+    """Each expert's small last tile on the thin kernel gives the one-table result (the per-row arithmetic is the
+    same; the down scatter's atomics may add in another order)."""
+    L, x, ids, w, cfg = synth.make_config("headline", seed=3, T=2048)
+    TL = synth.to_device(L, dev)
+    args = (t16(x, dev), t16(ids, dev), t16(w, dev), TL, LIMIT)
+    a = rt.grouped_prefill(*args, scatter="atomic", thin_tiles=True)
+    b = rt.grouped_prefill(*args, scatter="atomic", thin_tiles=False)
+    torch.cuda.synchronize()
+    assert ((a - b).norm() / b.norm()).item() < 1e-6
+
+
 def _margins(logits, bias, k):
     """Per token: is the chosen set unambiguous (k-th and (k+1)-th selection scores more than 1e-5 apart), and is the
     order too (every adjacent pair among the first k + 1 apart)? fp32 sigmoids may differ by an ulp between devices."""
