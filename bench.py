@@ -7,8 +7,9 @@ inputs resident in HBM before timing starts. A step is one full grouped_prefill 
 gather + input Hadamard, gate|up GEMM, SwiGLU + down Hadamard, down GEMM with fp32 atomic scatter).
 
 Prints ONE JSON line: value = routed tokens/s (T*topk / step time); ms_per_step = per-layer MoE ms; roofline of the
-dominant kernel (the gate|up grouped GEMM, MFMA-bound: algorithmic 4*R*H*I flop per launch over its event-timed
-average duration on the launch stream); cpu_baseline = the CPU oracle's expert loop on a bounded sample.
+dominant stage (the gate|up grouped GEMM: full expert tiles on the main kernel, each expert's last tile of <= 64 rows on
+the thin kernel; MFMA-bound: algorithmic 4*R*H*I flop per stage call over its event-timed average duration on the
+launch stream); cpu_baseline = the CPU oracle's expert loop on a bounded sample.
 
   python bench.py [--steps K] [--warmup W] [--tokens T] [--bits B] [--routing R] [--no-cpu-baseline]
   python bench.py --sweep          (extra lines for T = 1024, 2048, 4096, 8192; not the driver's contract line)
@@ -27,8 +28,10 @@ sys.path[:0] = [os.path.join(ROOT, "glm53-exl3-prefill_amd")]
 
 MFMA_F16_PEAK_TFLOPS = 2500.0      # MI355X dense fp16 (no sparsity)
 HBM_PEAK_GBS = 8000.0
-# the dominant kernel's name as rocprofv3 reports it (key of the committed traffic summary)
-GATE_UP_KERNEL = "trellis_gemm_kernel<{bits}, 0, false, 4>(GemmParams)"
+# the dominant stage's kernels as rocprofv3 reports them (keys of the committed traffic summary): the gate|up GEMM
+# runs full expert tiles on the main kernel and each expert's last tile of <= 64 rows on the thin one
+GATE_UP_KERNELS = ("trellis_gemm_kernel<{bits}, 0, false, 4>(GemmParams)",
+                   "trellis_gemm_kernel<{bits}, 0, false, 1>(GemmParams)")
 
 
 def parse():
@@ -68,15 +71,16 @@ def copy_probe(mib: int):
     print(json.dumps({"copy_probe_bytes_per_launch": n * 4, "launches": 5}), flush=True)
 
 
-def traffic_from_profiles(workload: str, kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary of `workload`
-    (profiles/grouped_prefill_<workload>_traffic.md: FETCH_SIZE and WRITE_SIZE passes scaled by a copy-kernel
-    calibration, in its fenced JSON block), or None if there is no such summary."""
+def traffic_from_profiles(workload: str, kernels):
+    """HBM bytes per call of the stage made of `kernels` (one launch each) from the committed rocprofv3 --pmc summary
+    of `workload` (profiles/grouped_prefill_<workload>_traffic.md: FETCH_SIZE and WRITE_SIZE passes scaled by a
+    copy-kernel calibration, in its fenced JSON block), or None if the summary or one of the kernels is missing."""
     path = os.path.join(ROOT, "profiles", f"grouped_prefill_{workload}_traffic.md")
     try:
         text = open(path).read()
         block = text.split("```json", 1)[1].split("```", 1)[0]
-        return json.loads(block)["bytes_per_launch"].get(kernel)
+        per = json.loads(block)["bytes_per_launch"]
+        return sum(per[k] for k in kernels)
     except (OSError, IndexError, ValueError, KeyError):
         return None
 
@@ -134,6 +138,8 @@ def run(args, T=None, emit=True):
                           "gemm_tflops_both": round(both_gemm_tflops, 1),
                           "layer_tflops": round(layer_tflops, 1)}), file=sys.stderr, flush=True)
     workload = f"{cfg_name}: E={E} H={H} I={I} {bits}bpw T={T_} top{k} {cfg['routing']}"
+    thin = rt.thin_tiles_enabled() and scatter == "atomic"
+    gate_up_kernels = [kname.format(bits=bits) for kname in (GATE_UP_KERNELS if thin else GATE_UP_KERNELS[:1])]
     result = {
         "metric": "per-layer MoE ms + routed tok/s, 288 experts @8192 tok; % MFMA peak",
         "value": round(R / (ms_per_step * 1e-3), 1),
@@ -154,11 +160,11 @@ def run(args, T=None, emit=True):
         "stage_ms": {n: round(v, 4) for n, v in stage_avg.items()},
         "gemm_tflops_gate_up_and_down": round(both_gemm_tflops, 1),
         "mfma_frac_layer": round(layer_tflops / MFMA_F16_PEAK_TFLOPS, 4),
-        "roofline": {"kernel": f"grouped_gemm gate|up ({GATE_UP_KERNEL.format(bits=bits)})", "bound": "mfma",
+        "roofline": {"kernel": "grouped_gemm gate|up stage (" + " + ".join(gate_up_kernels) + ")", "bound": "mfma",
                      "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
-                     "traffic": traffic_from_profiles(cfg_name, GATE_UP_KERNEL.format(bits=bits)),
-                     "work_per_launch": f"4*R*H*I = {gate_up_flop:.4g} flop (R={R} routed rows)"},
+                     "traffic": traffic_from_profiles(cfg_name, gate_up_kernels),
+                     "work_per_launch": f"4*R*H*I = {gate_up_flop:.4g} flop (R={R} routed rows) per stage call"},
     }
     return result, (L, x, ids, w, cfg)
 
