@@ -21,8 +21,8 @@
 //   * Workgroups are laid out XCD-aware: the column tiles of one row tile share an XCD (and its L2).
 //   * Activations and trellis words are read through buffer resources: fixed per-lane offsets plus a scalar stage
 //     offset, and zero instead of a fault outside the operand.
-// 512-row tiles run an 8-wave ping-pong variant (trellis_gemm_pp_kernel): two groups of four waves alternate between
-// MFMA phases and decode/load phases, each decoded weight feeding 512 rows.
+// Variants of the same kernel: 16 rows per wave (64-row tiles, four workgroups per CU) for small tiles, and 8 waves
+// (512-row tiles, one workgroup per CU, each wave decoding one chunk per lane) for 512-row tiles and large dense GEMMs.
 #include "exl3_common.h"
 #include "trellis_decode.h"
 
@@ -501,7 +501,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
     }
 }
 
-// ------------------------------------------------------------------------------------------- kernel: 4 waves
+// ------------------------------------------------------------------------------------------- kernel
 // 128- and 256-row tiles: every wave decodes a quarter of each stage and multiplies its own 64 rows; two workgroups
 // share a CU. Pipeline of stage s: barrier; read stage s's weight fragments; decode stage s+1 while stage s's MFMAs run;
 // write stage s+1 into the other of two LDS buffers; issue loads for later stages.
@@ -509,11 +509,14 @@ template <int WAVES> constexpr int lds_scatter_bytes() { return WAVES * 16 * SC_
 
 // MBN: 16-row groups per wave. 4 (the default): 256-row tiles, two workgroups per CU. 1 (thin): 64-row tiles of small
 // batches, where most waves only decode; a quarter of the accumulators lets four workgroups share a CU.
-template <int BITS, int MODE, bool DENSE, int MBN = 4>
-__global__ __launch_bounds__(256, MBN == 4 ? 2 : 4)
+// WAVES = 8: 512-row tiles, one workgroup per CU; each wave decodes half as much of every stage (one chunk per lane),
+// so a decoded weight feeds twice the rows for the same VALU work per wave.
+template <int BITS, int MODE, bool DENSE, int MBN = 4, int WAVES = 4>
+__global__ __launch_bounds__(64 * WAVES, WAVES == 8 ? 1 : (MBN == 4 ? 2 : 4))
 void trellis_gemm_kernel(const GemmParams p)
 {
-    constexpr int SCB = lds_scatter_bytes<4>();
+    static_assert(WAVES == 4 || (WAVES == 8 && MBN == 4), "8-wave workgroups run 64 rows per wave");
+    constexpr int SCB = lds_scatter_bytes<WAVES>();
     constexpr int LDS_BYTES = (atomic_mode(MODE) && SCB > LDS_MAIN_BYTES) ? SCB : LDS_MAIN_BYTES;
     __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
     uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
@@ -525,7 +528,7 @@ void trellis_gemm_kernel(const GemmParams p)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int num_kb = t.num_kb;
-    using Dec = Decoder<BITS>;
+    using Dec = typename std::conditional<WAVES == 8, Decoder1<BITS>, Decoder<BITS>>::type;
     constexpr int NR = Dec::NR;
     const Dec dec(p, t, wave, lane, num_kb);
     const Mma mm(p, t, wave, lane, num_kb, 16 * MBN);
@@ -593,142 +596,6 @@ void trellis_gemm_kernel(const GemmParams p)
     else mainloop(std::integral_constant<int, 0>{});
 
     if constexpr (atomic_mode(MODE)) __syncthreads();            // decoded tiles are dead; LDS becomes staging
-    if (rows_w <= 0) return;
-    epilogue<MODE>(p, t, wave, lane, acc, reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW));
-}
-
-// ------------------------------------------------------------------------------------------- kernel: ping-pong
-// 512-row tiles with 8 waves in two groups of four (group g = waves 4g .. 4g + 3, one wave of each group per SIMD;
-// wave w multiplies rows 64 w ..). The two waves of a SIMD take turns: while one group runs a stage's MFMAs from weight
-// fragments already in registers, the other group reads its next fragments from LDS, decodes its half of a later stage
-// (group g decodes k-tile g of every stage, one chunk per lane) and issues loads. The MFMA pipe of each SIMD is fed by
-// one group or the other in every phase, and the decode VALU work runs beside it. Phases, each ended by a barrier:
-//   A(s): group 0 multiplies stage s;  group 1 reads W(s), decodes its half of W(s + 1)
-//   B(s): group 1 multiplies stage s;  group 0 reads W(s + 1), decodes its half of W(s + 2)
-// W(s) lives in LDS buffer s % 2. Group 0 reaches its epilogue while group 1 runs the last phase.
-template <int BITS, int MODE, bool DENSE>
-__global__ __launch_bounds__(512, 1)
-void trellis_gemm_pp_kernel(const GemmParams p)
-{
-    constexpr int SCB = lds_scatter_bytes<8>();
-    constexpr int LDS_BYTES = (atomic_mode(MODE) && SCB > LDS_MAIN_BYTES) ? SCB : LDS_MAIN_BYTES;
-    __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
-    uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
-
-    int group, slot;
-    xcd_group_slot((int) blockIdx.x, p.k_split > 1 ? p.n_slots * p.k_split : p.n_slots, group, slot);
-    Tile t;
-    if (!resolve_tile<DENSE>(p, group, slot, t)) return;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int g = wave >> 2;
-    const int num_kb = t.num_kb;
-    using Dec = Decoder1<BITS>;
-    const Dec dec(p, t, wave, lane, num_kb);
-    const Mma mm(p, t, wave, lane, num_kb, 64);
-    const int rows_w = t.rows_valid - 64 * wave;          // valid rows of this wave (uniform)
-
-    floatx4 acc[4][8];
-    #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-        #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = {};
-
-    // Each group runs its own copy of the loop (G is a compile-time constant), so neither instruction stream carries
-    // the other's branches and the compiler's wait counts follow the loads of one role only. Both copies execute the
-    // same barriers in the same order.
-    // A phase boundary: the barrier, with scheduling fences so that the compiler keeps every MFMA and decode
-    // instruction in the phase it was written in (register-only work may otherwise move across the barrier).
-    auto phase_end = [] {
-        __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    auto mainloop = [&](auto mba_tag, auto g_tag) {
-        constexpr int MBA = decltype(mba_tag)::value;
-        constexpr int G = decltype(g_tag)::value;
-        uint32_t raw[RAW_DEPTH][Dec::NR];                   // slot d % RAW_DEPTH: this wave's half of stage d
-        half8_t act[2][4];                                  // slot s % 2: stage s
-        half8_t w[8];
-        auto decode_to = [&](int d, int slot_d, uint16_t* dst) {
-            typename Dec::Out o;
-            dec.decode(raw[slot_d], o);
-            dec.store(o, dst);
-            dec.load(d + RAW_DEPTH, raw[slot_d]);
-        };
-        #pragma unroll
-        for (int d = 0; d < RAW_DEPTH; ++d) dec.load(d, raw[d]);
-        mm.load_act<MBA>(0, act[0]);
-        mm.load_act<MBA>(1, act[1]);
-        decode_to(0, 0, lds_b);                             // both groups: their halves of W(0)
-        phase_end();
-        if constexpr (G == 0)                               // group 0's phase B(-1)
-        {
-            if constexpr (MBA > 0) mm.read_w(lds_b, w);
-            if (num_kb > 1) decode_to(1, 1, lds_b + LDS_TILE);
-        }
-        phase_end();
-        // N stages from s0 (a multiple of RAW_DEPTH, so every buffer index is compile-time). The last trip (TAIL)
-        // skips the work past the last stage at compile time: no branch inside a trip, so wait counts stay exact.
-        auto trip = [&](int s0, auto n_tag, auto tail_tag) {
-            constexpr int N = decltype(n_tag)::value;
-            constexpr bool TAIL = decltype(tail_tag)::value;
-            static_for<N>([&](auto u_tag) {
-                constexpr int U = decltype(u_tag)::value;
-                constexpr bool HAS1 = !TAIL || U + 1 < N;           // stage s + 1 exists
-                constexpr bool HAS2 = !TAIL || U + 2 < N;           // stage s + 2 exists
-                const int s = s0 + U;
-                // phase A(s)
-                if constexpr (G == 0)
-                {
-                    Mma::mfma<MBA>(w, act[U & 1], acc);
-                    mm.load_act<MBA>(s + 2, act[U & 1]);
-                }
-                else
-                {
-                    if constexpr (MBA > 0) mm.read_w(lds_b + (U & 1) * LDS_TILE, w);
-                    if constexpr (HAS1) decode_to(s + 1, (U + 1) % RAW_DEPTH, lds_b + ((U + 1) & 1) * LDS_TILE);
-                }
-                phase_end();
-                // phase B(s)
-                if constexpr (G == 1)
-                {
-                    Mma::mfma<MBA>(w, act[U & 1], acc);
-                    mm.load_act<MBA>(s + 2, act[U & 1]);
-                }
-                else
-                {
-                    if constexpr (MBA > 0 && HAS1) mm.read_w(lds_b + ((U + 1) & 1) * LDS_TILE, w);
-                    if constexpr (HAS2) decode_to(s + 2, (U + 2) % RAW_DEPTH, lds_b + (U & 1) * LDS_TILE);
-                }
-                if constexpr (HAS1) phase_end();
-            });
-        };
-        // num_kb is even (K % 64 == 0): whole trips of RAW_DEPTH stages and possibly a 2-stage tail.
-        using full = std::integral_constant<int, RAW_DEPTH>;
-        using half_trip = std::integral_constant<int, 2>;
-        using no = std::false_type;
-        using yes = std::true_type;
-        const bool rem2 = (num_kb % RAW_DEPTH) != 0;
-        const int body = rem2 ? num_kb / RAW_DEPTH : num_kb / RAW_DEPTH - 1;     // trips before the tail
-        int s0 = 0;
-        if (body > 0)
-        {
-            trip(0, full{}, no{});
-            for (s0 = RAW_DEPTH; s0 < body * RAW_DEPTH; s0 += RAW_DEPTH) trip(s0, full{}, no{});
-        }
-        if (rem2) trip(s0, half_trip{}, yes{});
-        else trip(s0, full{}, yes{});
-    };
-    auto by_rows = [&](auto g_tag) {
-        if (rows_w > 16) mainloop(std::integral_constant<int, 4>{}, g_tag);
-        else if (rows_w > 0) mainloop(std::integral_constant<int, 1>{}, g_tag);
-        else mainloop(std::integral_constant<int, 0>{}, g_tag);
-    };
-    if (g == 0) by_rows(std::integral_constant<int, 0>{});
-    else by_rows(std::integral_constant<int, 1>{});
-
-    // No barrier: after the last phase no wave touches the weight buffers, and the scatter's staging rows are per wave.
     if (rows_w <= 0) return;
     epilogue<MODE>(p, t, wave, lane, acc, reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW));
 }
@@ -810,9 +677,8 @@ __global__ void decode_states_kernel(const uint32_t* __restrict__ states, uint32
     if (i + 1 < n2) out[i + 1] = wb;
 }
 
-// 512-row tiles run the 8-wave ping-pong kernel, 128- and 256-row tiles the 4-wave one (the only one built for
-// ATOMIC_F32, whose split-K launches serve small batches), 64-row tiles of grouped modes 0, 1 and 3 the thin 4-wave
-// one.
+// 512-row tiles run the 8-wave variant, 128- and 256-row tiles the 4-wave kernel (the only one built for ATOMIC_F32,
+// whose split-K launches serve small batches), 64-row tiles of grouped modes 0, 1 and 3 the thin 4-wave variant.
 template <int BITS, int MODE, bool DENSE>
 int launch_gemm(const GemmParams& p, hipStream_t s)
 {
@@ -834,7 +700,7 @@ int launch_gemm(const GemmParams& p, hipStream_t s)
     }
     else if (p.tile_rows > 256)
     {
-        trellis_gemm_pp_kernel<BITS, MODE, DENSE><<<(unsigned) grid, 512, 0, s>>>(p);
+        trellis_gemm_kernel<BITS, MODE, DENSE, 4, 8><<<(unsigned) grid, 512, 0, s>>>(p);
         return EXL3_OK;
     }
     trellis_gemm_kernel<BITS, MODE, DENSE><<<(unsigned) grid, 256, 0, s>>>(p);

@@ -61,7 +61,8 @@ def scatter_mode() -> str:
 
 def tile_rows() -> int:
     """Rows per expert row tile of the grouped GEMMs (EXL3_GROUPED_TILE_ROWS, default TILE_ROWS): 512-row tiles run
-    the 8-wave GEMM kernel, which decodes each trellis stage once for twice the MFMA work."""
+    the 8-wave GEMM kernel, which decodes each trellis stage once for twice the MFMA work (slower than the 256-row
+    default on the configs measured)."""
     v = os.environ.get("EXL3_GROUPED_TILE_ROWS")
     if v is None:
         return TILE_ROWS
