@@ -15,7 +15,10 @@
  *
  * Trellis tensors: [tiles_k, tiles_n, 16*bits] int16 per matrix (bits in {2,3,4}); a tile holds the 16x16
  * weights W'[16 tk + k][16 tn + n] as 256 bits-wide symbols with a tail-biting 16-bit state window and the
- * MCG codebook (the bit-level spec is written out in oracle/exl3_oracle.c and DESIGN.md).
+ * MCG codebook: position p's state is stream bits [(p+1)K - 16, (p+1)K) mod 256K of the tile's little-endian dword
+ * stream, x = state * 0xCBAC1FED mod 2^32, y = (x & 0x8FFF8FFF) ^ 0x3B603B60, w = fp16(y.lo) + fp16(y.hi), and
+ * position p = 8c + j sits at k = 2(c & 3) + (j & 1) + 8((j >> 1) & 1), n = (c >> 2) + 8(j >> 2) (the bit-level
+ * restatement is oracle/exl3_oracle.c).
  */
 #ifndef EXL3_GROUPED_H
 #define EXL3_GROUPED_H
