@@ -70,19 +70,23 @@ DecodeLayout decode_layout(int64_t tokens, int topk, int n_experts, int hidden, 
     return L;
 }
 
+#ifndef EXL3_DECODE_WG_PER_CU
+#define EXL3_DECODE_WG_PER_CU 4
+#endif
+
 // Workgroups a launch should put on the device: four resident thin-kernel workgroups per CU.
 int target_workgroups(hipStream_t)
 {
     static int cus[64] = {};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return EXL3_DECODE_WG_PER_CU * 256;
     if (cus[dev] == 0)
     {
         int n = 0;
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
         cus[dev] = n;
     }
-    return 4 * cus[dev];
+    return EXL3_DECODE_WG_PER_CU * cus[dev];
 }
 
 // K slices for a launch of `wgs` workgroups over `stages` 32-wide K stages: as many as fit in one round of `target`

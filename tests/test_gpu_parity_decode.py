@@ -265,6 +265,18 @@ def test_decode_skewed_rows_span_tiles(dev):
     assert O.rel_l2(got, prefill) < 1e-3
 
 
+def test_decode_past_the_one_launch_route_prep(dev):
+    """More than 2048 routes: the decode op falls back to the three-pass sort, a separate clear and the tile table."""
+    L, cfg = layer_case("tiny", svh_scale=1 / 64)
+    TL = device_layer("tiny", svh_scale=1 / 64)
+    T = 1100                                                        # 2200 routes at top-2
+    x, ids, w = inputs(cfg, T, 13)
+    got = decode(TL, x, ids, w, dev).cpu().numpy()
+    assert O.rel_l2(got, O.expert_loop(x, ids, w, to_np_layer(L), LIMIT)) < 1e-3
+    prefill = rt.grouped_prefill(dt(x, dev), dt(ids, dev), dt(w, dev), TL, LIMIT).cpu().numpy()
+    assert O.rel_l2(got, prefill) < 1e-3
+
+
 def test_decode_dropped_ids_and_dtypes(dev):
     L, cfg = layer_case("tiny")
     TL = device_layer("tiny")
