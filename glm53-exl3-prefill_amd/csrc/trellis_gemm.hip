@@ -36,9 +36,15 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int TILE_N = 128;
 constexpr int TILE_K = 32;
-constexpr int LDS_ROW = TILE_K + 8;                 // halves per n-row of the decoded tile (80 B)
-constexpr int LDS_BLK = 16 * LDS_ROW + 64;          // halves per 16-row block: the pad puts neighbouring tiles' decode
-                                                    // stores 32 banks apart
+#ifndef EXL3_LDS_ROW_PAD
+#define EXL3_LDS_ROW_PAD 8
+#endif
+#ifndef EXL3_LDS_BLK_PAD
+#define EXL3_LDS_BLK_PAD 64
+#endif
+constexpr int LDS_ROW = TILE_K + EXL3_LDS_ROW_PAD;  // halves per n-row of the decoded tile (80 B)
+constexpr int LDS_BLK = 16 * LDS_ROW + EXL3_LDS_BLK_PAD;   // halves per 16-row block: the pad puts neighbouring
+                                                    // tiles' decode stores 32 banks apart
 constexpr int LDS_TILE = 8 * LDS_BLK;               // halves per decoded stage (128 n-rows)
 constexpr int SC_ROW = TILE_N + 4;                  // floats per staged output row of the scatter epilogue
 constexpr int LDS_MAIN_BYTES = 2 * LDS_TILE * 2;
