@@ -518,7 +518,8 @@ template <int WAVES> constexpr int lds_scatter_bytes() { return WAVES * 16 * SC_
 // WAVES = 8: 512-row tiles, one workgroup per CU; each wave decodes half as much of every stage (one chunk per lane),
 // so a decoded weight feeds twice the rows for the same VALU work per wave.
 template <int BITS, int MODE, bool DENSE, int MBN = 4, int WAVES = 4>
-__global__ __launch_bounds__(64 * WAVES, WAVES == 8 ? 1 : (MBN == 4 ? 2 : 4))
+// (HIP's second launch bound is the minimum number of waves per SIMD: 2 leaves 256 VGPRs per wave, 4 leaves 128.)
+__global__ __launch_bounds__(64 * WAVES, MBN == 4 ? 2 : 4)
 void trellis_gemm_kernel(const GemmParams p)
 {
     static_assert(WAVES == 4 || (WAVES == 8 && MBN == 4), "8-wave workgroups run 64 rows per wave");
