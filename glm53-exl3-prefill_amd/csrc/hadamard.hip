@@ -190,6 +190,7 @@ void row_had_t16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__
 }
 
 // 8 consecutive gate|up values: fp16 as stored, or fp32 partial sums rounded to fp16 first (the reference's gu is fp16).
+// idx is the element offset of the first (8-aligned) value in gu's layout.
 template <bool GU_F32>
 __device__ __forceinline__ void load_gu8(const void* gu, int64_t idx, float (&x)[8])
 {
@@ -205,7 +206,13 @@ __device__ __forceinline__ void load_gu8(const void* gu, int64_t idx, float (&x)
         unpack8(*reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(gu) + idx), x);
 }
 
-template <bool GU_F32>
+// Element offset of (r, c) in a T16 [*, W] matrix (c a multiple of 8 here).
+__device__ __forceinline__ int64_t t16_index(int64_t r, int64_t c, int64_t W)
+{
+    return (((r >> 4) * (W >> 3) + (c >> 3)) * 16 + (r & 15)) * 8 + (c & 7);
+}
+
+template <bool GU_F32, bool GU_T16 = false>
 __global__ __launch_bounds__(HAD_THREADS)
 void act_had_t16_kernel(const void* __restrict__ gu, uint16_t* __restrict__ act,
                         const int32_t* __restrict__ expert_of_row, const uint16_t* __restrict__ suh,
@@ -229,8 +236,9 @@ void act_had_t16_kernel(const void* __restrict__ gu, uint16_t* __restrict__ act,
         {
             const int c = blk * 128 + 8 * (4 * cq + i);
             float gs[8], us[8], ss[8];
-            load_gu8<GU_F32>(gu, r * (2 * (int64_t) I) + c, gs);
-            load_gu8<GU_F32>(gu, r * (2 * (int64_t) I) + I + c, us);
+            const int64_t W = 2 * (int64_t) I;
+            load_gu8<GU_F32>(gu, GU_T16 ? t16_index(r, c, W) : r * W + c, gs);
+            load_gu8<GU_F32>(gu, GU_T16 ? t16_index(r, I + c, W) : r * W + I + c, us);
             unpack8(*reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + c), ss);
             #pragma unroll
             for (int j = 0; j < 8; ++j)
@@ -347,6 +355,22 @@ extern "C" int exl3_act_had_f32(const float* gu, int64_t gu_width, uint16_t* act
     act_had_t16_kernel<true><<<t16_grid(rows, I), HAD_THREADS, 0, as_stream(stream)>>>(gu, act, expert_of_row, suh_down,
                                                                                        suh_stride, rows, I, limit);
     return hip_status("act_had_f32");
+}
+
+extern "C" int exl3_act_had_t16(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
+                                const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit,
+                                void* stream)
+{
+    EXL3_CHECK(I > 0 && gu_width == 2 * (int64_t) I && I % 128 == 0, "gate|up width must be 2I, I multiple of 128");
+    EXL3_CHECK(rows >= 0, "bad row count");
+    if (rows == 0) return EXL3_OK;
+    EXL3_CHECK(gu && act && suh_down, "null pointer");
+    EXL3_CHECK(((reinterpret_cast<uintptr_t>(gu) | reinterpret_cast<uintptr_t>(act) | reinterpret_cast<uintptr_t>(suh_down)) & 15) == 0
+               && suh_stride % 8 == 0, "gu/act/suh must be 16-byte aligned");
+    act_had_t16_kernel<false, true><<<t16_grid(rows, I), HAD_THREADS, 0, as_stream(stream)>>>(gu, act, expert_of_row,
+                                                                                              suh_down, suh_stride,
+                                                                                              rows, I, limit);
+    return hip_status("act_had_t16");
 }
 
 extern "C" int exl3_act_had(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,

@@ -95,6 +95,7 @@ struct GemmParams
     const int32_t* route_index;    // STORE_ROUTE_F32 destination row per sorted row
     void* out;
     int64_t out_ld;                // elements per output row
+    int out_t16;                   // STORE_F16: out in the T16 layout (16-row x 8-column blocks), width out_ld
 };
 
 // In-place Walsh-Hadamard transform of 32 values (Sylvester order over the index bits).
@@ -473,7 +474,10 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
             if (!row_ok) continue;
             if constexpr (MODE == MODE_STORE_F16)
             {
-                uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + orow * p.out_ld + out_col0 + col;
+                const int64_t c = out_col0 + col;              // a multiple of 4: one half of an 8-column block
+                uint16_t* o = reinterpret_cast<uint16_t*>(p.out) +
+                              (p.out_t16 ? ((((orow >> 4) * (p.out_ld >> 3) + (c >> 3)) * 16 + (orow & 15)) * 8 + (c & 7))
+                                         : orow * p.out_ld + c);
                 uint2 pk;
                 pk.x = (uint32_t) f2h(v[0]) | ((uint32_t) f2h(v[1]) << 16);
                 pk.y = (uint32_t) f2h(v[2]) | ((uint32_t) f2h(v[3]) << 16);
@@ -745,7 +749,7 @@ extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int si
 {
     EXL3_CHECK(tile_rows == 128 || tile_rows == 256 || tile_rows == 512 ||
                (tile_rows == 64 && mode != EXL3_GEMM_STORE_ROUTE_F32),
-               "tile_rows must be 128, 256 or 512 (or 64 in modes 0, 1 and 3)");
+               "tile_rows must be 128, 256 or 512 (or 64 in modes 0, 1, 3 and 4)");
     EXL3_CHECK(a_layout == EXL3_LAYOUT_ROWS || a_layout == EXL3_LAYOUT_T16, "unknown layout");
     EXL3_CHECK(bits >= 2 && bits <= 4, "unsupported bits %d (2, 3 or 4)", bits);
     EXL3_CHECK(size_k == tiles_k * 16 && size_k % 64 == 0 && size_k > 0, "K mismatch");
@@ -782,10 +786,12 @@ extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int si
     p.k_split = (total_kb + p.kb_per_split - 1) / p.kb_per_split;
     hipStream_t s = as_stream(stream);
     int rc;
-    if (mode == EXL3_GEMM_STORE_F16)
+    if (mode == EXL3_GEMM_STORE_F16 || mode == EXL3_GEMM_STORE_F16_T16)
     {
         p.out_ld = (int64_t) n_tensors * size_n_each;
-        EXL3_CHECK(out_rows >= a_rows, "mode 0: out fp16 [rows, n_tensors*N]");
+        p.out_t16 = mode == EXL3_GEMM_STORE_F16_T16;
+        EXL3_CHECK(p.out_t16 ? out_rows >= (a_rows + 15) / 16 * 16 : out_rows >= a_rows,
+                   "mode 0: out fp16 [rows, n_tensors*N] (mode 4: T16, rows rounded up to 16)");
         EXL3_CHECK((reinterpret_cast<uintptr_t>(out) & 7) == 0, "out must be 8-byte aligned");
         rc = launch_bits<MODE_STORE_F16, false>(bits, p, s);
     }
@@ -813,8 +819,8 @@ extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int si
         rc = launch_bits<MODE_ATOMIC_F32, false>(bits, p, s);
     }
     else
-        return fail("mode must be 0 (fp16 store), 1 (fp32 atomic scatter), 2 (fp32 per-route store) or 3 (fp32 atomic "
-                    "rows)");
+        return fail("mode must be 0 (fp16 store), 1 (fp32 atomic scatter), 2 (fp32 per-route store), 3 (fp32 atomic "
+                    "rows) or 4 (fp16 store, T16 layout)");
     if (rc != EXL3_OK) return rc;
     return hip_status("grouped_gemm");
 }

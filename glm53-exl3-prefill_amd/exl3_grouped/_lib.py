@@ -38,6 +38,7 @@ SIGNATURES = {
     "exl3_act_had": (I32, [P, I64, P, P, P, I64, I64, I32, F32, P]),
     "exl3_act_had_ex": (I32, [P, I64, P, P, P, I64, I64, I32, F32, I32, P]),
     "exl3_act_had_f32": (I32, [P, I64, P, P, P, I64, I64, I32, F32, P]),
+    "exl3_act_had_t16": (I32, [P, I64, P, P, P, I64, I64, I32, F32, P]),
     "exl3_grouped_gemm": (I32, [P, I64, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, P, P, I32, P, P,
                                 P, P, I64, I32, P]),
     "exl3_grouped_gemm_ex": (I32, [P, I64, I32, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, I32, P, P,

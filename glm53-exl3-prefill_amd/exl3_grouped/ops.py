@@ -203,16 +203,20 @@ def row_had(src: torch.Tensor, dst: torch.Tensor, token_sorted: Optional[torch.T
 
 
 def act_had(gu: torch.Tensor, act: torch.Tensor, expert_of_row: torch.Tensor, suh_down: torch.Tensor,
-            limit: float, dst_layout: int = 0) -> None:
+            limit: float, dst_layout: int = 0, gu_layout: int = 0, rows: Optional[int] = None) -> None:
     """kernel/exl3_grouped_prefill.cu:313-322. dst_layout (new): 0 row-major act [rows, I]; 1 T16 (rows = gu rows,
     act holds t16_rows(rows) rows). gu may be fp32 (new; the partial sums of a split-K gate|up, grouped_gemm mode 3),
-    rounded to fp16 on load, with dst_layout 1."""
+    rounded to fp16 on load, with dst_layout 1. gu_layout (new): 1 = fp16 gu in the T16 layout (grouped_gemm mode 4,
+    with dst_layout 1; `rows` gives its logical rows)."""
     I = act.shape[1]
     if dst_layout == 0:
         rows = act.shape[0]
     else:
-        rows = gu.shape[0]
+        rows = gu.shape[0] if rows is None else int(rows)
         _check(dst_layout == 1 and act.shape[0] >= t16_rows(rows), "T16 act needs t16_rows(rows) rows")
+    _check(gu_layout in (0, 1) and (gu_layout == 0 or (dst_layout == 1 and gu.dtype == torch.float16 and
+                                                       gu.size(0) >= t16_rows(rows))),
+           "a T16 gu is fp16 with t16_rows(rows) rows and writes a T16 act")
     _check(gu.size(1) == 2 * I and I % 128 == 0, "gate|up width must be 2I, I multiple of 128")
     _check(gu.dtype in (torch.float16, torch.float32) and act.dtype == torch.float16 and
            suh_down.dtype == torch.float16, "fp16 tensors (gu fp16 or fp32)")
@@ -222,7 +226,10 @@ def act_had(gu: torch.Tensor, act: torch.Tensor, expert_of_row: torch.Tensor, su
     _check(expert_of_row.dtype == torch.int32 and expert_of_row.numel() >= rows, "expert_of_row int32 [rows]")
     dev = _require_cuda(gu, act, expert_of_row, suh_down)
     with _On(dev) as s:
-        if gu.dtype == torch.float32:
+        if gu_layout == 1:
+            _lib.call("exl3_act_had_t16", _p(gu), gu.size(1), _p(act), _p(expert_of_row), _p(suh_down),
+                      suh_down.stride(0), rows, I, float(limit), s)
+        elif gu.dtype == torch.float32:
             _lib.call("exl3_act_had_f32", _p(gu), gu.size(1), _p(act), _p(expert_of_row), _p(suh_down),
                       suh_down.stride(0), rows, I, float(limit), s)
         else:
@@ -240,13 +247,14 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
     """kernel/exl3_grouped_prefill.cu:326-378. mode 0: fp16 store; mode 1: fp32 atomic scatter into
     out[token_sorted[r]]; mode 2 (new): fp32 store of the weighted row into out[route_index[r]] (out [T*topk, N]),
     summed per token by combine_routes in a fixed order; mode 3 (new): fp32 atomic add of the unweighted row into
-    out[r] (out [rows, n_tensors*N], caller-zeroed). tile_rows (new): rows per block-table entry, 128 for
+    out[r] (out [rows, n_tensors*N], caller-zeroed); mode 4 (new): mode 0 into a T16-layout out (what act_had reads
+    with gu_layout=1). tile_rows (new): rows per block-table entry, 128 for
     build_blocks' table (the reference's), 256 or 512 for a build_tiles(..., 256 | 512) table (512 runs the 8-wave
     kernel), 64 in modes 0, 1 and 3 (a thin kernel for small tiles, 16 rows per wave). a_layout (new): 0 row-major a,
     1 T16 (a from row_had / act_had with dst_layout=1; a_rows gives its logical rows). k_split (new): slices of K
     whose partial products are added into out (modes 1 and 3 only)."""
-    _check(int(tile_rows) in (128, 256, 512) or (int(tile_rows) == 64 and mode in (0, 1, 3)),
-           "tile_rows must be 128, 256 or 512 (or 64 in modes 0, 1 and 3)")
+    _check(int(tile_rows) in (128, 256, 512) or (int(tile_rows) == 64 and mode in (0, 1, 3, 4)),
+           "tile_rows must be 128, 256 or 512 (or 64 in modes 0, 1, 3 and 4)")
     _check(int(k_split) >= 1 and int(k_split) <= a.size(1) // 64, "k_split must be in [1, K / 64]")
     _check(int(k_split) == 1 or mode in (1, 3), "k_split > 1 needs mode 1 or 3")
     _check(a_layout in (0, 1), "unknown layout")
@@ -279,9 +287,10 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
     _check(block_expert.dtype == torch.int32 and block_row0.dtype == torch.int32 and counts.dtype == torch.int32
            and expert_row0.dtype == torch.int32, "int32 block table")
     max_blocks = block_expert.numel()
-    if mode == 0:
+    if mode in (0, 4):
         _check(out.dtype == torch.float16 and out.dim() == 2 and out.size(1) == n_tensors * size_n_each and
-               out.is_contiguous() and out.size(0) >= a_rows, "mode 0: out fp16 [rows, n_tensors*N]")
+               out.is_contiguous() and out.size(0) >= (a_rows if mode == 0 else t16_rows(a_rows)),
+               "mode 0: out fp16 [rows, n_tensors*N] (mode 4: T16, t16_rows(rows) rows)")
     elif mode == 1:
         _check(out.dtype == torch.float32 and out.dim() == 2 and out.size(1) == size_n_each and n_tensors == 1 and
                out.is_contiguous(), "mode 1: out fp32 [T, N], single tensor")
@@ -297,7 +306,7 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
                out.is_contiguous() and out.size(0) >= a_rows, "mode 3: out fp32 [rows, n_tensors*N]")
         _check(int(tile_rows) <= 256, "mode 3 takes row tiles of 64, 128 or 256 rows")
     else:
-        raise RuntimeError("mode must be 0, 1, 2 or 3")
+        raise RuntimeError("mode must be 0, 1, 2, 3 or 4")
     weighted = mode in (1, 2)
     dev = _require_cuda(a, packed_gate, packed_up, svh_gate, svh_up, block_expert, block_row0, counts,
                         expert_row0, out, token_sorted if mode == 1 else None, route_weight if weighted else None,

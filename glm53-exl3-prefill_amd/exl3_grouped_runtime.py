@@ -139,16 +139,17 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     h13 = torch.empty(gp.t16_rows(R), K, dtype=torch.float16, device=dev)
     gp.row_had(x16, h13, token_sorted, expert_of_row, layer.w13_suh[:, 0], True, dst_layout=1, rows=R)
     mark("row_had")
-    gu = torch.empty(R, 2 * I, dtype=torch.float16, device=dev)
+    # gu in the T16 layout too (mode 4), so act_had's loads are contiguous 16-row blocks
+    gu = torch.empty(gp.t16_rows(R), 2 * I, dtype=torch.float16, device=dev)
     w13 = (layer.w13_trellis[:, 0], layer.w13_trellis[:, 1], layer.w13_svh[:, 0], layer.w13_svh[:, 1])
-    gp.grouped_gemm(h13, *w13, block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 0,
+    gp.grouped_gemm(h13, *w13, block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 4,
                     tile_rows=tr, a_layout=1, a_rows=R)
     if thin:
-        gp.grouped_gemm(h13, *w13, thin_expert, thin_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 0,
+        gp.grouped_gemm(h13, *w13, thin_expert, thin_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 4,
                         tile_rows=THIN_ROWS, a_layout=1, a_rows=R)
     mark("gemm_gate_up")
     act = torch.empty(gp.t16_rows(R), I, dtype=torch.float16, device=dev)
-    gp.act_had(gu, act, expert_of_row, layer.w2_suh, float(limit), dst_layout=1)
+    gp.act_had(gu, act, expert_of_row, layer.w2_suh, float(limit), dst_layout=1, gu_layout=1, rows=R)
     mark("act_had")
     if scatter == "atomic":
         out = torch.zeros(T, K, dtype=torch.float32, device=dev)

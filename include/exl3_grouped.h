@@ -49,6 +49,7 @@ extern "C" {
 #define EXL3_GEMM_SCATTER_F32 1    /* grouped_gemm mode 1: fp32 atomic add into out[token_sorted[r]] * w[r] */
 #define EXL3_GEMM_STORE_ROUTE_F32 2 /* grouped_gemm mode 2: fp32 store of w[r] * y[r] into out[route_index[r]] */
 #define EXL3_GEMM_ATOMIC_F32 3      /* grouped_gemm mode 3: fp32 atomic add of y[r] into out[r] (split-K gate|up) */
+#define EXL3_GEMM_STORE_F16_T16 4   /* grouped_gemm mode 4: mode 0 with out in the T16 layout (what act_had_t16 reads) */
 
 /* Message for the calling thread's last failing call ("" if none). */
 const char* exl3_last_error(void);
@@ -103,6 +104,8 @@ int exl3_build_blocks(const int32_t* counts, int n_experts, int max_blocks,
  * reference counterpart): the grouped GEMM amortises each decoded trellis tile over up to 256 (512) rows of one
  * expert when given a 256-row (512-row) table (max_tiles >= R/tile_rows + n_experts).
  */
+int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_rows, int max_tiles,
+                     int32_t* tile_expert, int32_t* tile_row0, int32_t* meta, void* stream);
 /*
  * Two row-tile tables for one launch pair (new): tile_rows-row tiles (128, 256 or 512), except that each expert's
  * last tile goes to a second table of thin_rows-row tiles (64) when it holds at most thin_rows rows;
@@ -113,8 +116,6 @@ int exl3_build_blocks(const int32_t* counts, int n_experts, int max_blocks,
 int exl3_build_tiles_split(const int32_t* counts, int n_experts, int tile_rows, int thin_rows, int max_full,
                            int max_thin, int32_t* full_expert, int32_t* full_row0, int32_t* thin_expert,
                            int32_t* thin_row0, int32_t* meta, void* stream);
-int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_rows, int max_tiles,
-                     int32_t* tile_expert, int32_t* tile_row0, int32_t* meta, void* stream);
 
 /*
  * Input Hadamard (pybind op row_had, kernel/exl3_grouped_prefill.cu:101-115 and :296-311):
@@ -148,6 +149,10 @@ int exl3_act_had_ex(const uint16_t* gu, int64_t gu_width, uint16_t* act, const i
 /* exl3_act_had_ex(..., EXL3_LAYOUT_T16) reading gate|up as fp32 partial sums (grouped GEMM mode 3), each rounded to
  * fp16 first -- the reference's fp16 gu -- so the result is what the fp16 gu of the same sums would give. New. */
 int exl3_act_had_f32(const float* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
+                     const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, void* stream);
+/* exl3_act_had_ex(..., EXL3_LAYOUT_T16) reading gate|up in the T16 layout too (grouped GEMM mode 4): every load is a
+ * contiguous 16-row x 8-column block. Same result as the row-major input. New. */
+int exl3_act_had_t16(const uint16_t* gu, int64_t gu_width, uint16_t* act, const int32_t* expert_of_row,
                      const uint16_t* suh_down, int64_t suh_stride, int64_t rows, int I, float limit, void* stream);
 
 /*

@@ -76,7 +76,8 @@ def test_grouped_gemm_contract():
     assert "too many experts" in _gemm(E=2000)[1]
     assert "single tensor" in _gemm(pu=FAKE, su=FAKE)[1]
     assert "gate/up strides must match" in _gemm(pu=FAKE, su=None)[1]
-    assert "mode must be" in _gemm(mode=4)[1]
+    assert "mode must be" in _gemm(mode=5)[1]
+    assert "mode 4: T16" in _gemm(mode=4, a_rows=250, out_rows=250)[1]   # T16 rows round up to 256
     assert "mode 3: out fp32" in _gemm(mode=3)[1]                       # out_rows < a_rows
     assert "route_index" in _gemm(mode=2)[1]
     assert "combine" in rc_and_msg("exl3_combine_routes", FAKE, FAKE, None, 4, 8, 10, 8, 6, None)[1]

@@ -319,6 +319,9 @@ def test_act_had(dev, scale):
     act16 = torch.full((gp.t16_rows(R), I), float("nan"), dtype=torch.float16, device=dev)
     gp.act_had(t16(gu, dev), act16, t16(eor, dev), t16(suh, dev), LIMIT, dst_layout=1)
     assert np.array_equal(from_t16(act16.cpu().numpy(), R).view(np.uint16), got.view(np.uint16))
+    act_t = torch.full((gp.t16_rows(R), I), float("nan"), dtype=torch.float16, device=dev)   # gu in T16 too
+    gp.act_had(t16(to_t16(gu), dev), act_t, t16(eor, dev), t16(suh, dev), LIMIT, dst_layout=1, gu_layout=1, rows=R)
+    assert np.array_equal(from_t16(act_t.cpu().numpy(), R).view(np.uint16), got.view(np.uint16))
     # fp16 rounding of the SwiGLU output can land one step apart (fast exp vs libm exp) before the Hadamard
     assert O.rel_l2(got, ref) < 1e-3 and within_f16_steps(got, ref, steps=2, frac=0.99)
 
@@ -376,6 +379,11 @@ def test_grouped_gemm_gate_up(dev, name, T, bits, tile_rows):
                     TL.w13_svh[:, 1], be, br, t16(counts, dev), t16(row0, dev), None, None, gu16, 0, tile_rows=tile_rows,
                     a_layout=1, a_rows=R)
     assert torch.equal(gu16, gu)                                  # T16 activations: identical arithmetic
+    gut = torch.full((gp.t16_rows(R), 2 * cfg["I"]), float("nan"), dtype=torch.float16, device=dev)
+    gp.grouped_gemm(t16(to_t16(h13), dev), TL.w13_trellis[:, 0], TL.w13_trellis[:, 1], TL.w13_svh[:, 0],
+                    TL.w13_svh[:, 1], be, br, t16(counts, dev), t16(row0, dev), None, None, gut, 4, tile_rows=tile_rows,
+                    a_layout=1, a_rows=R)
+    assert np.array_equal(from_t16(gut.cpu().numpy(), R).view(np.uint16), gu.cpu().numpy().view(np.uint16))   # mode 4
 
 
 @pytest.mark.parametrize("tile_rows", [128, 256, 512])
