@@ -89,9 +89,19 @@ void sort_offsets_kernel(int32_t* __restrict__ hist, const int32_t* __restrict__
         for (int b = 0; b < n_chunks; ++b) d += bad_per_chunk[b];
         *dropped = d;
     }
+    // 8 independent loads per step: one loop-carried load per chunk would serialise n_chunks memory latencies
     int c = 0;
     if (e < n_experts)
-        for (int b = 0; b < n_chunks; ++b) c += hist[(int64_t) b * n_experts + e];
+    {
+        int part[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int b = 0;
+        for (; b + 8 <= n_chunks; b += 8)
+            #pragma unroll
+            for (int i = 0; i < 8; ++i) part[i] += hist[(int64_t) (b + i) * n_experts + e];
+        for (; b < n_chunks; ++b) part[0] += hist[(int64_t) b * n_experts + e];
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) c += part[i];
+    }
     s_scan[e] = (e < n_experts) ? c : 0;
     __syncthreads();
     // Hillis-Steele inclusive scan over 1024 entries
@@ -108,10 +118,23 @@ void sort_offsets_kernel(int32_t* __restrict__ hist, const int32_t* __restrict__
         counts[e] = c;
         expert_row0[e] = row0;
         int cur = row0;
-        for (int b = 0; b < n_chunks; ++b)
+        int b = 0;
+        for (; b + 8 <= n_chunks; b += 8)
+        {
+            int h[8];
+            #pragma unroll
+            for (int i = 0; i < 8; ++i) h[i] = hist[(int64_t) (b + i) * n_experts + e];
+            #pragma unroll
+            for (int i = 0; i < 8; ++i)
+            {
+                hist[(int64_t) (b + i) * n_experts + e] = cur;   // becomes chunk b + i's first row for expert e
+                cur += h[i];
+            }
+        }
+        for (; b < n_chunks; ++b)
         {
             const int h = hist[(int64_t) b * n_experts + e];
-            hist[(int64_t) b * n_experts + e] = cur;      // becomes chunk b's first row for expert e
+            hist[(int64_t) b * n_experts + e] = cur;
             cur += h;
         }
     }

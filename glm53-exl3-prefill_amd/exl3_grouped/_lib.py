@@ -61,7 +61,7 @@ SIGNATURES = {
                               P, I64, P, I64, F32, P, P, I64, P]),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lib = None
 _path = None
