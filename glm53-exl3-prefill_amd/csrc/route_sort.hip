@@ -55,15 +55,18 @@ void sort_hist_kernel(const void* __restrict__ ids, int ids_dtype, int64_t R, in
     __syncthreads();
     const int64_t base = (int64_t) blockIdx.x * CHUNK;
     int bad = 0;
+    int ev[ROUTES_PER_THREAD];
+    #pragma unroll
     for (int k = 0; k < ROUTES_PER_THREAD; ++k)
     {
         const int64_t i = base + k * SORT_THREADS + t;
-        if (i < R)
-        {
-            const int e = route_id(ids, ids_dtype, i, n_experts);
-            if (e >= 0) atomicAdd(&s_hist[e], 1);
-            else ++bad;
-        }
+        ev[k] = (i < R) ? route_id(ids, ids_dtype, i, n_experts) : -2;
+    }
+    #pragma unroll
+    for (int k = 0; k < ROUTES_PER_THREAD; ++k)
+    {
+        if (ev[k] >= 0) atomicAdd(&s_hist[ev[k]], 1);
+        else if (ev[k] == -1) ++bad;
     }
     __syncthreads();
     for (int e = t; e < n_experts; e += SORT_THREADS) hist[(int64_t) blockIdx.x * n_experts + e] = s_hist[e];
@@ -166,10 +169,21 @@ __device__ __forceinline__ void scatter_chunk(const void* __restrict__ ids, int 
 {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    // all of this thread's ids and weights up front: one round of memory latency instead of one per step
+    int ev[ROUTES_PER_THREAD];
+    uint16_t wv[ROUTES_PER_THREAD];
+    #pragma unroll
     for (int k = 0; k < ROUTES_PER_THREAD; ++k)
     {
         const int64_t i = base + k * SORT_THREADS + t;
-        const int e = (i < R) ? route_id(ids, ids_dtype, i, n_experts) : -1;
+        ev[k] = (i < R) ? route_id(ids, ids_dtype, i, n_experts) : -1;
+        wv[k] = (i < R) ? route_weight_f16(weights, w_dtype, i) : 0;
+    }
+    #pragma unroll
+    for (int k = 0; k < ROUTES_PER_THREAD; ++k)
+    {
+        const int64_t i = base + k * SORT_THREADS + t;
+        const int e = ev[k];
         const bool valid = e >= 0;
         const uint64_t peers = match_lanes(valid ? e : 0, valid);
         const int rank = __popcll(peers & below);
@@ -181,7 +195,7 @@ __device__ __forceinline__ void scatter_chunk(const void* __restrict__ ids, int 
             int row = s_cursor[e] + rank;
             for (int w = 0; w < wave; ++w) row += s_wave_cnt[w][e];
             token_sorted[row] = i / topk;
-            weight_sorted[row] = route_weight_f16(weights, w_dtype, i);
+            weight_sorted[row] = wv[k];
             expert_of_row[row] = e;
             if (route_index) route_index[row] = (int32_t) i;
         }
@@ -250,12 +264,16 @@ void route_prep_small_kernel(const void* __restrict__ ids, int ids_dtype, const 
         for (int w = 0; w < SORT_WAVES; ++w) s_wave_cnt[w][e] = 0;
     }
     __syncthreads();
+    int ev[ROUTES_PER_THREAD];
+    #pragma unroll
     for (int k = 0; k < ROUTES_PER_THREAD; ++k)
     {
         const int64_t i = (int64_t) k * SORT_THREADS + t;
-        const int e = (i < R) ? route_id(ids, ids_dtype, i, n_experts) : -1;
-        if (e >= 0) atomicAdd(&s_cursor[e], 1);
+        ev[k] = (i < R) ? route_id(ids, ids_dtype, i, n_experts) : -1;
     }
+    #pragma unroll
+    for (int k = 0; k < ROUTES_PER_THREAD; ++k)
+        if (ev[k] >= 0) atomicAdd(&s_cursor[ev[k]], 1);
     __syncthreads();
     int c[4], nbk[4], my_rows = 0, my_tiles = 0;
     #pragma unroll
