@@ -129,10 +129,10 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
         # each expert's last tile of <= 64 rows goes to a second table, run by the thin kernel
         thin_expert = torch.empty(min(E, R), dtype=torch.int32, device=dev)
         thin_row0 = torch.empty_like(thin_expert)
-        meta = torch.zeros(3, dtype=torch.int32, device=dev)
+        meta = torch.empty(3, dtype=torch.int32, device=dev)              # written whole by the kernel
         gp.build_tiles_split(counts, block_expert, block_row0, thin_expert, thin_row0, meta, tr, THIN_ROWS)
     else:
-        meta = torch.zeros(2, dtype=torch.int32, device=dev)
+        meta = torch.empty(2, dtype=torch.int32, device=dev)
         gp.build_tiles(counts, block_expert, block_row0, meta, tr)
     mark("build_blocks")
     # the GEMMs' activation operands (h13, act) are written in the T16 layout, which makes their loads contiguous
