@@ -119,30 +119,33 @@ void act_had_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ act,
 }
 
 // ---- T16-layout passes. A wave owns one 16-row group x one 128-column block: lane l holds row l & 15 and the 8-column
-// chunks 4 (l >> 4) + i (i = 0..3), so for each i the wave stores whole 256-byte T16 chunks (16 rows x 8 columns)
-// side by side: 1 KB contiguous per store. Column bits 0-2 and 3-4 of the block are in the lane's registers
-// (5 butterfly stages), bits 5 and 6 across lanes l ^ 16 and l ^ 32.
-__device__ __forceinline__ void fwht32_regs(float (&x)[32])
+// chunks 4 i + (l >> 4) (i = 0..3). For each i the four lanes of a row then read 64 contiguous bytes of it, and the
+// wave stores four whole, adjacent 256-byte T16 chunks (16 rows x 8 columns): 1 KB contiguous per store. Column bits
+// 0-2 and 5-6 of the block are in the lane's registers (x[8 i + j]: 5 butterfly stages), bits 3 and 4 across lanes
+// l ^ 16 and l ^ 32.
+// Butterfly stages len, 2 len, ... < end over the lane's 32 registers.
+template <int LEN0, int END>
+__device__ __forceinline__ void fwht_regs(float (&x)[32])
 {
     #pragma unroll
-    for (int len = 1; len < 32; len <<= 1)
+    for (int len = LEN0; len < END; len <<= 1)
         #pragma unroll
         for (int i = 0; i < 32; ++i)
             if (!(i & len)) { const float a = x[i], b = x[i + len]; x[i] = a + b; x[i + len] = a - b; }
 }
 
+// Stages in column-bit order 0..6 (bits 0-2: registers 1, 2, 4; bits 3-4: lanes 16, 32; bits 5-6: registers 8, 16),
+// the order of the row-major pass, so both layouts round identically.
 __device__ __forceinline__ void had128_t16(float (&x)[32], int lane)
 {
-    fwht32_regs(x);
+    fwht_regs<1, 8>(x);
     #pragma unroll
     for (int i = 0; i < 32; i += 2) pair_butterfly16(x[i], x[i + 1]);
     #pragma unroll
-    for (int i = 0; i < 32; i += 2)
-    {
-        pair_butterfly32(x[i], x[i + 1]);
-        x[i] *= HAD_SCALE;
-        x[i + 1] *= HAD_SCALE;
-    }
+    for (int i = 0; i < 32; i += 2) pair_butterfly32(x[i], x[i + 1]);
+    fwht_regs<8, 32>(x);
+    #pragma unroll
+    for (int i = 0; i < 32; ++i) x[i] *= HAD_SCALE;
 }
 
 template <bool GATHER>
@@ -168,7 +171,7 @@ void row_had_t16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__
         #pragma unroll
         for (int i = 0; i < 4; ++i)
         {
-            const int c = blk * 128 + 8 * (4 * cq + i);
+            const int c = blk * 128 + 8 * (4 * i + cq);
             float xs[8], ss[8];
             unpack8(*reinterpret_cast<const uint4*>(src + srow * K + c), xs);
             unpack8(*reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + c), ss);
@@ -183,7 +186,7 @@ void row_had_t16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__
                 float o[8];
                 #pragma unroll
                 for (int j = 0; j < 8; ++j) o[j] = x[8 * i + j];
-                const int64_t chunk = g * (K / 8) + blk * 16 + 4 * cq + i;
+                const int64_t chunk = g * (K / 8) + blk * 16 + 4 * i + cq;
                 *reinterpret_cast<uint4*>(dst + chunk * 128 + rl * 8) = pack8(o);
             }
     }
@@ -234,7 +237,7 @@ void act_had_t16_kernel(const void* __restrict__ gu, uint16_t* __restrict__ act,
         #pragma unroll
         for (int i = 0; i < 4; ++i)
         {
-            const int c = blk * 128 + 8 * (4 * cq + i);
+            const int c = blk * 128 + 8 * (4 * i + cq);
             float gs[8], us[8], ss[8];
             const int64_t W = 2 * (int64_t) I;
             load_gu8<GU_F32>(gu, GU_T16 ? t16_index(r, c, W) : r * W + c, gs);
@@ -257,7 +260,7 @@ void act_had_t16_kernel(const void* __restrict__ gu, uint16_t* __restrict__ act,
                 float o[8];
                 #pragma unroll
                 for (int j = 0; j < 8; ++j) o[j] = x[8 * i + j];
-                const int64_t chunk = g * (I / 8) + blk * 16 + 4 * cq + i;
+                const int64_t chunk = g * (I / 8) + blk * 16 + 4 * i + cq;
                 *reinterpret_cast<uint4*>(act + chunk * 128 + rl * 8) = pack8(o);
             }
     }
