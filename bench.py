@@ -30,8 +30,8 @@ MFMA_F16_PEAK_TFLOPS = 2500.0      # MI355X dense fp16 (no sparsity)
 HBM_PEAK_GBS = 8000.0
 # the dominant stage's kernels as rocprofv3 reports them (keys of the committed traffic summary): the gate|up GEMM
 # runs full expert tiles on the main kernel and each expert's last tile of <= 64 rows on the thin one
-GATE_UP_KERNELS = ("trellis_gemm_kernel<{bits}, 0, false, 4>(GemmParams)",
-                   "trellis_gemm_kernel<{bits}, 0, false, 1>(GemmParams)")
+GATE_UP_KERNELS = ("trellis_gemm_kernel<{bits}, 0, false, 4, 4>(GemmParams)",
+                   "trellis_gemm_kernel<{bits}, 0, false, 1, 4>(GemmParams)")
 
 
 def parse():
