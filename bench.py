@@ -164,9 +164,31 @@ def run(args, T=None, emit=True):
                      "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": traffic_from_profiles(cfg_name, gate_up_kernels),
-                     "work_per_launch": f"4*R*H*I = {gate_up_flop:.4g} flop (R={R} routed rows) per stage call"},
+                     "work_per_launch": f"4*R*H*I = {gate_up_flop:.4g} flop (R={R} routed rows) per stage call",
+                     "peak_source": "MI355X dense fp16 MFMA, AMD datasheet (256 CUs x 2.4 GHz x 4096 flop/clk)"},
+        "device": device_info(),
     }
     return result, (L, x, ids, w, cfg)
+
+
+def device_info():
+    """Name, CU count and peak engine clock of cuda:0. The clock comes from hipDeviceGetAttribute in the HIP runtime
+    the extension already loaded (dlopen by soname returns that copy); None if the query fails."""
+    import ctypes
+
+    import torch
+
+    props = torch.cuda.get_device_properties(0)
+    clock_mhz = None
+    try:
+        hip = ctypes.CDLL("libamdhip64.so.7")
+        v = ctypes.c_int(0)
+        if hip.hipDeviceGetAttribute(ctypes.byref(v), 5, 0) == 0:          # hipDeviceAttributeClockRate, kHz
+            clock_mhz = round(v.value / 1e3)
+    except OSError:
+        pass
+    return {"name": props.name, "arch": getattr(props, "gcnArchName", None), "cus": props.multi_processor_count,
+            "peak_clock_mhz": clock_mhz}
 
 
 def cpu_baseline(inputs, seconds: float):
