@@ -15,6 +15,7 @@
 //   * Everything lives in one caller-provided workspace; buffers that accumulate are cleared by a fill kernel (no
 //     memset nodes), and nothing is read back to the host, so a caller may capture the call in a HIP graph.
 #include <algorithm>
+#include <atomic>
 
 #include "exl3_common.h"
 
@@ -74,19 +75,20 @@ DecodeLayout decode_layout(int64_t tokens, int topk, int n_experts, int hidden, 
 #define EXL3_DECODE_WG_PER_CU 4
 #endif
 
-// Workgroups a launch should put on the device: four resident thin-kernel workgroups per CU.
+// Workgroups a launch should put on the device: four resident thin-kernel workgroups per CU. The CU count is cached per
+// device; threads that race on the first query store the same value.
 int target_workgroups(hipStream_t)
 {
-    static int cus[64] = {};
+    static std::atomic<int> cus[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return EXL3_DECODE_WG_PER_CU * 256;
-    if (cus[dev] == 0)
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0)
     {
-        int n = 0;
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev] = n;
+        cus[dev].store(n, std::memory_order_relaxed);
     }
-    return EXL3_DECODE_WG_PER_CU * cus[dev];
+    return EXL3_DECODE_WG_PER_CU * n;
 }
 
 // K slices for a launch of `wgs` workgroups over `stages` 32-wide K stages: as many as fit in one round of `target`
