@@ -310,6 +310,8 @@ def main():
         return
     if args.sweep:
         for T in (1024, 2048, 4096, 8192):
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()        # each size starts from a fresh allocator pool, as in its own process
             r, _ = run(args, T=T, emit=False)
             r.pop("cpu_baseline", None)
             print(json.dumps(r), flush=True)
