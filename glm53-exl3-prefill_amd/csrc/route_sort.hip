@@ -209,9 +209,27 @@ __device__ __forceinline__ void scatter_chunk(const void* __restrict__ ids, int 
     }
 }
 
+// Rows past sum(counts) (only present when routes were dropped): token 0, weight 0, expert 0, route 0. Disjoint from
+// the rows the scatter writes, so every workgroup of the scatter launch takes a grid-strided share.
+__device__ __forceinline__ void fill_tail(const int32_t* __restrict__ counts, const int32_t* __restrict__ expert_row0,
+                                          int n_experts, int64_t R, int64_t* __restrict__ token_sorted,
+                                          uint16_t* __restrict__ weight_sorted, int32_t* __restrict__ expert_of_row,
+                                          int32_t* __restrict__ route_index)
+{
+    const int64_t n_rows = (int64_t) expert_row0[n_experts - 1] + counts[n_experts - 1];
+    for (int64_t r = n_rows + (int64_t) blockIdx.x * blockDim.x + threadIdx.x; r < R; r += (int64_t) gridDim.x * blockDim.x)
+    {
+        token_sorted[r] = 0;
+        weight_sorted[r] = 0;
+        expert_of_row[r] = 0;
+        if (route_index) route_index[r] = 0;
+    }
+}
+
 __global__ __launch_bounds__(SORT_THREADS)
 void sort_scatter_kernel(const void* __restrict__ ids, int ids_dtype, const void* __restrict__ weights, int w_dtype,
                          int64_t R, int topk, int n_experts, const int32_t* __restrict__ cursor0,
+                         const int32_t* __restrict__ counts, const int32_t* __restrict__ expert_row0,
                          int64_t* __restrict__ token_sorted, uint16_t* __restrict__ weight_sorted,
                          int32_t* __restrict__ expert_of_row, int32_t* __restrict__ route_index)
 {
@@ -226,11 +244,12 @@ void sort_scatter_kernel(const void* __restrict__ ids, int ids_dtype, const void
     __syncthreads();
     scatter_chunk(ids, ids_dtype, weights, w_dtype, R, topk, n_experts, (int64_t) blockIdx.x * CHUNK, s_cursor,
                   s_wave_cnt, token_sorted, weight_sorted, expert_of_row, route_index);
+    fill_tail(counts, expert_row0, n_experts, R, token_sorted, weight_sorted, expert_of_row, route_index);
 }
 
 // The decode path's route preparation in one launch, for R <= CHUNK routes. Workgroup 0 sorts: expert histogram in
 // LDS, exclusive scans of rows and tiles over the experts (thread t owns experts 4t .. 4t + 3), counts / expert_row0,
-// the tile table of build_blocks_kernel, the tail rows of sort_fill_tail_kernel, then the stable scatter of
+// the tile table of build_blocks_kernel, the tail rows of fill_tail, then the stable scatter of
 // sort_scatter_kernel from the scanned cursors -- the same rows the three-pass sort writes. Workgroups 1.. clear two
 // fp32 buffers (float4 counts na, nb).
 __global__ __launch_bounds__(SORT_THREADS)
@@ -324,22 +343,6 @@ void route_prep_small_kernel(const void* __restrict__ ids, int ids_dtype, const 
     __syncthreads();
     scatter_chunk(ids, ids_dtype, weights, w_dtype, R, topk, n_experts, 0, s_cursor, s_wave_cnt, token_sorted,
                   weight_sorted, expert_of_row, nullptr);
-}
-
-// Rows past sum(counts) (only present when routes were dropped): token 0, weight 0, expert 0, route 0.
-__global__ void sort_fill_tail_kernel(const int32_t* __restrict__ counts, const int32_t* __restrict__ expert_row0,
-                                      int n_experts, int64_t R, int64_t* __restrict__ token_sorted,
-                                      uint16_t* __restrict__ weight_sorted, int32_t* __restrict__ expert_of_row,
-                                      int32_t* __restrict__ route_index)
-{
-    const int64_t n_rows = (int64_t) expert_row0[n_experts - 1] + counts[n_experts - 1];
-    for (int64_t r = n_rows + (int64_t) blockIdx.x * blockDim.x + threadIdx.x; r < R; r += (int64_t) gridDim.x * blockDim.x)
-    {
-        token_sorted[r] = 0;
-        weight_sorted[r] = 0;
-        expert_of_row[r] = 0;
-        if (route_index) route_index[r] = 0;
-    }
 }
 
 // Per-expert row tiles of `tile_rows` rows (128 for the reference's block table).
@@ -542,10 +545,8 @@ extern "C" int exl3_sort_routes(const void* topk_ids, int ids_dtype, const void*
     if (n_chunks > 0)
     {
         sort_scatter_kernel<<<n_chunks, SORT_THREADS, 0, s>>>(topk_ids, ids_dtype, topk_weights, weights_dtype, R, topk,
-                                                              n_experts, hist, token_sorted, weight_sorted, expert_of_row,
-                                                              route_index);
-        sort_fill_tail_kernel<<<64, 256, 0, s>>>(counts, expert_row0, n_experts, R, token_sorted, weight_sorted,
-                                                 expert_of_row, route_index);
+                                                              n_experts, hist, counts, expert_row0, token_sorted,
+                                                              weight_sorted, expert_of_row, route_index);
     }
     return hip_status("sort_routes");
 }
