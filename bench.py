@@ -27,6 +27,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [os.path.join(ROOT, "glm53-exl3-prefill_amd")]
 
 MFMA_F16_PEAK_TFLOPS = 2500.0      # MI355X dense fp16 (no sparsity)
+# The reference's published per-layer ms of its grouped path on GB10 at the `repro` shape (288 experts, H=4096,
+# I=1024 per rank, routing_skewed(hot=12, share=0.55), real checkpoint layer 3): reference README.md:41-44.
+REFERENCE_GB10_MS = {1024: 11.4, 2048: 13.7, 4096: 20.2, 8192: 33.2}
 HBM_PEAK_GBS = 8000.0
 # the dominant stage's kernels as rocprofv3 reports them (keys of the committed traffic summary): the gate|up GEMM
 # runs full expert tiles on the main kernel and each expert's last tile of <= 64 rows on the thin one
@@ -150,7 +153,8 @@ def run(args, T=None, emit=True):
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": None,
+        "vs_baseline": (round(REFERENCE_GB10_MS[T_] / ms_per_step, 2)
+                        if cfg_name == "repro" and T_ in REFERENCE_GB10_MS else None),
         "dtype": "f16",
         "data": "synthetic (seeded random trellis codes, signs, scales, N(0,1) activations, Zipf-skewed router)",
         "config": {"workload": workload, "experts": E, "hidden": H, "intermediate": I, "bits": bits,

@@ -25,6 +25,9 @@ CONFIGS = {
     "headline": dict(E=288, H=4096, I=768, bits=4, T=8192, topk=8, routing="zipf", zipf_s=1.1),
     # thin-expert stress at 4 bpw (repeated at 3 and 2 bpw)
     "thin": dict(E=288, H=4096, I=768, bits=4, T=7168, topk=8, routing="thin"),
+    # the shape of the reference's own published grouped-path numbers (README.md:41-44: I = 1024 per rank,
+    # routing_skewed(hot=12, share=0.55), T = 1K / 2K / 4K / 8K), with synthetic codes in place of the checkpoint
+    "repro": dict(E=288, H=4096, I=1024, bits=4, T=8192, topk=8, routing="skewed"),
 }
 
 

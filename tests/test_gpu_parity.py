@@ -553,6 +553,15 @@ def test_headline_sampled_tokens_and_properties(dev, scatter):
     assert (outp - out[torch.from_numpy(perm).to(dev)]).norm().item() <= 1e-6 * out.norm().item()
 
 
+def test_repro_config_sampled_tokens(dev):
+    """The reference's published shape (I = 1024 per rank, skewed routing) at 1024 tokens, sampled tokens against
+    the expert loop."""
+    L, x, ids, w, cfg = synth.make_config("repro", seed=0, T=1024)
+    out = run_layer(L, x, ids, w, dev).cpu().numpy()
+    tokens = np.random.default_rng(7).choice(cfg["T"], 16, replace=False)
+    assert O.rel_l2(out[tokens], sampled_loop(L, x, ids, w, tokens)) < 1e-3
+
+
 @pytest.mark.parametrize("bits", [4, 3, 2])
 def test_thin_config_all_bits(dev, bits):
     L, x, ids, w, cfg = synth.make_config("thin", seed=0, bits=bits)
