@@ -106,3 +106,7 @@ def test_zipf_and_thin_skews():
     cs = np.sort(c)[::-1]
     assert 0.5 < cs[:16].sum() / c.sum() < 0.65          # 16 hot experts take ~60%
     assert 180 <= int((c <= 16).sum()) <= 220            # ~200 experts with <= 16 rows
+    ids, _ = synth.routing_skewed(8192, 288, 8, 0)         # the reference's routing_skewed(hot=12, share=0.55)
+    c = np.bincount(ids.ravel(), minlength=288)
+    assert 0.48 < c[:12].sum() / c.sum() < 0.56            # 55% of draws go to the 12 hot experts, fewer slots after
+    assert c[:12].min() > 10 * c[12:].max()                # duplicates within a token are redrawn
