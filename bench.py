@@ -15,6 +15,9 @@ launch stream); cpu_baseline = the CPU oracle's expert loop on a bounded sample.
   python bench.py --sweep          (extra lines for T = 1024, 2048, 4096, 8192; not the driver's contract line)
   python bench.py --decode         (the decode path, moe_decode, at small batches of the same layer: one line per
                                     batch, eager and graph-replayed; not the driver's contract line)
+  python bench.py --fat            (the per-expert fat GEMM per call: config 2 and the reference's published shapes)
+  python bench.py --config repro --tokens T   (the reference's published grouped-path shape; vs_baseline = its GB10
+                                    per-layer ms / this run's)
 """
 import argparse
 import json
@@ -50,6 +53,8 @@ def parse():
     ap.add_argument("--cpu-sample-seconds", type=float, default=20.0)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--decode", action="store_true", help="time the decode path (moe_decode) at small batches")
+    ap.add_argument("--fat", action="store_true", help="time the per-expert fat GEMM (config 2 and the reference's "
+                    "published per-call shapes)")
     ap.add_argument("--decode-tokens", default="1,4,16,32,64,128")
     ap.add_argument("--decode-no-compare", action="store_true",
                     help="with --decode: skip the prefill-path comparison (clean kernel traces of the decode path)")
@@ -233,6 +238,52 @@ def cpu_baseline(inputs, seconds: float):
             "ms_per_layer_extrapolated": round(total / rows * counts.sum() * 1e3, 1)}
 
 
+# The reference's published per-call ms of its per-expert fat GEMM on GB10 (variant K64/2-stage): gate|up
+# M x 4096 x 2048 and down M x 1024 x 4096 (reference docs/BASELINE.md:105-106).
+REFERENCE_FAT_GB10_MS = {128: (0.093, 0.032), 256: (0.093, 0.050), 512: (0.159, 0.075), 1024: (0.239, 0.146),
+                         2048: (0.457, 0.272)}
+
+
+def fat_bench(args):
+    """Per-call time of fat_gemm_v2 (fp32 store) with HIP events: config 2 (M=4096, K=4096, N=1536), then the shapes
+    the reference published per-call times for. One JSON line per shape."""
+    import torch
+
+    import exl3_grouped as gp
+    from exl3_grouped import synth
+
+    dev = torch.device("cuda:0")
+
+    def timed(M, K, N, variant=1):
+        a, packed, svh = synth.make_fat(0, M=M, K=K, N=N)
+        at, pt, st = (torch.from_numpy(v).to(dev) for v in (a, packed, svh))
+        out = torch.empty(M, N, dtype=torch.float32, device=dev)
+        for _ in range(args.warmup):
+            gp.fat_gemm_v2(at, pt, out, st, 4, True, False, variant)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = max(args.steps, 10)
+        e0.record()
+        for _ in range(n):
+            gp.fat_gemm_v2(at, pt, out, st, 4, True, False, variant)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    def line(name, M, K, N, ref_ms=None):
+        ms = timed(M, K, N)
+        tflops = 2.0 * M * K * N / (ms * 1e-3) / 1e12
+        print(json.dumps({"metric": "fat GEMM ms per call", "shape": name, "M": M, "K": K, "N": N, "bits": 4,
+                          "ms": round(ms, 4), "tflops": round(tflops, 1),
+                          "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                          "reference_gb10_ms": ref_ms,
+                          "vs_reference": round(ref_ms / ms, 2) if ref_ms else None}), flush=True)
+
+    line("config 2 (gate|up of one expert, N = 2 x 768)", 4096, 4096, 1536)
+    for M, (gu_ms, dn_ms) in REFERENCE_FAT_GB10_MS.items():
+        line("gate|up, I = 1024", M, 4096, 2048, gu_ms)
+        line("down, I = 1024", M, 1024, 4096, dn_ms)
+
+
 def decode_bench(args):
     """moe_decode on the config-3 layer (E=288, H=4096, I=768) at small batches with softmax top-8 routing: HIP-event
     time per call, eager and replayed from a captured graph, beside the prefill path at the same batch. Its bound is
@@ -311,6 +362,9 @@ def main():
         return
     if args.decode:
         decode_bench(args)
+        return
+    if args.fat:
+        fat_bench(args)
         return
     if args.sweep:
         for T in (1024, 2048, 4096, 8192):

@@ -26,6 +26,8 @@
 #include "exl3_common.h"
 #include "trellis_decode.h"
 
+#include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 namespace exl3 {
@@ -879,6 +881,53 @@ int fat_common(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed,
 // Single-expert row tiles: 512 rows (8-wave kernel) unless the matrix is thin enough for one 256-row tile.
 int dense_tile_rows(int64_t m) { return m > 256 ? 512 : 256; }
 
+__global__ __launch_bounds__(256)
+void zero_f32x4_kernel(float4* __restrict__ p, int64_t n4)
+{
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t) gridDim.x * 256) p[i] = z;
+}
+
+int device_cus()
+{
+    static std::atomic<int> cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0)
+    {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// A single-expert fp32 GEMM with a long K whose 256-row tiles would give at most one workgroup per CU (two fit) runs
+// as two K slices on 256-row tiles instead: the output is zeroed and each slice adds its H128-transformed partial
+// product with fp32 atomics. Two additions onto zero commute exactly, so the result is still the same on every run.
+// With K < 2048 the zero fill and the second epilogue cost more than the slices gain (measured at K = 1024).
+bool dense_split_pays(int64_t m, int n_slots, int size_k)
+{
+    return (m + 255) / 256 * n_slots <= device_cus() && size_k >= 2048;
+}
+
+template <int MODE>
+int launch_dense_split2(GemmParams p, int bits, float* out, int64_t out_floats, hipStream_t s)
+{
+    const int total_kb = p.size_k / TILE_K;
+    p.tile_rows = 256;
+    p.n_groups = (int) ((p.m + 255) / 256);
+    p.kb_per_split = ((total_kb + 1) / 2 + 1) / 2 * 2;        // even: both slices have an even number of stages
+    p.k_split = (total_kb + p.kb_per_split - 1) / p.kb_per_split;
+    const int64_t n4 = out_floats / 4;
+    if (n4 > 0)
+    {
+        const int64_t zgrid = std::min<int64_t>((n4 + 255) / 256, 4096);
+        zero_f32x4_kernel<<<(unsigned) zgrid, 256, 0, s>>>(reinterpret_cast<float4*>(out), n4);
+    }
+    return launch_bits<MODE, true>(bits, p, s);
+}
+
 }  // namespace
 
 extern "C" int exl3_fat_gemm(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed, int tiles_k, int tiles_n,
@@ -893,7 +942,9 @@ extern "C" int exl3_fat_gemm(const uint16_t* a, int64_t m, int size_k, const uin
     p.svh0 = svh; p.tile_rows = dense_tile_rows(m); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
     p.n_tiles_each = (int) (svh_len / TILE_N);
     p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = svh_len;
-    rc = launch_bits<MODE_STORE_F32, true>(bits, p, as_stream(stream));
+    rc = dense_split_pays(m, p.n_slots, size_k)
+             ? launch_dense_split2<MODE_ATOMIC_F32>(p, bits, out, m * svh_len, as_stream(stream))
+             : launch_bits<MODE_STORE_F32, true>(bits, p, as_stream(stream));
     if (rc) return rc;
     return hip_status("fat_gemm_v2");
 }
@@ -946,8 +997,11 @@ extern "C" int exl3_linear(const uint16_t* x, int64_t m, int k, const uint16_t* 
     p.a = work; p.a_rows = m; p.a_t16 = 1; p.size_k = k; p.packed0 = packed; p.tiles_n = tiles_n;
     p.svh0 = svh; p.tile_rows = dense_tile_rows(m); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
     p.n_tiles_each = n / TILE_N; p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = n;
-    rc = out_dtype == EXL3_DTYPE_F32 ? launch_bits<MODE_STORE_F32, true>(bits, p, s)
-                                     : launch_bits<MODE_STORE_F16, true>(bits, p, s);
+    if (out_dtype == EXL3_DTYPE_F32 && dense_split_pays(m, p.n_slots, k))
+        rc = launch_dense_split2<MODE_ATOMIC_F32>(p, bits, reinterpret_cast<float*>(out), m * n, s);
+    else
+        rc = out_dtype == EXL3_DTYPE_F32 ? launch_bits<MODE_STORE_F32, true>(bits, p, s)
+                                         : launch_bits<MODE_STORE_F16, true>(bits, p, s);
     if (rc) return rc;
     return hip_status("linear");
 }
