@@ -699,7 +699,7 @@ int launch_gemm(const GemmParams& p, hipStream_t s)
     const int64_t grid = (int64_t) groups8 * p.n_slots * (p.k_split > 1 ? p.k_split : 1);
     if (grid == 0) return EXL3_OK;
     if (grid > 0x7FFFFFFF) return fail("grid too large");
-    if constexpr (MODE != MODE_STORE_ROUTE_F32 && !DENSE)
+    if constexpr (MODE != MODE_STORE_ROUTE_F32)
     {
         if (p.tile_rows == 64)
         {
@@ -878,8 +878,16 @@ int fat_common(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed,
     return EXL3_OK;
 }
 
-// Single-expert row tiles: 512 rows (8-wave kernel) unless the matrix is thin enough for one 256-row tile.
-int dense_tile_rows(int64_t m) { return m > 256 ? 512 : 256; }
+// Single-expert row tiles. A single expert's matrix is short next to the device: 256-row tiles of a 2048 x 4096 x 4096
+// GEMM are 256 workgroups for 256 CUs. 64-row tiles on the thin kernel (four workgroups per CU) decode each weight
+// once per 64 rows instead of 256 but spread the work over four times the workgroups, which wins up to 256 rows, and
+// up to 2048 rows when K is short (K < 2048: fewer stages to decode per tile). Larger matrices take 512-row tiles on
+// the 8-wave kernel. Measured per call (gate|up M x 4096 x 2048, down M x 1024 x 4096, M = 128 .. 2048).
+int dense_tile_rows(int64_t m, int size_k)
+{
+    if (m <= 256 || (m <= 2048 && size_k < 2048)) return 64;
+    return 512;
+}
 
 __global__ __launch_bounds__(256)
 void zero_f32x4_kernel(float4* __restrict__ p, int64_t n4)
@@ -903,9 +911,10 @@ int device_cus()
 }
 
 // A single-expert fp32 GEMM with a long K whose 256-row tiles would give at most one workgroup per CU (two fit) runs
-// as two K slices on 256-row tiles instead: the output is zeroed and each slice adds its H128-transformed partial
-// product with fp32 atomics. Two additions onto zero commute exactly, so the result is still the same on every run.
-// With K < 2048 the zero fill and the second epilogue cost more than the slices gain (measured at K = 1024).
+// as two K slices (on 64-row tiles up to 1024 rows, 256-row tiles above) instead: the output is zeroed and each slice
+// adds its H128-transformed partial product with fp32 atomics. Two additions onto zero commute exactly, so the result
+// is still the same on every run. With K < 2048 the zero fill and the second epilogue cost more than the slices gain
+// (measured at K = 1024).
 bool dense_split_pays(int64_t m, int n_slots, int size_k)
 {
     return (m + 255) / 256 * n_slots <= device_cus() && size_k >= 2048;
@@ -915,8 +924,8 @@ template <int MODE>
 int launch_dense_split2(GemmParams p, int bits, float* out, int64_t out_floats, hipStream_t s)
 {
     const int total_kb = p.size_k / TILE_K;
-    p.tile_rows = 256;
-    p.n_groups = (int) ((p.m + 255) / 256);
+    p.tile_rows = p.m <= 1024 ? 64 : 256;                       // thin tiles here too, up to 1024 rows (measured)
+    p.n_groups = (int) ((p.m + p.tile_rows - 1) / p.tile_rows);
     p.kb_per_split = ((total_kb + 1) / 2 + 1) / 2 * 2;        // even: both slices have an even number of stages
     p.k_split = (total_kb + p.kb_per_split - 1) / p.kb_per_split;
     const int64_t n4 = out_floats / 4;
@@ -939,7 +948,7 @@ extern "C" int exl3_fat_gemm(const uint16_t* a, int64_t m, int size_k, const uin
     EXL3_CHECK(out_rows == m, "out shape must be [M, N]");
     GemmParams p{};
     p.a = a; p.a_rows = m; p.size_k = size_k; p.packed0 = packed; p.tiles_n = tiles_n;
-    p.svh0 = svh; p.tile_rows = dense_tile_rows(m); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
+    p.svh0 = svh; p.tile_rows = dense_tile_rows(m, size_k); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
     p.n_tiles_each = (int) (svh_len / TILE_N);
     p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = svh_len;
     rc = dense_split_pays(m, p.n_slots, size_k)
@@ -960,7 +969,7 @@ extern "C" int exl3_fat_gemm_scatter(const uint16_t* a, int64_t m, int size_k, c
     EXL3_CHECK(out_rows >= 0, "bad out rows");
     GemmParams p{};
     p.a = a; p.a_rows = m; p.size_k = size_k; p.packed0 = packed; p.tiles_n = tiles_n;
-    p.svh0 = svh; p.tile_rows = dense_tile_rows(m); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
+    p.svh0 = svh; p.tile_rows = dense_tile_rows(m, size_k); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
     p.n_tiles_each = (int) (svh_len / TILE_N);
     p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = svh_len;
     p.token = token_idx; p.route_weight = route_weight;
@@ -995,7 +1004,7 @@ extern "C" int exl3_linear(const uint16_t* x, int64_t m, int k, const uint16_t* 
     const int n = tiles_n * 16;
     GemmParams p{};
     p.a = work; p.a_rows = m; p.a_t16 = 1; p.size_k = k; p.packed0 = packed; p.tiles_n = tiles_n;
-    p.svh0 = svh; p.tile_rows = dense_tile_rows(m); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
+    p.svh0 = svh; p.tile_rows = dense_tile_rows(m, k); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
     p.n_tiles_each = n / TILE_N; p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = n;
     if (out_dtype == EXL3_DTYPE_F32 && dense_split_pays(m, p.n_slots, k))
         rc = launch_dense_split2<MODE_ATOMIC_F32>(p, bits, reinterpret_cast<float*>(out), m * n, s);
