@@ -236,6 +236,9 @@ int exl3_combine_routes(const float* partial, float* out, const void* topk_ids, 
  * bits must be 2, 3 or 4 with mcg != 0 and mul1 == 0 (the reference accepts only bits 4: "only K4 MCG tensors");
  * size_k % 64 == 0, n % 128 == 0. variant in [0, 3] selects a tile schedule (the reference's four
  * smem/pipeline variants); exl3_smem_bytes(variant) returns its LDS bytes per workgroup, or -1 if unknown.
+ * Every variant gives bit-identical results. A store with size_k >= 2048 that would leave CUs idle first zeroes out and
+ * then adds two K halves into it with fp32 atomics (exact: two additions onto zero commute), so out must not overlap
+ * a, packed or svh.
  */
 int exl3_fat_gemm(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed, int tiles_k, int tiles_n,
                   int packed_words, float* out, int64_t out_rows, const uint16_t* svh, int64_t svh_len,
