@@ -80,6 +80,18 @@ void row_had_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst
     }
 }
 
+// silu(g) * u in fp32 with the hardware exp and reciprocal: the reference builds with --use_fast_math, so its
+// g / (1 + __expf(-g)) is an approximate division too (kernel/exl3_grouped_prefill.cu:135); the result is rounded to
+// fp16 next. An IEEE division here cost ~10 VALU per value in a VALU-heavy pass.
+__device__ __forceinline__ float silu_mul(float g, float u)
+{
+#if EXL3_EXACT_SILU_DIV
+    return g / (1.0f + __expf(-g)) * u;
+#else
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+#endif
+}
+
 __global__ __launch_bounds__(HAD_THREADS)
 void act_had_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ act, const int32_t* __restrict__ expert_of_row,
                     const uint16_t* __restrict__ suh, int64_t suh_stride, int64_t rows, int I, float limit)
@@ -110,7 +122,7 @@ void act_had_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ act,
         {
             const float gc = fminf(x[i], limit);
             const float uc = fminf(fmaxf(u[i], -limit), limit);
-            const float a = gc / (1.0f + __expf(-gc)) * uc;
+            const float a = silu_mul(gc, uc);
             x[i] = h2f(f2h(a)) * s[i];                        // fp16 rounding point of the reference
         }
         had128_lane8(x, lane);
@@ -248,7 +260,7 @@ void act_had_t16_kernel(const void* __restrict__ gu, uint16_t* __restrict__ act,
             {
                 const float gc = fminf(gs[j], limit);
                 const float uc = fminf(fmaxf(us[j], -limit), limit);
-                const float a = gc / (1.0f + __expf(-gc)) * uc;
+                const float a = silu_mul(gc, uc);
                 x[8 * i + j] = h2f(f2h(a)) * ss[j];                 // fp16 rounding point of the reference
             }
         }
