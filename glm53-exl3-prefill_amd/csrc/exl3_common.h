@@ -5,6 +5,7 @@
 #include <stdint.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <atomic>
 #include <string>
 
 #include "../../include/exl3_grouped.h"
@@ -41,6 +42,22 @@ inline int hip_status(const char* what)
 #define EXL3_CHECK(cond, ...) do { if (!(cond)) return ::exl3::fail(__VA_ARGS__); } while (0)
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// CUs of the current device (256 if the query fails), cached per device; threads racing on the first query store the
+// same value.
+inline int device_cus()
+{
+    static std::atomic<int> cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0)
+    {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
 
 // ------------------------------------------------------------------------------------------- device helpers
 constexpr float HAD_SCALE = 0.088388347648f;     // 1/sqrt(128)

@@ -15,7 +15,6 @@
 //   * Everything lives in one caller-provided workspace; buffers that accumulate are cleared by a fill kernel (no
 //     memset nodes), and nothing is read back to the host, so a caller may capture the call in a HIP graph.
 #include <algorithm>
-#include <atomic>
 
 #include "exl3_common.h"
 
@@ -75,21 +74,8 @@ DecodeLayout decode_layout(int64_t tokens, int topk, int n_experts, int hidden, 
 #define EXL3_DECODE_WG_PER_CU 4
 #endif
 
-// Workgroups a launch should put on the device: four resident thin-kernel workgroups per CU. The CU count is cached per
-// device; threads that race on the first query store the same value.
-int target_workgroups(hipStream_t)
-{
-    static std::atomic<int> cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return EXL3_DECODE_WG_PER_CU * 256;
-    int n = cus[dev].load(std::memory_order_relaxed);
-    if (n == 0)
-    {
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev].store(n, std::memory_order_relaxed);
-    }
-    return EXL3_DECODE_WG_PER_CU * n;
-}
+// Workgroups a launch should put on the device: four resident thin-kernel workgroups per CU.
+int target_workgroups() { return EXL3_DECODE_WG_PER_CU * device_cus(); }
 
 // K slices for a launch of `wgs` workgroups over `stages` 32-wide K stages: as many as fit in one round of `target`
 // resident workgroups (a partial second round would double the launch's time), each slice at least 2 stages.
@@ -179,7 +165,7 @@ extern "C" int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, co
     rc = exl3_row_had_ex(x, h13, token_sorted, expert_of_row, suh_gate, suh13_stride, hidden, R, hidden, 1,
                          EXL3_LAYOUT_T16, stream);
     if (rc) return rc;
-    const int target = target_workgroups(s);
+    const int target = target_workgroups();
     const int gu_split = k_split_for((int64_t) L.max_blocks * 2 * (inter / 128), hidden / 32, target);
     rc = exl3_grouped_gemm_split(h13, R, hidden, EXL3_LAYOUT_T16, packed_gate, packed_up, w13_expert_stride_words,
                                  hidden / 16, inter / 16, bits, svh_gate, svh_up, svh13_stride, block_expert,

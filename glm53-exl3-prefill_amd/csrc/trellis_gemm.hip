@@ -27,7 +27,6 @@
 #include "trellis_decode.h"
 
 #include <algorithm>
-#include <atomic>
 #include <type_traits>
 
 namespace exl3 {
@@ -894,20 +893,6 @@ void zero_f32x4_kernel(float4* __restrict__ p, int64_t n4)
 {
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t) gridDim.x * 256) p[i] = z;
-}
-
-int device_cus()
-{
-    static std::atomic<int> cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    int n = cus[dev].load(std::memory_order_relaxed);
-    if (n == 0)
-    {
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev].store(n, std::memory_order_relaxed);
-    }
-    return n;
 }
 
 // A single-expert fp32 GEMM with a long K whose 256-row tiles would give at most one workgroup per CU (two fit) runs
