@@ -388,8 +388,16 @@ __global__ __launch_bounds__(1024)
 void build_tiles_split_kernel(const int32_t* __restrict__ counts, int n_experts, int tile_rows, int thin_rows,
                               int max_full, int max_thin, int32_t* __restrict__ full_expert,
                               int32_t* __restrict__ full_row0, int32_t* __restrict__ thin_expert,
-                              int32_t* __restrict__ thin_row0, int32_t* __restrict__ meta)
+                              int32_t* __restrict__ thin_row0, int32_t* __restrict__ meta,
+                              float4* __restrict__ zero, int64_t zero4)
 {
+    if (blockIdx.x > 0)                                   // workgroups 1..: clear the caller's fp32 buffer
+    {
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int64_t i = (int64_t) (blockIdx.x - 1) * 1024 + threadIdx.x; i < zero4; i += (int64_t) (gridDim.x - 1) * 1024)
+            zero[i] = z;
+        return;
+    }
     __shared__ int32_t s_rows[1024];
     __shared__ int32_t s_full[1024];
     __shared__ int32_t s_thin[1024];
@@ -598,7 +606,8 @@ extern "C" int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_r
 
 extern "C" int exl3_build_tiles_split(const int32_t* counts, int n_experts, int tile_rows, int thin_rows,
                                       int max_full, int max_thin, int32_t* full_expert, int32_t* full_row0,
-                                      int32_t* thin_expert, int32_t* thin_row0, int32_t* meta, void* stream)
+                                      int32_t* thin_expert, int32_t* thin_row0, int32_t* meta, float* zero,
+                                      int64_t zero_floats, void* stream)
 {
     EXL3_CHECK(n_experts >= 0 && n_experts <= MAX_EXPERTS, "too many experts");
     EXL3_CHECK((tile_rows == 128 || tile_rows == 256 || tile_rows == 512) && thin_rows == 64,
@@ -606,9 +615,13 @@ extern "C" int exl3_build_tiles_split(const int32_t* counts, int n_experts, int 
     EXL3_CHECK(max_full >= 0 && max_thin >= 0, "bad table sizes");
     EXL3_CHECK(counts && meta && (max_full == 0 || (full_expert && full_row0)) &&
                (max_thin == 0 || (thin_expert && thin_row0)), "null pointer");
-    build_tiles_split_kernel<<<1, 1024, 0, as_stream(stream)>>>(counts, n_experts, tile_rows, thin_rows, max_full,
-                                                                max_thin, full_expert, full_row0, thin_expert,
-                                                                thin_row0, meta);
+    EXL3_CHECK(zero_floats >= 0 && zero_floats % 4 == 0 && (zero_floats == 0 || zero) &&
+               (reinterpret_cast<uintptr_t>(zero) & 15) == 0, "zero must be 16-byte aligned, a multiple of 4 floats");
+    const int64_t zero4 = zero_floats / 4;
+    const int64_t zwgs = zero4 > 0 ? std::min<int64_t>((zero4 + 1023) / 1024, 2048) : 0;
+    build_tiles_split_kernel<<<(unsigned) (1 + zwgs), 1024, 0, as_stream(stream)>>>(
+        counts, n_experts, tile_rows, thin_rows, max_full, max_thin, full_expert, full_row0, thin_expert, thin_row0,
+        meta, reinterpret_cast<float4*>(zero), zero4);
     return hip_status("build_tiles_split");
 }
 

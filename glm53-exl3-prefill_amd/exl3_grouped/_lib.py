@@ -32,7 +32,7 @@ SIGNATURES = {
     "exl3_sort_routes": (I32, [P, I32, P, I32, I64, I32, I32, P, P, P, P, P, P, P, SZ, P]),
     "exl3_build_blocks": (I32, [P, I32, I32, P, P, P, P]),
     "exl3_build_tiles": (I32, [P, I32, I32, I32, P, P, P, P]),
-    "exl3_build_tiles_split": (I32, [P, I32, I32, I32, I32, I32, P, P, P, P, P, P]),
+    "exl3_build_tiles_split": (I32, [P, I32, I32, I32, I32, I32, P, P, P, P, P, P, I64, P]),
     "exl3_row_had": (I32, [P, P, P, P, P, I64, I64, I64, I32, I32, P]),
     "exl3_row_had_ex": (I32, [P, P, P, P, P, I64, I64, I64, I32, I32, I32, P]),
     "exl3_act_had": (I32, [P, I64, P, P, P, I64, I64, I32, F32, P]),
@@ -61,7 +61,7 @@ SIGNATURES = {
                               P, I64, P, I64, F32, P, P, I64, P]),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lib = None
 _path = None

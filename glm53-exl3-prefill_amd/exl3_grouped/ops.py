@@ -155,18 +155,23 @@ def build_tiles(counts: torch.Tensor, tile_expert: torch.Tensor, tile_row0: torc
 # ------------------------------------------------------------------------------------------- Hadamard passes
 def build_tiles_split(counts: torch.Tensor, full_expert: torch.Tensor, full_row0: torch.Tensor,
                       thin_expert: torch.Tensor, thin_row0: torch.Tensor, meta: torch.Tensor, tile_rows: int = 256,
-                      thin_rows: int = 64) -> None:
+                      thin_rows: int = 64, zero: Optional[torch.Tensor] = None) -> None:
     """Two tile tables (new): `tile_rows`-row tiles with each expert's small last tile (<= thin_rows rows) moved to a
-    `thin_rows`-row table for the grouped GEMM's thin kernel. meta int32[3] = {full tiles, rows, thin tiles}."""
+    `thin_rows`-row table for the grouped GEMM's thin kernel. meta int32[3] = {full tiles, rows, thin tiles}.
+    zero (optional, fp32 contiguous, numel % 4 == 0): cleared by the same launch (the down scatter's output)."""
     for t in (counts, full_expert, full_row0, thin_expert, thin_row0, meta):
         _check(t.dtype == torch.int32 and t.is_contiguous(), "int32 contiguous tensors")
     _check(full_row0.numel() >= full_expert.numel() and thin_row0.numel() >= thin_expert.numel() and
            meta.numel() >= 3, "tables: row0 at least as long as expert, meta int32[3]")
-    dev = _require_cuda(counts, full_expert, full_row0, thin_expert, thin_row0, meta)
+    _check(zero is None or (zero.dtype == torch.float32 and zero.is_contiguous() and zero.numel() % 4 == 0),
+           "zero must be fp32 contiguous with a multiple of 4 elements")
+    tensors = (counts, full_expert, full_row0, thin_expert, thin_row0, meta) + ((zero,) if zero is not None else ())
+    dev = _require_cuda(*tensors)
     with _On(dev) as s:
         _lib.call("exl3_build_tiles_split", _p(counts), counts.numel(), int(tile_rows), int(thin_rows),
                   full_expert.numel(), thin_expert.numel(), _p(full_expert), _p(full_row0), _p(thin_expert),
-                  _p(thin_row0), _p(meta), s)
+                  _p(thin_row0), _p(meta), _p(zero) if zero is not None else None,
+                  zero.numel() if zero is not None else 0, s)
 
 
 def t16_rows(rows: int) -> int:

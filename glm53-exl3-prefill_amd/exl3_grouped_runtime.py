@@ -125,12 +125,15 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     block_expert = torch.empty(max_blocks, dtype=torch.int32, device=dev)
     block_row0 = torch.empty_like(block_expert)
     thin = (thin_tiles_enabled() if thin_tiles is None else thin_tiles) and scatter == "atomic"
+    out = None
     if thin:
-        # each expert's last tile of <= 64 rows goes to a second table, run by the thin kernel
+        # each expert's last tile of <= 64 rows goes to a second table, run by the thin kernel; the same launch
+        # clears the fp32 output the down scatter adds into
         thin_expert = torch.empty(min(E, R), dtype=torch.int32, device=dev)
         thin_row0 = torch.empty_like(thin_expert)
         meta = torch.empty(3, dtype=torch.int32, device=dev)              # written whole by the kernel
-        gp.build_tiles_split(counts, block_expert, block_row0, thin_expert, thin_row0, meta, tr, THIN_ROWS)
+        out = torch.empty(T, K, dtype=torch.float32, device=dev)
+        gp.build_tiles_split(counts, block_expert, block_row0, thin_expert, thin_row0, meta, tr, THIN_ROWS, zero=out)
     else:
         meta = torch.empty(2, dtype=torch.int32, device=dev)
         gp.build_tiles(counts, block_expert, block_row0, meta, tr)
@@ -152,8 +155,9 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     gp.act_had(gu, act, expert_of_row, layer.w2_suh, float(limit), dst_layout=1, gu_layout=1, rows=R)
     mark("act_had")
     if scatter == "atomic":
-        out = torch.zeros(T, K, dtype=torch.float32, device=dev)
-        mark("zero_out")
+        if out is None:
+            out = torch.zeros(T, K, dtype=torch.float32, device=dev)
+            mark("zero_out")
         gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
                         block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, out, 1,
                         tile_rows=tr, a_layout=1, a_rows=R)

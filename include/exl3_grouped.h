@@ -111,11 +111,12 @@ int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_rows, int ma
  * last tile goes to a second table of thin_rows-row tiles (64) when it holds at most thin_rows rows;
  * the grouped GEMM runs the second table on its thin kernel (modes 0, 1, 3 with tile_rows 64). Tails are -1 as in
  * exl3_build_tiles; meta int32[3] = {full tiles, rows, thin tiles}. Bounds: max_full >= R/tile_rows + n_experts,
- * max_thin >= min(n_experts, R).
+ * max_thin >= min(n_experts, R). The same launch also zeroes zero[0 .. zero_floats) (16-byte aligned, a multiple of 4
+ * floats; 0 and NULL for none): the fp32 output the down GEMM's atomic scatter adds into.
  */
 int exl3_build_tiles_split(const int32_t* counts, int n_experts, int tile_rows, int thin_rows, int max_full,
                            int max_thin, int32_t* full_expert, int32_t* full_row0, int32_t* thin_expert,
-                           int32_t* thin_row0, int32_t* meta, void* stream);
+                           int32_t* thin_row0, int32_t* meta, float* zero, int64_t zero_floats, void* stream);
 
 /*
  * Input Hadamard (pybind op row_had, kernel/exl3_grouped_prefill.cu:101-115 and :296-311):

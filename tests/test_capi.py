@@ -321,11 +321,15 @@ def test_route_prep_small_contract():
 
 
 def test_build_tiles_split_contract():
-    rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 8, 256, 128, 10, 8, FAKE, FAKE, FAKE, FAKE, FAKE, None)
+    rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 8, 256, 128, 10, 8, FAKE, FAKE, FAKE, FAKE, FAKE, None, 0, None)
     assert rc == _lib.EXL3_ERR_ARG and "thin_rows 64" in msg
-    rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 8, 64, 64, 10, 8, FAKE, FAKE, FAKE, FAKE, FAKE, None)
+    rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 8, 64, 64, 10, 8, FAKE, FAKE, FAKE, FAKE, FAKE, None, 0, None)
     assert rc == _lib.EXL3_ERR_ARG and "tile_rows" in msg
-    rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 1025, 256, 64, 10, 8, FAKE, FAKE, FAKE, FAKE, FAKE, None)
+    rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 1025, 256, 64, 10, 8, FAKE, FAKE, FAKE, FAKE, FAKE, None, 0, None)
     assert rc == _lib.EXL3_ERR_ARG and msg == "too many experts"
-    rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 8, 256, 64, 10, 8, FAKE, FAKE, None, FAKE, FAKE, None)
+    rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 8, 256, 64, 10, 8, FAKE, FAKE, None, FAKE, FAKE, None, 0, None)
     assert rc == _lib.EXL3_ERR_ARG and msg == "null pointer"
+    for zero, n in ((None, 8), (FAKE, 6), (ctypes.c_void_p(0x1004), 8), (FAKE, -4)):   # the clear: NULL, ragged, misaligned
+        rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 8, 256, 64, 10, 8, FAKE, FAKE, FAKE, FAKE, FAKE, zero, n,
+                             None)
+        assert rc == _lib.EXL3_ERR_ARG and "zero must be" in msg, (zero, n)

@@ -173,7 +173,10 @@ def test_build_tiles_split_bit_exact(dev, kind, T, E, k, tile_rows):
     assert sorted(full + thin) == sorted(zip(rbe[:n].tolist(), rbr[:n].tolist()))
     t = [torch.full((m,), -7, dtype=torch.int32, device=dev) for m in (mf, mf, mt, mt)]
     meta = torch.full((3,), -5, dtype=torch.int32, device=dev)
-    gp.build_tiles_split(t16(counts, dev), *t, meta, tile_rows, 64)
+    zero = torch.full((T * 37 * 4 + 8,), float("nan"), dtype=torch.float32, device=dev)     # the fused output clear
+    gp.build_tiles_split(t16(counts, dev), *t, meta, tile_rows, 64, zero=zero[4:-4])
+    torch.cuda.synchronize()
+    assert (zero[4:-4] == 0).all() and zero[:4].isnan().all() and zero[-4:].isnan().all()   # exactly the range
     fe, fr, te, tr_ = (x.cpu().numpy() for x in t)
     assert meta.tolist() == [len(full), rows, len(thin)]
     assert list(zip(fe[:len(full)].tolist(), fr[:len(full)].tolist())) == full
