@@ -1,0 +1,676 @@
+// Weight-stationary trellis GEMM kernels for gfx950: the grouped gate|up / down stages of the EXL3 MoE prefill
+// (kernel/exl3_grouped_prefill.cu:148-279) and the single-expert fat GEMM (kernel/exl3_fat_gemm_v2.cu:72-234).
+//
+// Workgroup = 4 waves, tile = up to 256 rows x 128 output columns (one H128 block), K stage = 32.
+//   * Each stage's 16 trellis tiles (32 x 128 weights) are decoded ONCE per workgroup -- a 16-lane row per tile, every
+//     lane decoding two 8-weight chunks from one coalesced load of its own stream words -- into a k-contiguous [n][k]
+//     fp16 tile in LDS, and reused by all four waves for every row of the tile. A row tile covers `tile_rows` (128 or
+//     256) rows of one expert, so each decoded weight feeds up to 256 rows of MFMA work.
+//   * Each wave owns 64 rows x 128 columns and runs v_mfma_f32_16x16x32_f16 with the DECODED WEIGHTS as the first
+//     operand and the activations as the second (out^T in the accumulators: a lane owns one row and 32 columns). The
+//     activation operand of one MFMA is 16 rows x 64 contiguous bytes, so each activation load instruction touches 16
+//     cache-line halves -- the vector memory pipeline (TA/TD), not HBM, is what the loads are sized for.
+//   * Pipeline of stage s: barrier; read stage s's weight fragments from LDS; decode stage s+1 (VALU) while stage s's
+//     MFMAs run; write stage s+1 into the other LDS buffer; issue loads for later stages. Raw trellis words are
+//     prefetched RAW_DEPTH stages ahead and activations ACT_DEPTH stages ahead, straight into VGPRs. One barrier per
+//     stage guards the double-buffered decoded tile.
+//   * A wave with <= 16 valid rows multiplies one 16-row group, a wave with none only decodes (thin experts).
+//   * Epilogue: H128 with 5 butterfly stages in registers and 2 across lanes, x svh / sqrt(128), fp16 store, fp32
+//     store, fp32 per-route store, or fp32 atomics staged through LDS so each atomic instruction covers 64 consecutive
+//     floats of one output row.
+//   * Workgroups are laid out XCD-aware: the column tiles of one row tile share an XCD (and its L2).
+//   * Activations and trellis words are read through buffer resources: fixed per-lane offsets plus a scalar stage
+//     offset, and zero instead of a fault outside the operand.
+// Variants of the same kernel: 16 rows per wave (64-row tiles, four workgroups per CU) for small tiles, and 8 waves
+// (512-row tiles, one workgroup per CU, each wave decoding one chunk per lane) for 512-row tiles and large dense GEMMs.
+#pragma once
+#include "exl3_common.h"
+#include "trellis_decode.h"
+
+#include <algorithm>
+#include <type_traits>
+
+namespace exl3 {
+
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int TILE_N = 128;
+constexpr int TILE_K = 32;
+#ifndef EXL3_LDS_ROW_PAD
+#define EXL3_LDS_ROW_PAD 8
+#endif
+#ifndef EXL3_LDS_BLK_PAD
+#define EXL3_LDS_BLK_PAD 64
+#endif
+constexpr int LDS_ROW = TILE_K + EXL3_LDS_ROW_PAD;  // halves per n-row of the decoded tile (80 B)
+constexpr int LDS_BLK = 16 * LDS_ROW + EXL3_LDS_BLK_PAD;   // halves per 16-row block: the pad puts neighbouring
+                                                    // tiles' decode stores 32 banks apart
+constexpr int LDS_TILE = 8 * LDS_BLK;               // halves per decoded stage (128 n-rows)
+constexpr int SC_ROW = TILE_N + 4;                  // floats per staged output row of the scatter epilogue
+constexpr int LDS_MAIN_BYTES = 2 * LDS_TILE * 2;
+#ifndef EXL3_RAW_DEPTH
+#define EXL3_RAW_DEPTH 4
+#endif
+#ifndef EXL3_ACT_DEPTH
+#define EXL3_ACT_DEPTH 2
+#endif
+constexpr int RAW_DEPTH = EXL3_RAW_DEPTH;           // raw trellis words in flight (stages)
+constexpr int ACT_DEPTH = EXL3_ACT_DEPTH;           // activation tiles in flight (stages)
+constexpr int UNROLL = 4;                           // stages per loop trip: register buffers keep static names
+static_assert(UNROLL % 2 == 0 && UNROLL % RAW_DEPTH == 0 && UNROLL % ACT_DEPTH == 0, "static buffer rotation");
+
+// STORE_F16: fp16 rows (gate|up). SCATTER_F32: fp32 atomic add into out[token[r]]. STORE_F32: fp32 rows (fat GEMM).
+// STORE_ROUTE_F32: fp32 rows at out[route_index[r]] (per-route partials for the deterministic combine).
+// ATOMIC_F32: fp32 atomic add into out[r] (gate|up partial sums of a split-K launch).
+enum { MODE_STORE_F16 = 0, MODE_SCATTER_F32 = 1, MODE_STORE_F32 = 2, MODE_STORE_ROUTE_F32 = 3, MODE_ATOMIC_F32 = 4 };
+// Modes whose epilogue stages rows through LDS and adds them to the output with atomics.
+constexpr bool atomic_mode(int mode) { return mode == MODE_SCATTER_F32 || mode == MODE_ATOMIC_F32; }
+
+struct GemmParams
+{
+    const uint16_t* a;             // [a_rows, size_k] fp16, row-major or T16 (a_t16)
+    int64_t a_rows;
+    int a_t16;
+    int size_k;
+    const uint16_t* packed0;       // trellis of tensor 0 (gate / single tensor)
+    const uint16_t* packed1;       // trellis of tensor 1 (up), may be null
+    int64_t expert_stride_words;   // uint16 words between experts
+    int tiles_n;                   // 16-col trellis tiles per tensor
+    const uint16_t* svh0;
+    const uint16_t* svh1;
+    int64_t svh_stride;
+    const int32_t* block_expert;   // grouped schedule: row tiles of `tile_rows` rows
+    const int32_t* block_row0;
+    const int32_t* counts;
+    const int32_t* expert_row0;
+    int tile_rows;                 // rows per row tile (grouped: 128, 256 or 512; dense: 64 x waves)
+    int n_groups;                  // row tiles (grouped: table entries; dense: ceil(m / tile_rows))
+    int n_slots;                   // 128-col tiles over all tensors
+    int n_tiles_each;              // 128-col tiles per tensor
+    int k_split;                   // K slices per output tile (0 or 1: none); slices add into the output atomically
+    int kb_per_split;              // TILE_K stages per slice (even)
+    int64_t m;                     // dense rows
+    const int64_t* token;          // scatter destination row per sorted row
+    const uint16_t* route_weight;  // fp16 per sorted row
+    const int32_t* route_index;    // STORE_ROUTE_F32 destination row per sorted row
+    void* out;
+    int64_t out_ld;                // elements per output row
+    int out_t16;                   // STORE_F16: out in the T16 layout (16-row x 8-column blocks), width out_ld
+};
+
+// In-place Walsh-Hadamard transform of 32 values (Sylvester order over the index bits).
+__device__ __forceinline__ void fwht32(float (&x)[32])
+{
+    #pragma unroll
+    for (int len = 1; len < 32; len <<= 1)
+        #pragma unroll
+        for (int i = 0; i < 32; ++i)
+            if (!(i & len))
+            {
+                const float a = x[i], b = x[i + len];
+                x[i] = a + b;
+                x[i + len] = a - b;
+            }
+}
+
+// Raw stream dwords a lane holds per stage. K=4 / K=2: the lane's own 2 / 1 dwords of the tile (one coalesced load
+// per 16-lane row) -- the 16-bit look-back of its first chunk is the previous lane's last dword (DPP rotate);
+// K=3: the three dwords its two windows touch, loaded directly.
+template <int BITS> constexpr int raw_words() { return BITS == 4 ? 2 : (BITS == 2 ? 1 : 3); }
+
+// Value of `v` in the previous lane of this lane's 16-lane row (lane 0 of the row gets lane 15's).
+__device__ __forceinline__ uint32_t prev_in_row(uint32_t v)
+{
+    return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, 0x121, 0xF, 0xF, false);     // row_ror:1
+}
+
+// Raw buffer resource over [base, base + bytes): loads through it take a per-lane 32-bit offset and a uniform scalar
+// offset, and return zero (instead of faulting) outside the range. Word 3 selects 32-bit data for untyped access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int64_t bytes)
+{
+    const int n = (int) (bytes < 0 ? 0 : (bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes));
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short) 0, n, 0x00020000);
+}
+
+// f(integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for_from(F&& f)
+{
+    if constexpr (I < N)
+    {
+        f(std::integral_constant<int, I>{});
+        static_for_from<I + 1, N>(f);
+    }
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) { static_for_from<0, N>(f); }
+
+// ------------------------------------------------------------------------------------------- workgroup tile
+// The rows (of one expert), tensor and 128-column tile one workgroup computes.
+struct Tile
+{
+    int e, row0, rows_valid, which, nt;
+    int kb0, num_kb;               // the workgroup's K slice: TILE_K stages kb0 .. kb0 + num_kb - 1
+    const uint32_t* packed;        // the tensor's trellis for expert e
+    const uint16_t* svh;           // svh of the tile's 128 output columns
+};
+
+// `slot` runs over n_slots x k_split: the column tile, then the K slice.
+template <bool DENSE>
+__device__ __forceinline__ bool resolve_tile(const GemmParams& p, int group, int slot, Tile& t)
+{
+    if (group >= p.n_groups) return false;
+    const int total_kb = p.size_k / TILE_K;
+    t.kb0 = 0;
+    t.num_kb = total_kb;
+    if (p.k_split > 1)
+    {
+        const int ks = slot / p.n_slots;
+        slot -= ks * p.n_slots;
+        t.kb0 = ks * p.kb_per_split;
+        t.num_kb = min(p.kb_per_split, total_kb - t.kb0);
+        if (t.num_kb <= 0) return false;
+    }
+    if constexpr (DENSE)
+    {
+        t.e = 0;
+        t.row0 = group * p.tile_rows;
+        t.rows_valid = (int) min((int64_t) p.tile_rows, p.m - t.row0);
+    }
+    else
+    {
+        t.e = p.block_expert[group];
+        if (t.e < 0) return false;
+        t.row0 = p.block_row0[group];
+        t.rows_valid = min(p.tile_rows, p.expert_row0[t.e] + p.counts[t.e] - t.row0);
+    }
+    if (t.rows_valid <= 0) return false;
+    t.which = slot >= p.n_tiles_each ? 1 : 0;
+    t.nt = slot - t.which * p.n_tiles_each;
+    t.packed = reinterpret_cast<const uint32_t*>((t.which ? p.packed1 : p.packed0) +
+                                                 (int64_t) t.e * p.expert_stride_words);
+    t.svh = (t.which ? p.svh1 : p.svh0) + (int64_t) t.e * p.svh_stride + t.nt * TILE_N;
+    return true;
+}
+
+// ------------------------------------------------------------------------------------------- decoding share
+// Wave dw's (0..3) share of decoding each stage. A stage holds 16 trellis tiles (kt, nt8) = (k-tile 0..1, n-tile
+// 0..7); wave dw decodes the four tiles kt = dw >> 1, nt8 = 4 (dw & 1) .. + 3 (512 contiguous bytes at 4 bpw), one
+// 16-lane row per tile. Lane j16 of a row decodes chunks 2 j16 and 2 j16 + 1 (positions 16 j16 .. + 15): tile column
+// a = j16 >> 1 and a + 8, rows 4 b .. 4 b + 3 and 8 + 4 b .. with b = j16 & 1.
+template <int N> struct Chunks { Chunk4 c[N]; };
+
+template <int BITS>
+struct Decoder
+{
+    static constexpr int NDW = 8 * BITS;                  // dwords per tile
+    static constexpr int NR = raw_words<BITS>();
+    using Out = Chunks<2>;
+    __amdgpu_buffer_rsrc_t raw;    // based at the wave's first tile of stage 0
+    int stage_bytes, last_kb, tb, wcol0, wcol1;
+    uint32_t off[NR];              // per-lane byte offsets of the raw words
+
+    __device__ __forceinline__ Decoder(const GemmParams& p, const Tile& t, int dw, int lane, int num_kb)
+    {
+        const int j16 = lane & 15;
+        const int ta = j16 >> 1;
+        tb = j16 & 1;
+        const int kt = dw >> 1;
+        const int nt8 = 4 * (dw & 1) + (lane >> 4);
+        stage_bytes = 2 * p.tiles_n * NDW * 4;
+        const int64_t first = ((int64_t) (2 * t.kb0 + kt) * p.tiles_n + t.nt * 8 + 4 * (dw & 1)) * NDW;
+        raw = buffer_rsrc(t.packed + first, ((int64_t) (p.size_k >> 4) * p.tiles_n * NDW - first) * 4);
+        last_kb = num_kb - 1;
+        const int tile_off = (lane >> 4) * NDW;
+        if constexpr (BITS == 3)
+        {
+            const int d0 = (16 * j16 * BITS + BITS - 16) >> 5;  // dword of the first window bit (may be -1)
+            #pragma unroll
+            for (int i = 0; i < NR; ++i) off[i] = 4 * (tile_off + (d0 + i + NDW) % NDW);
+        }
+        else
+        {
+            #pragma unroll
+            for (int i = 0; i < NR; ++i) off[i] = 4 * (tile_off + NR * j16 + i);
+        }
+        wcol0 = nt8 * LDS_BLK + ta * LDS_ROW + kt * 16 + 4 * tb;         // column a, rows 4 b ..
+        wcol1 = wcol0 + 8 * LDS_ROW;                                    // column a + 8
+    }
+    // Raw words of stage kb (clamped to the last stage, so callers may run ahead of the end).
+    __device__ __forceinline__ void load(int kb, uint32_t (&r)[NR]) const
+    {
+        const int so = min(kb, last_kb) * stage_bytes;
+        if constexpr (BITS == 4)
+        {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(raw, off[0], so, 0);
+            r[0] = v[0];
+            r[1] = v[1];
+        }
+        else
+        {
+            #pragma unroll
+            for (int i = 0; i < NR; ++i) r[i] = __builtin_amdgcn_raw_buffer_load_b32(raw, off[i], so, 0);
+        }
+    }
+    __device__ __forceinline__ void decode(const uint32_t (&r)[NR], Out& o) const
+    {
+        Chunk4& c0 = o.c[0];
+        Chunk4& c1 = o.c[1];
+        if constexpr (BITS == 4)
+        {
+            const uint32_t prev = prev_in_row(r[1]);
+            c0 = decode_chunk<4>(prev, r[0], 20);
+            c1 = decode_chunk<4>(r[0], r[1], 20);
+        }
+        else if constexpr (BITS == 2)
+        {
+            const uint32_t prev = prev_in_row(r[0]);
+            c0 = decode_chunk<2>(prev, r[0], 18);
+            c1 = decode_chunk<2>(r[0], r[0], 2);              // window ends inside r[0]
+        }
+        else
+        {
+            // chunk pair j16: windows start 19 / 43 bits (j16 even) or 3 / 27 bits (odd) into dw_off[0]. Even lanes
+            // shift their words down by 16 bits first, so both kinds decode at the compile-time offsets 3 and 27:
+            // constant shifts of a 64-bit window compile to 32-bit funnel shifts, while per-lane 64-bit shift amounts
+            // feeding the decoder's asm gave wrong results at random.
+            const uint32_t x0 = tb ? r[0] : __builtin_amdgcn_alignbit(r[1], r[0], 16);
+            const uint32_t x1 = tb ? r[1] : __builtin_amdgcn_alignbit(r[2], r[1], 16);
+            c0 = decode_chunk<3>(x0, x1, 3);
+            c1 = decode_chunk<3>(x0, x1, 27);
+        }
+    }
+    __device__ __forceinline__ void store(const Out& o, uint16_t* lds) const
+    {
+        const Chunk4& c0 = o.c[0];
+        const Chunk4& c1 = o.c[1];
+        *reinterpret_cast<uint2*>(lds + wcol0) = make_uint2(c0.w[0], c1.w[0]);
+        *reinterpret_cast<uint2*>(lds + wcol0 + 8) = make_uint2(c0.w[1], c1.w[1]);
+        *reinterpret_cast<uint2*>(lds + wcol1) = make_uint2(c0.w[2], c1.w[2]);
+        *reinterpret_cast<uint2*>(lds + wcol1 + 8) = make_uint2(c0.w[3], c1.w[3]);
+    }
+};
+
+// Wave dw's (0..7) share of decoding each stage in an 8-wave workgroup: the two tiles kt = dw >> 2,
+// nt8 = 2 (dw & 3) .. + 1, one 32-lane half per tile. Lane c (0..31) of a half decodes chunk c (positions 8c .. 8c + 7):
+// tile column c >> 2 and (c >> 2) + 8, rows 2 (c & 3), + 1, + 8, + 9. Its window bits [8cK + K - 16, 8cK + 8K) sit in
+// the two tile dwords lo = floor(b / 32), hi = lo + 1 (mod 8K, the stream is tail-biting) starting `shift` bits into
+// lo; 16 + 7K <= 44 bits and shift <= 27 for K <= 4, so two dwords always hold them.
+template <int BITS>
+struct Decoder1
+{
+    static constexpr int NDW = 8 * BITS;
+    static constexpr int NR = 2;
+    using Out = Chunks<1>;
+    __amdgpu_buffer_rsrc_t raw;    // based at the wave's first tile of stage 0
+    int stage_bytes, last_kb, shift, wcol0, wcol1;
+    uint32_t lo_off, hi_off;       // per-lane byte offsets of the two raw words
+
+    __device__ __forceinline__ Decoder1(const GemmParams& p, const Tile& t, int dw, int lane, int num_kb)
+    {
+        const int c = lane & 31;
+        const int kt = dw >> 2;
+        const int nt8 = 2 * (dw & 3) + (lane >> 5);
+        stage_bytes = 2 * p.tiles_n * NDW * 4;
+        const int64_t first = ((int64_t) (2 * t.kb0 + kt) * p.tiles_n + t.nt * 8 + 2 * (dw & 3)) * NDW;
+        raw = buffer_rsrc(t.packed + first, ((int64_t) (p.size_k >> 4) * p.tiles_n * NDW - first) * 4);
+        last_kb = num_kb - 1;
+        const int b0 = 8 * c * BITS + BITS - 16;              // first window bit, >= -15
+        const int d0 = b0 >= 0 ? (b0 >> 5) : -1;
+        shift = b0 - 32 * d0;
+        lo_off = 4 * ((lane >> 5) * NDW + (d0 + NDW) % NDW);
+        hi_off = 4 * ((lane >> 5) * NDW + (d0 + 1) % NDW);
+        wcol0 = nt8 * LDS_BLK + (c >> 2) * LDS_ROW + kt * 16 + 2 * (c & 3);
+        wcol1 = wcol0 + 8 * LDS_ROW;
+    }
+    __device__ __forceinline__ void load(int kb, uint32_t (&r)[NR]) const
+    {
+        const int so = min(kb, last_kb) * stage_bytes;
+        r[0] = __builtin_amdgcn_raw_buffer_load_b32(raw, lo_off, so, 0);
+        r[1] = __builtin_amdgcn_raw_buffer_load_b32(raw, hi_off, so, 0);
+    }
+    __device__ __forceinline__ void decode(const uint32_t (&r)[NR], Out& o) const
+    {
+        if constexpr (BITS == 4)
+            o.c[0] = decode_chunk<4>(r[0], r[1], 20);             // shift is 20 for every chunk
+        else
+        {
+            // Realign with 32-bit funnel shifts (per-lane 64-bit shift amounts feeding the decoder's asm gave wrong
+            // results at random), then decode at the compile-time offset 0.
+            const uint32_t x0 = __builtin_amdgcn_alignbit(r[1], r[0], shift);
+            const uint32_t x1 = r[1] >> shift;
+            o.c[0] = decode_chunk<BITS>(x0, x1, 0);
+        }
+    }
+    __device__ __forceinline__ void store(const Out& o, uint16_t* lds) const
+    {
+        const Chunk4& c = o.c[0];
+        *reinterpret_cast<uint32_t*>(lds + wcol0) = c.w[0];
+        *reinterpret_cast<uint32_t*>(lds + wcol0 + 8) = c.w[1];
+        *reinterpret_cast<uint32_t*>(lds + wcol1) = c.w[2];
+        *reinterpret_cast<uint32_t*>(lds + wcol1 + 8) = c.w[3];
+    }
+};
+
+// ------------------------------------------------------------------------------------------- multiplying share
+// Wave mw's (0..3) share of the MFMA work: tile rows [64 mw, 64 mw + 64) in four groups of 16 (mb).
+// v_mfma_f32_16x16x32_f16 with the decoded weights as the first operand (16 columns x 32 k) and the activations as the
+// second (32 k x 16 rows): lane l supplies row / column l & 15 and k 8 (l >> 4) .. + 7 of both, and receives row
+// (token) l & 15, columns 4 (l >> 4) .. + 3 of the 16 x 16 output. Row-major A: an activation load is 16 rows x 16
+// bytes per lane (one lane per cycle in the address unit); T16 A: 256 contiguous bytes per 16-row group.
+// Activations are read through a buffer resource based at the tile's first row: per-lane offsets are fixed, the
+// stage advance is a scalar offset, so a load needs no vector address arithmetic.
+struct Mma
+{
+    __amdgpu_buffer_rsrc_t a_rsrc;
+    uint32_t a_off[4];
+    int a_step, wread, last_kb;
+
+    // rpw: rows per wave (contiguous groups), or gstride > 0: the wave's groups are mw, mw + gstride, ...
+    __device__ __forceinline__ Mma(const GemmParams& p, const Tile& t, int mw, int lane, int num_kb, int rpw,
+                                   int gstride = 0)
+    {
+        const int tok = lane & 15, kq = lane >> 4;
+        a_step = p.a_t16 ? 4 * 128 * 2 : TILE_K * 2;          // bytes per stage
+        const int g0 = t.row0 >> 4;
+        const int64_t base_el = (p.a_t16 ? (int64_t) g0 * (p.size_k >> 3) * 128 : (int64_t) t.row0 * p.size_k) +
+                                (int64_t) t.kb0 * (a_step / 2);       // the slice's first stage
+        const int64_t total_el = (p.a_t16 ? (p.a_rows + 15) / 16 * 16 : p.a_rows) * p.size_k;
+        a_rsrc = buffer_rsrc(p.a + base_el, (total_el - base_el) * 2);
+        #pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+        {
+            const int row = t.row0 + min((gstride ? 16 * (mw + gstride * mb) : rpw * mw + 16 * mb) + tok,
+                                         t.rows_valid - 1);
+            a_off[mb] = p.a_t16 ? (uint32_t) ((((row >> 4) - g0) * (p.size_k >> 3) + kq) * 256 + (row & 15) * 16)
+                                : (uint32_t) ((row - t.row0) * p.size_k * 2 + 16 * kq);
+        }
+        wread = tok * LDS_ROW + 8 * kq;
+        last_kb = num_kb - 1;
+    }
+    template <int MBA, int N>
+    __device__ __forceinline__ void load_act(int kb, half8_t (&a)[N]) const
+    {
+        static_assert(MBA <= N, "activation groups");
+        const int so = min(kb, last_kb) * a_step;
+        #pragma unroll
+        for (int mb = 0; mb < MBA; ++mb)
+            a[mb] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off[mb], so, 0));
+    }
+    __device__ __forceinline__ void read_w(const uint16_t* lds, half8_t (&w)[8]) const
+    {
+        #pragma unroll
+        for (int nb = 0; nb < 8; ++nb) w[nb] = *reinterpret_cast<const half8_t*>(lds + nb * LDS_BLK + wread);
+    }
+    template <int MBA, int MBN>
+    __device__ __forceinline__ static void mfma(const half8_t (&w)[8], const half8_t (&a)[MBN], floatx4 (&acc)[MBN][8])
+    {
+        static_assert(MBA <= MBN, "row groups");
+        #pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+            #pragma unroll
+            for (int mb = 0; mb < MBA; ++mb)
+                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[nb], a[mb], acc[mb][nb], 0, 0, 0);
+    }
+};
+
+// ------------------------------------------------------------------------------------------- epilogue
+// Per 16-row group of multiplying wave mw (16 MBN rows per wave): H128 over the 128 columns of each row (lane l holds columns
+// 16 nb + 4 (l >> 4) + r: 5 butterfly stages in registers, column bit 2 across lanes l ^ 16, bit 3 across l ^ 32),
+// scale by svh / sqrt(128) (and the route weight), then store / scatter. The scatter stages each group through LDS
+// (`stage`: 16 rows x SC_ROW floats of this wave) so that every atomic instruction covers 64 consecutive floats of
+// one output row.
+// GSTRIDE > 0: the wave's groups are interleaved over the tile (group mb of wave mw is the tile's 16-row group
+// mw + GSTRIDE mb); 0: they are contiguous (rows 16 MBN mw + 16 mb ..).
+template <int MODE, int MBN, int GSTRIDE = 0>
+__device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int mw, int lane, floatx4 (&acc)[MBN][8],
+                                         float* stage)
+{
+    const int tok = lane & 15, kq = lane >> 4;
+    auto group_row0 = [&](int mb) { return GSTRIDE ? 16 * (mw + GSTRIDE * mb) : 16 * MBN * mw + 16 * mb; };
+    const int out_col0 = t.which * p.n_tiles_each * TILE_N + t.nt * TILE_N;
+    float sv[32];
+    #pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+    {
+        const uint2 v = *reinterpret_cast<const uint2*>(t.svh + 16 * nb + 4 * kq);
+        sv[4 * nb + 0] = h2f(v.x & 0xFFFF) * HAD_SCALE;
+        sv[4 * nb + 1] = h2f(v.x >> 16) * HAD_SCALE;
+        sv[4 * nb + 2] = h2f(v.y & 0xFFFF) * HAD_SCALE;
+        sv[4 * nb + 3] = h2f(v.y >> 16) * HAD_SCALE;
+    }
+    #pragma unroll
+    for (int mb = 0; mb < MBN; ++mb)
+    {
+        const int grow0 = group_row0(mb);                       // the group's first row within the tile
+        if (grow0 >= t.rows_valid) break;                       // uniform over the wave
+        float x[32];
+        #pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+            #pragma unroll
+            for (int r = 0; r < 4; ++r) x[4 * nb + r] = acc[mb][nb][r];
+        fwht32(x);
+        #pragma unroll
+        for (int i = 0; i < 32; i += 2) pair_butterfly16(x[i], x[i + 1]);
+        #pragma unroll
+        for (int i = 0; i < 32; i += 2) pair_butterfly32(x[i], x[i + 1]);
+
+        const int r_local = grow0 + tok;                        // this lane's row within the tile
+        const bool row_ok = r_local < t.rows_valid;
+        const int64_t srow = (int64_t) t.row0 + min(r_local, t.rows_valid - 1);
+        float rw = 1.0f;
+        int64_t orow = srow;
+        if constexpr (MODE == MODE_SCATTER_F32 || MODE == MODE_STORE_ROUTE_F32)
+        {
+            rw = h2f(p.route_weight[srow]);
+            orow = (MODE == MODE_SCATTER_F32) ? p.token[srow] : (int64_t) p.route_index[srow];
+        }
+        #pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+        {
+            const int col = 16 * nb + 4 * kq;                   // first of this lane's 4 consecutive columns
+            float v[4];
+            #pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = x[4 * nb + r] * sv[4 * nb + r] * rw;
+            if constexpr (atomic_mode(MODE))
+            {
+                *reinterpret_cast<float4*>(stage + tok * SC_ROW + col) = make_float4(v[0], v[1], v[2], v[3]);
+                continue;
+            }
+            if (!row_ok) continue;
+            if constexpr (MODE == MODE_STORE_F16)
+            {
+                const int64_t c = out_col0 + col;              // a multiple of 4: one half of an 8-column block
+                uint16_t* o = reinterpret_cast<uint16_t*>(p.out) +
+                              (p.out_t16 ? ((((orow >> 4) * (p.out_ld >> 3) + (c >> 3)) * 16 + (orow & 15)) * 8 + (c & 7))
+                                         : orow * p.out_ld + c);
+                uint2 pk;
+                pk.x = (uint32_t) f2h(v[0]) | ((uint32_t) f2h(v[1]) << 16);
+                pk.y = (uint32_t) f2h(v[2]) | ((uint32_t) f2h(v[3]) << 16);
+                *reinterpret_cast<uint2*>(o) = pk;
+            }
+            else
+            {
+                float* o = reinterpret_cast<float*>(p.out) + orow * p.out_ld + out_col0 + col;
+                *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        }
+        if constexpr (atomic_mode(MODE))
+        {
+            // LDS accesses of one wave complete in order: the reads below see the writes above, and the next
+            // group's writes land after these reads. Lane t (< 16) holds row t's destination row (token, or the
+            // sorted row itself in ATOMIC_F32).
+            const int nrows = min(16, t.rows_valid - grow0);
+            const uint32_t tok_lo = (uint32_t) orow, tok_hi = (uint32_t) ((uint64_t) orow >> 32);
+            float* outp = reinterpret_cast<float*>(p.out) + out_col0 + lane;
+            for (int tr = 0; tr < nrows; ++tr)
+            {
+                const int64_t trow = (int64_t) (((uint64_t) __builtin_amdgcn_readlane(tok_hi, tr) << 32) |
+                                                __builtin_amdgcn_readlane(tok_lo, tr));
+                const float v0 = stage[tr * SC_ROW + lane];
+                const float v1 = stage[tr * SC_ROW + 64 + lane];
+                float* o = outp + trow * p.out_ld;
+                unsafeAtomicAdd(o, v0);
+                unsafeAtomicAdd(o + 64, v1);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------- kernel
+// 128- and 256-row tiles: every wave decodes a quarter of each stage and multiplies its own 64 rows; two workgroups
+// share a CU. Pipeline of stage s: barrier; read stage s's weight fragments; decode stage s+1 while stage s's MFMAs run;
+// write stage s+1 into the other of two LDS buffers; issue loads for later stages.
+template <int WAVES> constexpr int lds_scatter_bytes() { return WAVES * 16 * SC_ROW * 4; }
+
+// MBN: 16-row groups per wave. 4 (the default): 256-row tiles, two workgroups per CU. 1 (thin): 64-row tiles of small
+// batches, where most waves only decode; a quarter of the accumulators lets four workgroups share a CU.
+// WAVES = 8: 512-row tiles, one workgroup per CU; each wave decodes half as much of every stage (one chunk per lane),
+// so a decoded weight feeds twice the rows for the same VALU work per wave.
+template <int BITS, int MODE, bool DENSE, int MBN = 4, int WAVES = 4>
+// (HIP's second launch bound is the minimum number of waves per SIMD: 2 leaves 256 VGPRs per wave, 4 leaves 128.)
+__global__ __launch_bounds__(64 * WAVES, MBN == 4 ? 2 : 4)
+void trellis_gemm_kernel(const GemmParams p)
+{
+    static_assert(WAVES == 4 || (WAVES == 8 && MBN == 4), "8-wave workgroups run 64 rows per wave");
+    constexpr int SCB = lds_scatter_bytes<WAVES>();
+    constexpr int LDS_BYTES = (atomic_mode(MODE) && SCB > LDS_MAIN_BYTES) ? SCB : LDS_MAIN_BYTES;
+    __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
+    uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
+
+    int group, slot;
+    xcd_group_slot((int) blockIdx.x, p.k_split > 1 ? p.n_slots * p.k_split : p.n_slots, group, slot);
+    Tile t;
+    if (!resolve_tile<DENSE>(p, group, slot, t)) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int num_kb = t.num_kb;
+    using Dec = typename std::conditional<WAVES == 8, Decoder1<BITS>, Decoder<BITS>>::type;
+    constexpr int NR = Dec::NR;
+    // 8-wave workgroups interleave the 16-row groups over the waves (wave w multiplies groups w, w + 8, ...), so a
+    // partial tile keeps both waves of every SIMD equally busy; 4-wave workgroups give each wave 16 MBN contiguous rows.
+    constexpr int GSTRIDE = WAVES == 8 ? 8 : 0;
+    const Dec dec(p, t, wave, lane, num_kb);
+    const Mma mm(p, t, wave, lane, num_kb, 16 * MBN, GSTRIDE);
+    const int n_groups = (t.rows_valid + 15) >> 4;
+    const int n_w = GSTRIDE ? (n_groups > wave ? (n_groups - wave + GSTRIDE - 1) / GSTRIDE : 0)
+                            : min(MBN, max(0, n_groups - MBN * wave));          // this wave's groups (uniform)
+
+    floatx4 acc[MBN][8];
+    #pragma unroll
+    for (int mb = 0; mb < MBN; ++mb)
+        #pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = {};
+
+    // Main loop, specialised on the number of 16-row groups a wave multiplies (MBA: 0 = decode only, 1 for a wave with
+    // <= 16 valid rows, else MBN). Every variant runs the same barriers. Loads past the last stage are clamped to it, so
+    // every path keeps the same loads in flight.
+    auto mainloop = [&](auto mba_tag) {
+        constexpr int MBA = decltype(mba_tag)::value;
+        uint32_t raw[RAW_DEPTH][NR];
+        half8_t act[ACT_DEPTH][MBN];
+        {
+            uint32_t r0[NR];
+            dec.load(0, r0);
+            #pragma unroll
+            for (int s = 1; s <= RAW_DEPTH; ++s) dec.load(s, raw[s % RAW_DEPTH]);
+            #pragma unroll
+            for (int s = 0; s < ACT_DEPTH; ++s) mm.load_act<MBA>(s, act[s]);
+            typename Dec::Out o;
+            dec.decode(r0, o);
+            dec.store(o, lds_b);
+        }
+        // N stages starting at s0 (a multiple of UNROLL, so buffer indices are compile-time)
+        auto trip = [&](int s0, auto n_tag) {
+            constexpr int N = decltype(n_tag)::value;
+            #pragma unroll
+            for (int u = 0; u < N; ++u)
+            {
+                const int s = s0 + u;
+                __syncthreads();                                // stage s decoded; buffer (s + 1) & 1 free
+                // Keep every stage's work between its barriers: hoisting a later stage's decode above the barrier
+                // would make it wait for raw words loaded in the same trip.
+                __builtin_amdgcn_sched_barrier(0);
+                half8_t w[8];
+                if constexpr (MBA > 0) mm.read_w(lds_b + (u & 1) * LDS_TILE, w);
+                typename Dec::Out o;
+                dec.decode(raw[(u + 1) % RAW_DEPTH], o);        // stage s + 1
+                Mma::mfma<MBA>(w, act[u % ACT_DEPTH], acc);
+                dec.store(o, lds_b + ((u + 1) & 1) * LDS_TILE);
+                dec.load(s + 1 + RAW_DEPTH, raw[(u + 1) % RAW_DEPTH]);
+                mm.load_act<MBA>(s + ACT_DEPTH, act[u % ACT_DEPTH]);
+            }
+        };
+        // The first trip is peeled so that the loads in flight at the loop head are the same on entry and on the
+        // back edge; the compiler's wait counts there then only wait for the stage they feed. num_kb is even
+        // (K % 64 == 0), so what is left after whole trips is 0 or 2 stages.
+        using full = std::integral_constant<int, UNROLL>;
+        int s0 = 0;
+        if (num_kb >= UNROLL)
+        {
+            trip(0, full{});
+            for (s0 = UNROLL; s0 + UNROLL <= num_kb; s0 += UNROLL) trip(s0, full{});
+        }
+        if (s0 < num_kb) trip(s0, std::integral_constant<int, 2>{});
+    };
+    if constexpr (GSTRIDE > 0)
+    {
+        static_assert(MBN == 4, "interleaved groups: up to four per wave");
+        switch (n_w)
+        {
+            case 4: mainloop(std::integral_constant<int, 4>{}); break;
+            case 3: mainloop(std::integral_constant<int, 3>{}); break;
+            case 2: mainloop(std::integral_constant<int, 2>{}); break;
+            case 1: mainloop(std::integral_constant<int, 1>{}); break;
+            default: mainloop(std::integral_constant<int, 0>{}); break;
+        }
+    }
+    else if (MBN > 1 && n_w > 1) mainloop(std::integral_constant<int, MBN>{});
+    else if (n_w > 0) mainloop(std::integral_constant<int, 1>{});
+    else mainloop(std::integral_constant<int, 0>{});
+
+    if constexpr (atomic_mode(MODE)) __syncthreads();            // decoded tiles are dead; LDS becomes staging
+    if (n_w == 0) return;
+    epilogue<MODE, MBN, GSTRIDE>(p, t, wave, lane, acc, reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW));
+}
+
+// 512-row tiles run the 8-wave variant, 128- and 256-row tiles the 4-wave kernel (the only one built for ATOMIC_F32,
+// whose split-K launches serve small batches), 64-row tiles of grouped modes 0, 1 and 3 the thin 4-wave variant.
+template <int BITS, int MODE, bool DENSE>
+int launch_gemm(const GemmParams& p, hipStream_t s)
+{
+    const int groups8 = (p.n_groups + 7) / 8 * 8;
+    const int64_t grid = (int64_t) groups8 * p.n_slots * (p.k_split > 1 ? p.k_split : 1);
+    if (grid == 0) return EXL3_OK;
+    if (grid > 0x7FFFFFFF) return fail("grid too large");
+    if constexpr (MODE != MODE_STORE_ROUTE_F32)
+    {
+        if (p.tile_rows == 64)
+        {
+            trellis_gemm_kernel<BITS, MODE, DENSE, 1><<<(unsigned) grid, 256, 0, s>>>(p);
+            return EXL3_OK;
+        }
+    }
+    if constexpr (MODE == MODE_ATOMIC_F32)
+    {
+        if (p.tile_rows > 256) return fail("mode 3 (fp32 atomic rows) takes row tiles of at most 256 rows");
+    }
+    else if (p.tile_rows > 256)
+    {
+        trellis_gemm_kernel<BITS, MODE, DENSE, 4, 8><<<(unsigned) grid, 512, 0, s>>>(p);
+        return EXL3_OK;
+    }
+    trellis_gemm_kernel<BITS, MODE, DENSE><<<(unsigned) grid, 256, 0, s>>>(p);
+    return EXL3_OK;
+}
+
+// One translation unit per trellis width instantiates the kernels (they compile slowly); the entry points dispatch to
+// them here. mode is one of the MODE_* values, dense selects the single-matrix schedule.
+int launch_gemm_b2(int mode, bool dense, const GemmParams& p, hipStream_t s);
+int launch_gemm_b3(int mode, bool dense, const GemmParams& p, hipStream_t s);
+int launch_gemm_b4g(int mode, const GemmParams& p, hipStream_t s);
+int launch_gemm_b4d(int mode, const GemmParams& p, hipStream_t s);
+
+}  // namespace exl3
