@@ -15,8 +15,14 @@
 //   * Everything lives in one caller-provided workspace; buffers that accumulate are cleared by a fill kernel (no
 //     memset nodes), and nothing is read back to the host, so a caller may capture the call in a HIP graph.
 #include <algorithm>
+#include <mutex>
 
 #include "exl3_common.h"
+
+// Scratch of exl3_moe_decode_noalloc: the workspace of a decode call, for callers that cannot allocate. Every GPU
+// the library runs on holds its own copy until the process ends.
+constexpr int64_t DECODE_SCRATCH_BYTES = (int64_t) 32 << 20;
+static __device__ __align__(256) unsigned char scratch[DECODE_SCRATCH_BYTES];
 
 namespace exl3 {
 namespace {
@@ -84,6 +90,32 @@ int k_split_for(int64_t wgs, int stages, int target)
     if (wgs <= 0) return 1;
     const int64_t s = std::max<int64_t>(1, std::min<int64_t>(target / wgs, stages / 2));
     return (int) s;
+}
+
+// This device's address of `scratch`, looked up once per device with that device current. In host code the array's
+// name is not a device address: every host use of the scratch (kernel arguments, fills, copies) takes this pointer.
+int decode_scratch(void** ptr)
+{
+    constexpr int MAX_DEVICES = 64;
+    static std::mutex mu;
+    static void* addr[MAX_DEVICES] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+        return hip_status("moe_decode_noalloc: no current device");
+    std::lock_guard<std::mutex> guard(mu);
+    if (!addr[dev])
+    {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+        {
+            last_error() = std::string("moe_decode_noalloc: hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+            return EXL3_ERR_HIP;
+        }
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    return EXL3_OK;
 }
 
 }  // namespace
@@ -180,4 +212,30 @@ extern "C" int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, co
                                    block_row0, L.max_blocks, DECODE_TILE_ROWS, counts, expert_row0, n_experts,
                                    token_sorted, weight_sorted, nullptr, out, tokens, EXL3_GEMM_SCATTER_F32,
                                    down_split, stream);
+}
+
+extern "C" int exl3_moe_decode_noalloc(const uint16_t* x, int64_t tokens, int hidden, const void* topk_ids,
+                                       int ids_dtype, const void* topk_weights, int weights_dtype, int topk,
+                                       int n_experts, int inter, int bits, const uint16_t* packed_gate,
+                                       const uint16_t* packed_up, int64_t w13_expert_stride_words,
+                                       const uint16_t* suh_gate, int64_t suh13_stride, const uint16_t* svh_gate,
+                                       const uint16_t* svh_up, int64_t svh13_stride, const uint16_t* packed_down,
+                                       int64_t w2_expert_stride_words, const uint16_t* suh_down, int64_t suh2_stride,
+                                       const uint16_t* svh_down, int64_t svh2_stride, float limit, float* out,
+                                       void* stream)
+{
+    EXL3_CHECK(tokens >= 0 && topk > 0, "bad routing shape");
+    const int64_t need = exl3_moe_decode_workspace_bytes(tokens, topk, n_experts, hidden, inter);
+    EXL3_CHECK(need >= 0, "bad decode sizes");
+    EXL3_CHECK(need <= DECODE_SCRATCH_BYTES,
+               "moe_decode_noalloc: this call needs %lld bytes of workspace, more than its fixed scratch of %lld bytes "
+               "(use exl3_moe_decode with a caller workspace)", (long long) need, (long long) DECODE_SCRATCH_BYTES);
+    if (tokens == 0) return EXL3_OK;
+    void* ws = nullptr;
+    const int rc = decode_scratch(&ws);
+    if (rc) return rc;
+    return exl3_moe_decode(x, tokens, hidden, topk_ids, ids_dtype, topk_weights, weights_dtype, topk, n_experts, inter,
+                           bits, packed_gate, packed_up, w13_expert_stride_words, suh_gate, suh13_stride, svh_gate,
+                           svh_up, svh13_stride, packed_down, w2_expert_stride_words, suh_down, suh2_stride, svh_down,
+                           svh2_stride, limit, out, ws, DECODE_SCRATCH_BYTES, stream);
 }

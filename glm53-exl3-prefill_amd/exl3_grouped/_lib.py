@@ -59,9 +59,11 @@ SIGNATURES = {
     "exl3_moe_decode_workspace_bytes": (I64, [I64, I32, I32, I32, I32]),
     "exl3_moe_decode": (I32, [P, I64, I32, P, I32, P, I32, I32, I32, I32, I32, P, P, I64, P, I64, P, P, I64, P, I64,
                               P, I64, P, I64, F32, P, P, I64, P]),
+    "exl3_moe_decode_noalloc": (I32, [P, I64, I32, P, I32, P, I32, I32, I32, I32, I32, P, P, I64, P, I64, P, P, I64,
+                                      P, I64, P, I64, P, I64, F32, P, P]),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lib = None
 _path = None

@@ -316,6 +316,23 @@ int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, const void* t
                     const uint16_t* suh_down, int64_t suh2_stride, const uint16_t* svh_down, int64_t svh2_stride,
                     float limit, float* out, void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * exl3_moe_decode without a workspace argument: the workspace is a fixed 32 MiB scratch array in device memory that
+ * the library holds on every GPU it runs on until the process ends, so the call allocates nothing. No counterpart in
+ * the reference; it is for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Limit: calls whose exl3_moe_decode_workspace_bytes(tokens, topk, n_experts, hidden, inter)
+ * exceeds 32 MiB are rejected with EXL3_ERR_ARG (256 tokens x top-8 at hidden 4096, inter 768 fit). Every call on one
+ * GPU shares that GPU's scratch: calls that overlap on one GPU (concurrent streams or threads) race and must not be
+ * issued. Same arguments, result and graph-capture safety as exl3_moe_decode otherwise.
+ */
+int exl3_moe_decode_noalloc(const uint16_t* x, int64_t tokens, int hidden, const void* topk_ids, int ids_dtype,
+                            const void* topk_weights, int weights_dtype, int topk, int n_experts, int inter, int bits,
+                            const uint16_t* packed_gate, const uint16_t* packed_up, int64_t w13_expert_stride_words,
+                            const uint16_t* suh_gate, int64_t suh13_stride, const uint16_t* svh_gate,
+                            const uint16_t* svh_up, int64_t svh13_stride, const uint16_t* packed_down,
+                            int64_t w2_expert_stride_words, const uint16_t* suh_down, int64_t suh2_stride,
+                            const uint16_t* svh_down, int64_t svh2_stride, float limit, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

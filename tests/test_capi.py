@@ -281,6 +281,21 @@ def test_moe_decode_contract():
     assert rc == _lib.EXL3_OK                            # nothing to do: no pointer is needed
 
 
+def test_moe_decode_noalloc_contract():
+    """The no-allocation decode entry point rejects a call whose workspace would not fit its fixed 32 MiB scratch
+    before touching a GPU, and an empty batch is a no-op."""
+    lib = _lib.load()
+    assert lib.exl3_moe_decode_workspace_bytes(256, 8, 288, 4096, 768) <= 32 << 20
+    assert lib.exl3_moe_decode_workspace_bytes(512, 8, 288, 4096, 768) > 32 << 20
+    args = [FAKE, 512, 4096, FAKE, _lib.DTYPE_I64, FAKE, _lib.DTYPE_F32, 8, 288, 768, 4, FAKE, FAKE, 1, FAKE, 1,
+            FAKE, FAKE, 1, FAKE, 1, FAKE, 1, FAKE, 1, ctypes.c_float(10.0), FAKE, None]
+    rc, msg = rc_and_msg("exl3_moe_decode_noalloc", *args)
+    assert rc == _lib.EXL3_ERR_ARG and "scratch" in msg
+    args[1] = 0
+    rc, msg = rc_and_msg("exl3_moe_decode_noalloc", *args)
+    assert rc == _lib.EXL3_OK
+
+
 def test_shim_moe_decode_messages():
     x = torch.zeros(4, 512, dtype=torch.float16)
     ids = torch.zeros(4, 2, dtype=torch.int64)
