@@ -5,8 +5,8 @@ Installed into vLLM's exl3 overlay module by patch_exl3_grouped.py when EXL3_GRO
 Prefill calls (tokens > the fused kernel's row cap) go through one launch per stage over all experts
 (kernel/exl3_grouped_runtime.py:93-98). Decode calls (tokens <= cap), which the reference leaves to the overlay's
 fused exl3_moe (a CUDA kernel with no build on this GPU), go to moe_decode: the same stages with split-K GEMMs and a
-per-layer workspace, one fixed launch sequence that a HIP graph can capture. Expert-parallel calls (layer.expert_map
-set) and layers without w13_trellis keep the original path untouched.
+per-device workspace sized once for the row cap, one fixed launch sequence that a HIP graph can capture.
+Expert-parallel calls (layer.expert_map set) and layers without w13_trellis keep the original path untouched.
 
 Env:
   EXL3_GROUPED_PREFILL=1     enable (read by the hook)
@@ -194,22 +194,49 @@ def decode_enabled() -> bool:
     return os.environ.get("EXL3_GROUPED_DECODE", "1") != "0"
 
 
+# One decode workspace per device, shared by every MoE layer (layers run one after another on one stream). It is
+# allocated once, by the first decode call on the device (or reserve_decode_workspace), and never replaced: a graph
+# captured later keeps its address, so a later call that would need a larger one raises instead of swapping buffers.
+_decode_ws: dict = {}
+
+
+def _device_index(dev: torch.device) -> int:
+    return dev.index if dev.index is not None else torch.cuda.current_device()
+
+
+def reserve_decode_workspace(device, tokens: int, topk: int, n_experts: int, hidden: int, inter: int) -> torch.Tensor:
+    """Allocate the device's decode workspace for batches of up to `tokens` (the wrapper sizes it for the overlay's
+    row cap on the first decode call; call this before any graph capture to size it explicitly). Returns it; raises if
+    the device already has a smaller one (its address may be captured in a graph)."""
+    gp = _load_ext()
+    dev = torch.device(device)
+    need = gp.moe_decode_workspace_bytes(int(tokens), int(topk), int(n_experts), int(hidden), int(inter))
+    key = _device_index(dev)
+    ws = _decode_ws.get(key)
+    if ws is None:
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+        _decode_ws[key] = ws
+        logger.info("EXL3 decode workspace: %.1f MiB on cuda:%d (%d tokens x top-%d, E=%d, H=%d, I=%d)",
+                    ws.numel() / 2**20, key, tokens, topk, n_experts, hidden, inter)
+    elif ws.numel() < need:
+        raise RuntimeError(f"the decode workspace of cuda:{key} holds {ws.numel()} bytes, this call needs {need} "
+                           f"({tokens} tokens x top-{topk}); it is never reallocated (a captured graph may hold its "
+                           "address): size it for the largest batch with reserve_decode_workspace before first use")
+    return ws
+
+
 def moe_decode(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, layer, limit: float,
-               out: torch.Tensor | None = None) -> torch.Tensor:
+               out: torch.Tensor | None = None, cap: int | None = None) -> torch.Tensor:
     """Decode-path MoE for a small batch: x2d [T, H] (any float dtype), ids [T, topk], weights [T, topk] -> out fp32
-    [T, H]. The workspace lives on the layer (layer._exl3_decode_ws), grown to the largest batch seen and reused, so
-    a call after the first allocates nothing when `out` is given (the first call of each size should run before a
-    graph capture)."""
+    [T, H]. The workspace is the device's shared one (reserve_decode_workspace), sized on the first call for
+    max(T, cap) tokens and never reallocated, so a call allocates nothing when `out` is given (the first call on a
+    device should run before a graph capture)."""
     gp = _load_ext()
     T, H = x2d.shape
     topk = ids.shape[1]
     E = int(layer.w13_trellis.shape[0])
     I = int(layer._exl3_intermediate_local)
-    need = gp.moe_decode_workspace_bytes(T, topk, E, H, I)
-    ws = getattr(layer, "_exl3_decode_ws", None)
-    if ws is None or ws.numel() < need or ws.device != x2d.device:
-        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=x2d.device)
-        layer._exl3_decode_ws = ws
+    ws = reserve_decode_workspace(x2d.device, max(T, int(cap or 0)), topk, E, H, I)
     x16 = x2d if x2d.dtype == torch.float16 and x2d.is_contiguous() else x2d.to(torch.float16).contiguous()
     return gp.moe_decode(x16, ids.contiguous(), weights.contiguous(), layer.w13_trellis, layer.w13_suh,
                          layer.w13_svh, layer.w2_trellis, layer.w2_suh, layer.w2_svh, float(limit), out=out,
@@ -234,7 +261,7 @@ def install(ov):
         ids = topk_ids.reshape(tokens, -1).to(torch.long)
         weights = topk_weights.reshape(tokens, -1)
         if tokens <= cap:
-            out = moe_decode(x2d, ids, weights, layer, float(limit))
+            out = moe_decode(x2d, ids, weights, layer, float(limit), cap=cap)
             layer._exl3_last_apply = "decode"
             return out.to(dtype=x.dtype)
         out = grouped_prefill(x2d, ids, weights, layer, float(limit))

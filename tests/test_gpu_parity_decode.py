@@ -365,6 +365,53 @@ def test_decode_graph_capture_replays(dev):
     assert O.rel_l2(replay.cpu().numpy(), ref) < 1e-3
 
 
+def test_runtime_decode_workspace_survives_larger_calls_after_capture(dev):
+    """The runtime's decode workspace is one per device, sized on the first call for the row cap and never replaced:
+    capture a call at T=8, make an eager call at a larger T <= cap, replay the graph with new inputs, and check that
+    the workspace kept its address and the replay matches an eager call. A call beyond the reserved size raises."""
+    L, cfg = layer_case("layer1k", svh_scale=1 / 64)
+    TL = device_layer("layer1k", svh_scale=1 / 64)
+    cap, T, k, H = 32, 8, cfg["topk"], cfg["H"]
+    rt._decode_ws.clear()                                  # a fresh device workspace for this test
+    sx = torch.empty(T, H, dtype=torch.float16, device=dev)
+    sids = torch.empty(T, k, dtype=torch.int64, device=dev)
+    sw = torch.empty(T, k, dtype=torch.float32, device=dev)
+    sout = torch.empty(T, H, dtype=torch.float32, device=dev)
+
+    def load(seed):
+        x, ids, w = inputs(cfg, T, seed)
+        sx.copy_(dt(x, dev).half())
+        sids.copy_(dt(ids, dev))
+        sw.copy_(dt(w, dev).float())
+        return x, ids, w
+
+    load(1)
+    rt.moe_decode(sx, sids, sw, TL, LIMIT, out=sout, cap=cap)          # first call: sizes the workspace for cap
+    ws_ptr = rt._decode_ws[torch.cuda.current_device()].data_ptr()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rt.moe_decode(sx, sids, sw, TL, LIMIT, out=sout, cap=cap)
+    xb, idsb, wb = inputs(cfg, 24, 9)                                  # eager, larger than the captured batch
+    big = rt.moe_decode(dt(xb, dev).half(), dt(idsb, dev), dt(wb, dev), TL, LIMIT, cap=cap)
+    assert rt._decode_ws[torch.cuda.current_device()].data_ptr() == ws_ptr
+    assert O.rel_l2(big.cpu().numpy(), O.expert_loop(xb, idsb, wb, to_np_layer(L), LIMIT)) < 1e-3
+    for seed in (3, 4):
+        load(seed)
+        g.replay()
+        torch.cuda.synchronize()
+        replay = sout.clone()
+        eager = rt.moe_decode(sx, sids, sw, TL, LIMIT, cap=cap)
+        torch.cuda.synchronize()
+        assert ((replay - eager).norm() / eager.norm()).item() < RERUN_TOL
+    xc, idsc, wc = inputs(cfg, cap + 8, 5)
+    with pytest.raises(RuntimeError, match="never reallocated"):
+        rt.moe_decode(dt(xc, dev).half(), dt(idsc, dev), dt(wc, dev), TL, LIMIT)
+    assert rt._decode_ws[torch.cuda.current_device()].data_ptr() == ws_ptr
+    del g
+    rt._decode_ws.clear()                                  # later tests size their own
+
+
 def test_install_routes_decode_calls(dev, monkeypatch):
     L, cfg = layer_case("tiny")
     TL = device_layer("tiny")
@@ -377,6 +424,7 @@ def test_install_routes_decode_calls(dev, monkeypatch):
             return "original"
 
     rt.install(Ov)
+    rt._decode_ws.clear()                                  # sized by this test's first decode call (cap 64)
     TL._exl3_fused_temps = [torch.zeros(1, 64)]
     x, ids, w = inputs(cfg, 48, 5)
     xb = dt(x, dev).to(torch.bfloat16)

@@ -42,13 +42,13 @@ def test_install_passes_through_decode_ep_and_non_trellis_layers(monkeypatch):
     layer.expert_map = None
     decoded = []
 
-    def fake_decode(x2d, ids2d, w2d, lay, limit, out=None):
-        decoded.append((tuple(x2d.shape), ids2d.dtype, limit))
+    def fake_decode(x2d, ids2d, w2d, lay, limit, out=None, cap=None):
+        decoded.append((tuple(x2d.shape), ids2d.dtype, limit, cap))
         return torch.ones(x2d.shape, dtype=torch.float32)
 
     monkeypatch.setattr(rt, "moe_decode", fake_decode)
     got = ov.apply_exl3_experts(x, ids.to(torch.int32), w, layer, limit=7.0, fused="f")
-    assert got.dtype == torch.float16 and decoded == [((64, 512), torch.int64, 7.0)]
+    assert got.dtype == torch.float16 and decoded == [((64, 512), torch.int64, 7.0, 128)]   # sized for the cap
     assert layer._exl3_last_apply == "decode" and not calls
     monkeypatch.setenv("EXL3_GROUPED_DECODE", "0")
     assert ov.apply_exl3_experts(x, ids, w, layer, limit=7.0, fused="f") == "original"
