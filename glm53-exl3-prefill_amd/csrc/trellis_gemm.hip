@@ -254,6 +254,35 @@ int dense_tile_rows(int64_t m, int size_k)
     return 512;
 }
 
+// The fat GEMM's `variant` (the reference's four smem/pipeline variants, kernel/exl3_fat_gemm_v2.cu:285-295) selects
+// the row-tile schedule here: 1 (the reference's production variant, K64 / 2 stages) the shape-tuned policy above,
+// 0 64-row tiles on the thin kernel, 2 256-row tiles on the 4-wave kernel, 3 512-row tiles on the 8-wave kernel. A
+// long-K store that would leave CUs idle runs as two K slices under every variant (dense_split_pays), so all four give
+// bit-identical results: each row's sum over K runs in the same order whatever the tile height.
+int variant_tile_rows(int variant, int64_t m, int size_k)
+{
+    switch (variant)
+    {
+        case 0: return 64;
+        case 2: return 256;
+        case 3: return 512;
+        default: return dense_tile_rows(m, size_k);
+    }
+}
+
+// LDS bytes per workgroup of the kernels a variant can launch (the largest: the scatter form stages output rows).
+int64_t variant_lds_bytes(int variant)
+{
+    const int64_t four = std::max<int64_t>(LDS_MAIN_BYTES, lds_scatter_bytes<4>());   // 64- and 256-row kernels
+    const int64_t eight = std::max<int64_t>(LDS_MAIN_BYTES, lds_scatter_bytes<8>());  // 512-row kernel
+    switch (variant)
+    {
+        case 0: case 2: return four;
+        case 1: case 3: return eight;          // variant 1 picks 64- or 512-row tiles by shape
+        default: return -1;
+    }
+}
+
 __global__ __launch_bounds__(256)
 void zero_f32x4_kernel(float4* __restrict__ p, int64_t n4)
 {
@@ -272,10 +301,12 @@ bool dense_split_pays(int64_t m, int n_slots, int size_k)
 }
 
 template <int MODE>
-int launch_dense_split2(GemmParams p, int bits, float* out, int64_t out_floats, hipStream_t s)
+int launch_dense_split2(GemmParams p, int bits, float* out, int64_t out_floats, hipStream_t s, int variant = 1)
 {
     const int total_kb = p.size_k / TILE_K;
-    p.tile_rows = p.m <= 1024 ? 64 : 256;                       // thin tiles here too, up to 1024 rows (measured)
+    // thin tiles here too, up to 1024 rows (measured); a fixed-schedule variant keeps its tiles (at most 256 rows:
+    // the slices add with the 4-wave kernels)
+    p.tile_rows = variant == 1 ? (p.m <= 1024 ? 64 : 256) : std::min(p.tile_rows, 256);
     p.n_groups = (int) ((p.m + p.tile_rows - 1) / p.tile_rows);
     p.kb_per_split = ((total_kb + 1) / 2 + 1) / 2 * 2;        // even: both slices have an even number of stages
     p.k_split = (total_kb + p.kb_per_split - 1) / p.kb_per_split;
@@ -299,11 +330,12 @@ extern "C" int exl3_fat_gemm(const uint16_t* a, int64_t m, int size_k, const uin
     EXL3_CHECK(out_rows == m, "out shape must be [M, N]");
     GemmParams p{};
     p.a = a; p.a_rows = m; p.size_k = size_k; p.packed0 = packed; p.tiles_n = tiles_n;
-    p.svh0 = svh; p.tile_rows = dense_tile_rows(m, size_k); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
+    p.svh0 = svh; p.tile_rows = variant_tile_rows(variant, m, size_k);
+    p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
     p.n_tiles_each = (int) (svh_len / TILE_N);
     p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = svh_len;
     rc = dense_split_pays(m, p.n_slots, size_k)
-             ? launch_dense_split2<MODE_ATOMIC_F32>(p, bits, out, m * svh_len, as_stream(stream))
+             ? launch_dense_split2<MODE_ATOMIC_F32>(p, bits, out, m * svh_len, as_stream(stream), variant)
              : launch_bits<MODE_STORE_F32, true>(bits, p, as_stream(stream));
     if (rc) return rc;
     return hip_status("fat_gemm_v2");
@@ -320,7 +352,8 @@ extern "C" int exl3_fat_gemm_scatter(const uint16_t* a, int64_t m, int size_k, c
     EXL3_CHECK(out_rows >= 0, "bad out rows");
     GemmParams p{};
     p.a = a; p.a_rows = m; p.size_k = size_k; p.packed0 = packed; p.tiles_n = tiles_n;
-    p.svh0 = svh; p.tile_rows = dense_tile_rows(m, size_k); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
+    p.svh0 = svh; p.tile_rows = variant_tile_rows(variant, m, size_k);
+    p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
     p.n_tiles_each = (int) (svh_len / TILE_N);
     p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = svh_len;
     p.token = token_idx; p.route_weight = route_weight;
@@ -385,7 +418,7 @@ extern "C" int exl3_combine_routes(const float* partial, float* out, const void*
 extern "C" int64_t exl3_smem_bytes(int64_t variant)
 {
     if (variant < 0 || variant > 3) return -1;
-    return (int64_t) (lds_scatter_bytes<8>() > LDS_MAIN_BYTES ? lds_scatter_bytes<8>() : LDS_MAIN_BYTES);
+    return variant_lds_bytes((int) variant);
 }
 
 extern "C" int exl3_reconstruct(uint16_t* out, const uint16_t* packed, int tiles_k, int tiles_n, int bits, int mcg,

@@ -363,7 +363,8 @@ def _fat_check(a, packed, out, svh, K, mcg, mul1):
 
 def fat_gemm_v2(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, svh: torch.Tensor, K: int, mcg: bool,
                 mul1: bool, variant: int = 1) -> None:
-    """kernel/exl3_fat_gemm_v2.cu:298-303: out[M, N] = H128(a @ W') / sqrt(128) * svh (fp32)."""
+    """kernel/exl3_fat_gemm_v2.cu:298-303: out[M, N] = H128(a @ W') / sqrt(128) * svh (fp32). variant: the row-tile
+    schedule (see smem_bytes); every variant gives bit-identical results."""
     _fat_check(a, packed, out, svh, K, mcg, mul1)
     _check(out.size(0) == a.size(0) and out.size(1) == svh.numel(), "out shape must be [M, N]")
     _check(0 <= int(variant) <= 3, "unknown variant")
@@ -390,6 +391,20 @@ def fat_gemm_v2_scatter(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor
         _lib.call("exl3_fat_gemm_scatter", _p(a), a.size(0), a.size(1), _p(packed), packed.size(0), packed.size(1),
                   packed.size(2), _p(out), out.size(0), _p(svh), svh.numel(), _p(token_idx), _p(route_weight),
                   int(K), int(bool(mcg)), int(bool(mul1)), int(variant), s)
+
+
+def exl3_fat_gemm(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, svh: torch.Tensor, K: int, mcg: bool,
+                  mul1: bool) -> None:
+    """PR77's per-expert op with its argument order, ext.exl3_fat_gemm(a, packed, out, svh, K, mcg, mul1)
+    (kernel/test_fat_v2.py:122): fat_gemm_v2 with the shape-tuned schedule (variant 1)."""
+    fat_gemm_v2(a, packed, out, svh, K, mcg, mul1, 1)
+
+
+def exl3_fat_gemm_scatter(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, svh: torch.Tensor,
+                          tok: torch.Tensor, rw: torch.Tensor, K: int, mcg: bool, mul1: bool) -> None:
+    """PR77's scatter op with its argument order, ext.exl3_fat_gemm_scatter(a, packed, out, svh, tok, rw, K, mcg,
+    mul1) (kernel/test_fat_v2.py:134): fat_gemm_v2_scatter with the shape-tuned schedule (variant 1)."""
+    fat_gemm_v2_scatter(a, packed, out, svh, tok, rw, K, mcg, mul1, 1)
 
 
 def linear_workspace_bytes(m: int, k: int) -> int:
@@ -532,7 +547,9 @@ def moe_decode(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tens
 
 
 def smem_bytes(variant: int) -> int:
-    """kernel/exl3_fat_gemm_v2.cu:316-326: LDS bytes per workgroup of `variant`, -1 if unknown."""
+    """kernel/exl3_fat_gemm_v2.cu:316-326: LDS bytes per workgroup of the kernels `variant` launches (the largest of
+    them: the scatter form stages output rows), -1 if unknown. Variants select the row-tile schedule: 0 64-row tiles,
+    1 the shape-tuned policy (64- or 512-row tiles), 2 256-row tiles, 3 512-row tiles."""
     return int(_lib.load().exl3_smem_bytes(int(variant)))
 
 

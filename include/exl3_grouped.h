@@ -6,6 +6,10 @@
  * hipStream_t (NULL = the default stream); work is enqueued there with no host synchronisation. Work runs on
  * the calling thread's current HIP device.
  *
+ * Accumulating outputs (grouped GEMM modes 1 and 3, the fat GEMM scatter and its long-K store, the decode op's out)
+ * are updated with hardware fp32 atomics (built with -munsafe-fp-atomics): they must be ordinary coarse-grained device
+ * allocations (hipMalloc, torch CUDA tensors), not fine-grained or host-coherent memory, where such atomics can be lost.
+ *
  * Every entry point validates its arguments before touching the GPU and returns
  *   EXL3_OK (0), EXL3_ERR_ARG (1: bad argument, nothing launched) or EXL3_ERR_HIP (2: launch failed);
  * the message for the last non-zero status of the calling thread is exl3_last_error().
@@ -235,11 +239,13 @@ int exl3_combine_routes(const float* partial, float* out, const void* topk_ids, 
  *   store:   out[m, n]  = H128_n(a @ W') / sqrt(128) * svh          (out [m, n])
  *   scatter: out[token_idx[i], :] += fp32(route_weight[i]) * (same)  (out [out_rows, n], device atomics)
  * bits must be 2, 3 or 4 with mcg != 0 and mul1 == 0 (the reference accepts only bits 4: "only K4 MCG tensors");
- * size_k % 64 == 0, n % 128 == 0. variant in [0, 3] selects a tile schedule (the reference's four
- * smem/pipeline variants); exl3_smem_bytes(variant) returns its LDS bytes per workgroup, or -1 if unknown.
- * Every variant gives bit-identical results. A store with size_k >= 2048 that would leave CUs idle first zeroes out and
- * then adds two K halves into it with fp32 atomics (exact: two additions onto zero commute), so out must not overlap
- * a, packed or svh.
+ * size_k % 64 == 0, n % 128 == 0. variant in [0, 3] (the reference's four smem/pipeline variants) selects the row-tile
+ * schedule: 0 = 64-row tiles (thin kernel), 1 = the shape-tuned policy (64- or 512-row tiles; the reference's
+ * production variant), 2 = 256-row tiles, 3 = 512-row tiles (8-wave kernel). exl3_smem_bytes(variant) returns the LDS
+ * bytes per workgroup of the kernels that variant launches (the largest, the scatter form's: 33792 for 0 and 2, 67584
+ * for 1 and 3), or -1 if unknown. Every variant gives bit-identical results. A store with size_k >= 2048 that would
+ * leave CUs idle first zeroes out and then adds two K halves into it with fp32 atomics (exact: two additions onto zero
+ * commute), so out must not overlap a, packed or svh.
  */
 int exl3_fat_gemm(const uint16_t* a, int64_t m, int size_k, const uint16_t* packed, int tiles_k, int tiles_n,
                   int packed_words, float* out, int64_t out_rows, const uint16_t* svh, int64_t svh_len,

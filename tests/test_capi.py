@@ -108,7 +108,12 @@ def test_fat_gemm_contract():
     assert "16*K" in call(words=48)[1]
     assert "unknown variant" in call(variant=4)[1]
     assert "out shape" in call(out_rows=299)[1]
-    assert _lib.load().exl3_smem_bytes(9) == -1 and _lib.load().exl3_smem_bytes(0) > 0
+    lib = _lib.load()
+    # per-variant LDS of the kernels each schedule launches: 4-wave kernels (64/256-row tiles) stage 4 waves x 16 rows
+    # x 132 floats for the scatter, the 8-wave kernel (512-row tiles, also picked by variant 1) 8 waves' worth
+    assert [lib.exl3_smem_bytes(v) for v in range(4)] == [4 * 16 * 132 * 4, 8 * 16 * 132 * 4,
+                                                          4 * 16 * 132 * 4, 8 * 16 * 132 * 4]
+    assert lib.exl3_smem_bytes(9) == -1 and lib.exl3_smem_bytes(-1) == -1
 
 
 def test_sort_routes_contract():
@@ -153,6 +158,17 @@ def test_shim_fat_gemm_messages():
     with pytest.raises(RuntimeError, match="tensors must be CUDA"):
         gp.fat_gemm_v2(a, pk, out, svh, 4, True, False, 1)
     assert gp.smem_bytes(5) == -1
+    # PR77's names and argument order (kernel/test_fat_v2.py:122,134), same checks before the device
+    with pytest.raises(RuntimeError, match="only K2/K3/K4 MCG tensors"):
+        gp.exl3_fat_gemm(a, pk, out, svh, 4, False, False)
+    with pytest.raises(RuntimeError, match="tensors must be CUDA"):
+        gp.exl3_fat_gemm(a, pk, out, svh, 4, True, False)
+    tok = torch.zeros(300, dtype=torch.int64)
+    rw = torch.zeros(300, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="routing dtypes"):
+        gp.exl3_fat_gemm_scatter(a, pk, out, svh, tok, rw.float(), 4, True, False)
+    with pytest.raises(RuntimeError, match="tensors must be CUDA"):
+        gp.exl3_fat_gemm_scatter(a, pk, out, svh, tok, rw, 4, True, False)
 
 
 def test_shim_grouped_gemm_messages():
