@@ -6,10 +6,16 @@ H=4096, I=768, 4 bpw trellis, an 8192-token chunk, top-8 routing skewed by a Zip
 inputs resident in HBM before timing starts. A step is one full grouped_prefill call (route sort, block table,
 gather + input Hadamard, gate|up GEMM, SwiGLU + down Hadamard, down GEMM with fp32 atomic scatter).
 
-Prints ONE JSON line: value = routed tokens/s (T*topk / step time); ms_per_step = per-layer MoE ms; roofline of the
-dominant stage (the gate|up grouped GEMM: full expert tiles on the main kernel, each expert's last tile of <= 64 rows on
-the thin kernel; MFMA-bound: algorithmic 4*R*H*I flop per stage call over its event-timed average duration on the
-launch stream); cpu_baseline = the CPU oracle's expert loop on a bounded sample.
+Prints ONE JSON line: value = routed tokens/s (T*topk / step time); ms_per_step = per-layer MoE ms; stage_ms = the
+median over the timed steps of each stage's HIP-event time on the launch stream (stage_ms_mean beside it); roofline of
+the dominant stage (the gate|up grouped GEMM: full expert tiles on the main kernel, each expert's last tile of <= 64
+rows on the thin kernel; MFMA-bound: algorithmic 4*R*H*I flop per stage call over its median duration) and
+roofline_down for the down GEMM + scatter (2*R*H*I flop). From the committed rocprofv3 summaries of the same workload
+(profiles/grouped_prefill_headline_*.md): traffic (calibrated FETCH_SIZE + WRITE_SIZE bytes per stage call),
+stage_hbm_gbs (those bytes over this run's stage time) and counters (matrix-pipe and VALU busy fractions from
+SQ_VALU_MFMA_BUSY_CYCLES / SQ_ACTIVE_INST_VALU over GRBM_GUI_ACTIVE). cpu_baseline = a PyTorch CPU expert loop (the
+reference's prototype loop: dequantised fp16 weights, per-expert matmuls, index_add_ scatter) on a bounded sample of
+the active experts, dequant and loop timed apart and extrapolated to the layer.
 
   python bench.py [--steps K] [--warmup W] [--tokens T] [--bits B] [--routing R] [--no-cpu-baseline]
   python bench.py --sweep          (extra lines for T = 1024, 2048, 4096, 8192; not the driver's contract line)
@@ -34,10 +40,18 @@ MFMA_F16_PEAK_TFLOPS = 2500.0      # MI355X dense fp16 (no sparsity)
 # I=1024 per rank, routing_skewed(hot=12, share=0.55), real checkpoint layer 3): reference README.md:41-44.
 REFERENCE_GB10_MS = {1024: 11.4, 2048: 13.7, 4096: 20.2, 8192: 33.2}
 HBM_PEAK_GBS = 8000.0
-# the dominant stage's kernels as rocprofv3 reports them (keys of the committed traffic summary): the gate|up GEMM
-# runs full expert tiles on the main kernel and each expert's last tile of <= 64 rows on the thin one
-GATE_UP_KERNELS = ("trellis_gemm_kernel<{bits}, 0, false, 4, 4>(GemmParams)",
-                   "trellis_gemm_kernel<{bits}, 0, false, 1, 4>(GemmParams)")
+# The kernels of each stage of grouped_prefill as rocprofv3 names them (namespaces and parameter lists stripped; the keys
+# of the committed profile summaries): the GEMMs run full expert tiles on the main kernel and each expert's last tile
+# of <= 64 rows on the thin one.
+STAGE_KERNELS = {
+    "sort_routes": ("sort_hist_kernel", "sort_offsets_kernel", "sort_scatter_kernel"),
+    "build_blocks": ("build_tiles_split_kernel",),
+    "row_had": ("row_had_t16_kernel<true>",),
+    "gemm_gate_up": ("trellis_gemm_kernel<{bits}, 0, false, 4, 4>", "trellis_gemm_kernel<{bits}, 0, false, 1, 4>"),
+    "act_had": ("act_had_t16_kernel<false, true>",),
+    "gemm_down_scatter": ("trellis_gemm_kernel<{bits}, 1, false, 4, 4>", "trellis_gemm_kernel<{bits}, 1, false, 1, 4>"),
+}
+GATE_UP_KERNELS = STAGE_KERNELS["gemm_gate_up"]
 
 
 def parse():
@@ -79,17 +93,40 @@ def copy_probe(mib: int):
     print(json.dumps({"copy_probe_bytes_per_launch": n * 4, "launches": 5}), flush=True)
 
 
+def profile_json(name: str):
+    """The fenced JSON block of a committed profile summary (profiles/<name>.md), or None if it is missing."""
+    try:
+        text = open(os.path.join(ROOT, "profiles", f"{name}.md")).read()
+        return json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+    except (OSError, IndexError, ValueError):
+        return None
+
+
 def traffic_from_profiles(workload: str, kernels):
     """HBM bytes per call of the stage made of `kernels` (one launch each) from the committed rocprofv3 --pmc summary
     of `workload` (profiles/grouped_prefill_<workload>_traffic.md: FETCH_SIZE and WRITE_SIZE passes scaled by a
     copy-kernel calibration, in its fenced JSON block), or None if the summary or one of the kernels is missing."""
-    path = os.path.join(ROOT, "profiles", f"grouped_prefill_{workload}_traffic.md")
+    j = profile_json(f"grouped_prefill_{workload}_traffic")
     try:
-        text = open(path).read()
-        block = text.split("```json", 1)[1].split("```", 1)[0]
-        per = json.loads(block)["bytes_per_launch"]
+        per = j["bytes_per_launch"]
         return sum(per[k] for k in kernels)
-    except (OSError, IndexError, ValueError, KeyError):
+    except (TypeError, KeyError):
+        return None
+
+
+def mfma_busy_from_profiles(workload: str, kernels):
+    """Matrix-pipe busy fraction of a stage's launches from the committed SQ counter summary: sum of
+    SQ_VALU_MFMA_BUSY_CYCLES over the launches / (their GRBM_GUI_ACTIVE cycles per XCD x SIMDs), and the shader clock
+    the same counters imply; None if missing."""
+    j = profile_json(f"grouped_prefill_{workload}_sq_counters")
+    try:
+        ks = [j["kernels"][k] for k in kernels]
+        busy = sum(k["SQ_VALU_MFMA_BUSY_CYCLES"] for k in ks)
+        cycles = sum(k["GRBM_GUI_ACTIVE"] / j["xcds"] for k in ks)
+        return {"mfma_busy": round(busy / (cycles * j["simds"]), 4),
+                "valu_busy": round(sum(k["SQ_ACTIVE_INST_VALU"] for k in ks) * 4 / (cycles * j["simds"]), 4),
+                "clock_mhz": j.get("clock_mhz", {}).get(kernels[0])}
+    except (TypeError, KeyError, ZeroDivisionError):
         return None
 
 
@@ -122,7 +159,7 @@ def run(args, T=None, emit=True):
     t0 = time.perf_counter()
     for _ in range(args.steps):
         ev = []
-        rt.grouped_prefill(xt, it, wt, TL, limit, stage_events=ev, scatter=scatter)
+        out = rt.grouped_prefill(xt, it, wt, TL, limit, stage_events=ev, scatter=scatter)
         events.append(ev)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -132,7 +169,10 @@ def run(args, T=None, emit=True):
     for ev in events:
         for (name, e1), (_, e0) in zip(ev[1:], ev[:-1]):
             stage_ms.setdefault(name, []).append(e0.elapsed_time(e1))
-    stage_avg = {n: statistics.mean(v) for n, v in stage_ms.items()}
+    # per-stage medians: the device has been seen to pause for ~30 ms about once in 20-40 s of work (one step of one
+    # stage); a mean over 20 steps then misreports that stage several-fold. The means are reported beside them.
+    stage_avg = {n: statistics.median(v) for n, v in stage_ms.items()}
+    stage_mean = {n: statistics.mean(v) for n, v in stage_ms.items()}
     gemm_ms = stage_avg["gemm_gate_up"]
     gate_up_flop = 4.0 * R * H * I
     down_flop = 2.0 * R * H * I
@@ -147,7 +187,14 @@ def run(args, T=None, emit=True):
                           "layer_tflops": round(layer_tflops, 1)}), file=sys.stderr, flush=True)
     workload = f"{cfg_name}: E={E} H={H} I={I} {bits}bpw T={T_} top{k} {cfg['routing']}"
     thin = rt.thin_tiles_enabled() and scatter == "atomic"
-    gate_up_kernels = [kname.format(bits=bits) for kname in (GATE_UP_KERNELS if thin else GATE_UP_KERNELS[:1])]
+    kernels_of = {st: [kn.format(bits=bits) for kn in (ks if thin or not st.startswith("gemm") else ks[:1])]
+                  for st, ks in STAGE_KERNELS.items()}
+    gate_up_kernels = kernels_of["gemm_gate_up"]
+    down_kernels = kernels_of["gemm_down_scatter"]
+    down_achieved = down_flop / (down_ms * 1e-3) / 1e12
+    stage_bytes = {st: traffic_from_profiles(cfg_name, ks) for st, ks in kernels_of.items()}
+    stage_gbs = {st: (round(b / (stage_avg[st] * 1e-3) / 1e9, 1) if b and st in stage_avg else None)
+                 for st, b in stage_bytes.items()}
     result = {
         "metric": "per-layer MoE ms + routed tok/s, 288 experts @8192 tok; % MFMA peak",
         "value": round(R / (ms_per_step * 1e-3), 1),
@@ -167,6 +214,15 @@ def run(args, T=None, emit=True):
                    "tile_rows": rt.tile_rows()},
         "tokens_per_s": round(T_ / (ms_per_step * 1e-3), 1),
         "stage_ms": {n: round(v, 4) for n, v in stage_avg.items()},
+        "stage_ms_mean": {n: round(v, 4) for n, v in stage_mean.items()},
+        # HBM bytes per stage call from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload
+        # (calibrated against a copy kernel) over this run's stage time, against the 8 TB/s peak
+        "stage_hbm_gbs": stage_gbs,
+        "stage_hbm_frac": {st: (round(v / HBM_PEAK_GBS, 4) if v else None) for st, v in stage_gbs.items()},
+        # matrix-pipe and VALU busy fractions of the GEMM stages from the committed SQ counter summary (against the
+        # clock the counters measured, not the datasheet's)
+        "counters": {"gemm_gate_up": mfma_busy_from_profiles(cfg_name, gate_up_kernels),
+                     "gemm_down_scatter": mfma_busy_from_profiles(cfg_name, down_kernels)},
         "gemm_tflops_gate_up_and_down": round(both_gemm_tflops, 1),
         "mfma_frac_layer": round(layer_tflops / MFMA_F16_PEAK_TFLOPS, 4),
         "roofline": {"kernel": "grouped_gemm gate|up stage (" + " + ".join(gate_up_kernels) + ")", "bound": "mfma",
@@ -175,9 +231,14 @@ def run(args, T=None, emit=True):
                      "traffic": traffic_from_profiles(cfg_name, gate_up_kernels),
                      "work_per_launch": f"4*R*H*I = {gate_up_flop:.4g} flop (R={R} routed rows) per stage call",
                      "peak_source": "MI355X dense fp16 MFMA, AMD datasheet (256 CUs x 2.4 GHz x 4096 flop/clk)"},
+        "roofline_down": {"kernel": "grouped_gemm down + fp32 atomic scatter stage (" + " + ".join(down_kernels) + ")",
+                          "bound": "mfma", "achieved": round(down_achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(down_achieved / MFMA_F16_PEAK_TFLOPS, 4),
+                          "traffic": stage_bytes["gemm_down_scatter"],
+                          "work_per_launch": f"2*R*H*I = {down_flop:.4g} flop per stage call"},
         "device": device_info(),
     }
-    return result, (L, x, ids, w, cfg)
+    return result, (L, x, ids, w, cfg), out
 
 
 def device_info():
@@ -200,42 +261,89 @@ def device_info():
             "peak_clock_mhz": clock_mhz}
 
 
-def cpu_baseline(inputs, seconds: float):
-    """The oracle's expert loop (numpy/BLAS on the host cores) on a bounded sample of the same workload: whole
-    experts in decreasing-size order until about `seconds` of CPU work; rate = routed rows per second."""
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(inputs, seconds: float, gpu_out=None):
+    """The reference's expert loop as a PyTorch CPU loop (harness/proto_fp8.py:123-134, weights per :66-76 in the
+    real domain W = diag(suh) H128 W' H128 diag(svh), W' from the CPU trellis decode): per expert gather the routed
+    rows, gate = fp16(h W_g), up = fp16(h W_u), act = fp16(silu(min(gate, L)) clamp(up, -L, L)), down = act W_d,
+    out.index_add_(token, down * fp16(w)); fp32 arithmetic. A bounded sample (experts largest first, about `seconds`
+    of CPU work) extrapolated to the layer: dequant time per expert x active experts + loop time per routed row x
+    routed rows. Also the GPU output's rel L2 against the loop on the tokens whose routes all fall in the sample."""
     import numpy as np
+    import torch
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import exl3_oracle as O
 
     L, x, ids, w, cfg = inputs
-    layer = O.Layer(L.w13_trellis, L.w13_suh, L.w13_svh, L.w2_trellis, L.w2_suh, L.w2_svh)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    limit = 10.0
+    H128 = torch.from_numpy(O.sylvester(128).astype(np.float32)) / np.sqrt(128.0)
+
+    def full_weight(trellis, suh, svh):
+        wp = torch.from_numpy(O.reconstruct(trellis).astype(np.float32))                # W' [K, N]
+        K, N = wp.shape
+        wr = (H128 @ wp.view(-1, 128, N)).view(K, N) * torch.from_numpy(suh.astype(np.float32))[:, None]
+        wr = (wr.view(K, -1, 128) @ H128).view(K, N) * torch.from_numpy(svh.astype(np.float32))[None, :]
+        return wr
+
+    x16 = torch.from_numpy(np.asarray(x)).to(torch.float16).float()
+    ids_t = torch.from_numpy(ids)
+    w16 = torch.from_numpy(np.asarray(w, dtype=np.float32)).to(torch.float16).float()
+    out = torch.zeros(x16.shape[0], cfg["H"], dtype=torch.float32)
     counts = np.bincount(ids.ravel(), minlength=cfg["E"])
     order = [int(e) for e in np.argsort(-counts, kind="stable") if counts[e] > 0]
-    cache = O.WeightCache(layer)
     t_deq = t_loop = 0.0
     rows = 0
     used = []
     for e in order:
         t0 = time.perf_counter()
-        for which in ("gate", "up", "down"):
-            cache.get(e, which)
+        wg = full_weight(L.w13_trellis[e, 0], L.w13_suh[e, 0], L.w13_svh[e, 0])
+        wu = full_weight(L.w13_trellis[e, 1], L.w13_suh[e, 1], L.w13_svh[e, 1])
+        wd = full_weight(L.w2_trellis[e], L.w2_suh[e], L.w2_svh[e])
         t1 = time.perf_counter()
-        O.expert_loop(x, ids, w, layer, 10.0, cache=cache, experts=[e])
+        tok, kpos = (ids_t == e).nonzero(as_tuple=True)
+        h = x16.index_select(0, tok)
+        gate = (h @ wg).half().float()
+        up = (h @ wu).half().float()
+        act = (torch.nn.functional.silu(gate.clamp(max=limit)) * up.clamp(min=-limit, max=limit)).half().float()
+        down = act @ wd
+        out.index_add_(0, tok, down * w16[tok, kpos].unsqueeze(-1))
         t2 = time.perf_counter()
         t_deq += t1 - t0
         t_loop += t2 - t1
         rows += int(counts[e])
         used.append(e)
-        cache._c.clear()
         if t_deq + t_loop >= seconds:
             break
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    total = t_deq + t_loop
-    return {"value": round(rows / total, 1), "unit": "routed tok/s", "cores": threads, "kind": "port",
-            "sample": f"{len(used)} of {int((counts > 0).sum())} active experts (largest first), {rows} of "
-                      f"{int(counts.sum())} routed rows; dequant {t_deq:.2f}s + expert loop {t_loop:.2f}s; "
-                      f"host {os.cpu_count()} cpus visible",
-            "ms_per_layer_extrapolated": round(total / rows * counts.sum() * 1e3, 1)}
+    n_active = int((counts > 0).sum())
+    R = int(counts.sum())
+    layer_s = t_deq / len(used) * n_active + t_loop / rows * R
+    res = {"value": round(rows / (t_deq + t_loop), 1), "unit": "routed tok/s", "cores": threads, "kind": "port",
+           "cpu_model": cpu_model(),
+           "sample": f"PyTorch CPU expert loop on {len(used)} of {n_active} active experts (largest first), {rows} of "
+                     f"{R} routed rows, one run: dequant {t_deq:.2f} s + loop {t_loop:.2f} s; host {os.cpu_count()} "
+                     "cpus visible",
+           "dequant_s_per_expert": round(t_deq / len(used), 4), "loop_us_per_routed_row": round(t_loop / rows * 1e6, 2),
+           "ms_per_layer_extrapolated": round(layer_s * 1e3, 1),
+           "routed_tok_s_extrapolated": round(R / layer_s, 1)}
+    if gpu_out is not None:
+        covered = np.isin(ids, np.array(used)).all(axis=1)
+        if covered.any():
+            g = gpu_out[covered]
+            c = out.numpy()[covered]
+            res["gpu_rel_l2_vs_cpu_loop"] = float(np.linalg.norm(g - c) / max(np.linalg.norm(c), 1e-30))
+            res["gpu_rel_l2_tokens"] = int(covered.sum())
+    return res
 
 
 # The reference's published per-call ms of its per-expert fat GEMM on GB10 (variant K64/2-stage): gate|up
@@ -370,13 +478,13 @@ def main():
         for T in (1024, 2048, 4096, 8192):
             torch.cuda.synchronize()
             torch.cuda.empty_cache()        # each size starts from a fresh allocator pool, as in its own process
-            r, _ = run(args, T=T, emit=False)
+            r, _, _ = run(args, T=T, emit=False)
             r.pop("cpu_baseline", None)
             print(json.dumps(r), flush=True)
         return
-    result, inputs = run(args)
+    result, inputs, out = run(args)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(inputs, args.cpu_sample_seconds)
+        result["cpu_baseline"] = cpu_baseline(inputs, args.cpu_sample_seconds, gpu_out=out.cpu().numpy())
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

@@ -15,6 +15,7 @@ Env:
                              rows runs on the thin kernel, four workgroups per CU, in a second launch; atomic scatter)
   EXL3_GROUPED_SCATTER=...   down-projection output: "atomic" (fp32 atomic scatter by token, the reference's
                              method) or "combine" (per-route fp32 rows + a fixed-order sum per token: deterministic)
+  EXL3_GROUPED_WORKSPACE=0   allocate the prefill intermediates per call (default: one reused buffer per device)
   EXL3_GROUPED_LIB=<path>    prebuilt libexl3_grouped.so (default: exl3_grouped/libexl3_grouped.so beside this file)
 """
 import logging
@@ -77,6 +78,54 @@ def thin_tiles_enabled() -> bool:
 
 THIN_ROWS = 64
 
+# The prefill intermediates (sorted routes, tile tables, h13, gu, act: ~0.85 GB at 8192 tokens) live in one buffer per
+# device, reused by every call and grown (never shrunk) when a call needs more: steady-state calls allocate nothing but
+# their output, and the kernels keep working on memory they have touched before. Calls on one device must be ordered on
+# one stream (the model runner's); EXL3_GROUPED_WORKSPACE=0 allocates per call instead.
+_prefill_ws: dict = {}
+
+
+def _device_index(dev: torch.device) -> int:
+    return dev.index if dev.index is not None else torch.cuda.current_device()
+
+
+def workspace_enabled() -> bool:
+    return os.environ.get("EXL3_GROUPED_WORKSPACE", "1") != "0"
+
+
+class _Carve:
+    """Tensors carved out of one byte buffer at 256-byte boundaries (a first pass with buf=None only sizes them)."""
+
+    def __init__(self, buf=None, dev=None):
+        self.buf, self.dev, self.off = buf, dev, 0
+
+    def __call__(self, shape, dtype):
+        n = 1
+        for d in shape:
+            n *= int(d)
+        nbytes = n * torch.empty((), dtype=dtype).element_size()
+        start = (self.off + 255) // 256 * 256
+        self.off = start + nbytes
+        if self.buf is None:
+            return torch.empty(shape, dtype=dtype, device=self.dev) if self.dev is not None else None
+        return self.buf[start:start + nbytes].view(dtype).view(shape)
+
+
+def _prefill_buffers(dev, plan):
+    """plan(take) requests every intermediate via take(shape, dtype) and returns them; served from the device's prefill
+    workspace (grown to fit) or, with the workspace off, from the allocator."""
+    if not workspace_enabled():
+        return plan(_Carve(None, dev))
+    sizing = _Carve()
+    plan(sizing)
+    key = _device_index(dev)
+    ws = _prefill_ws.get(key)
+    if ws is None or ws.numel() < sizing.off:
+        _prefill_ws.pop(key, None)
+        ws = torch.empty(max(sizing.off, 256), dtype=torch.uint8, device=dev)
+        _prefill_ws[key] = ws
+    return plan(_Carve(ws))
+
 
 def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, layer, limit: float,
                     stage_events: list | None = None, scatter: str | None = None,
@@ -107,43 +156,49 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     x16 = x2d.to(torch.float16).contiguous()
     ids = ids.contiguous()
     weights = weights.contiguous()
-    token_sorted = torch.empty(R, dtype=torch.int64, device=dev)
-    weight_sorted = torch.empty(R, dtype=torch.float16, device=dev)
-    expert_of_row = torch.empty(R, dtype=torch.int32, device=dev)
-    counts = torch.empty(E, dtype=torch.int32, device=dev)
-    expert_row0 = torch.empty(E, dtype=torch.int32, device=dev)
-    route_index = torch.empty(R, dtype=torch.int32, device=dev) if scatter == "combine" else None
-    gp.sort_routes(ids, weights, E, token_sorted, weight_sorted, expert_of_row, counts, expert_row0,
-                   route_index=route_index)
-    mark("sort_routes")
     # row tiles of `tr` rows of one expert: each decoded trellis tile feeds up to `tr` rows of MFMA work
     # (the reference's 128-row block table is build_blocks; the GEMM accepts either)
     tr = rows_per_tile or tile_rows()
     if tr not in TILE_ROWS_CHOICES:
         raise RuntimeError(f"rows_per_tile must be one of {TILE_ROWS_CHOICES}, got {tr}")
     max_blocks = R // tr + E
-    block_expert = torch.empty(max_blocks, dtype=torch.int32, device=dev)
-    block_row0 = torch.empty_like(block_expert)
     thin = (thin_tiles_enabled() if thin_tiles is None else thin_tiles) and scatter == "atomic"
+    R16 = gp.t16_rows(R)
+
+    def plan(take):
+        return dict(
+            token_sorted=take((R,), torch.int64), weight_sorted=take((R,), torch.float16),
+            expert_of_row=take((R,), torch.int32), counts=take((E,), torch.int32), expert_row0=take((E,), torch.int32),
+            route_index=take((R,), torch.int32) if scatter == "combine" else None,
+            sort_ws=take((gp.sort_routes_workspace_bytes(T, topk, E),), torch.uint8),
+            block_expert=take((max_blocks,), torch.int32), block_row0=take((max_blocks,), torch.int32),
+            thin_expert=take((min(E, R),), torch.int32) if thin else None,
+            thin_row0=take((min(E, R),), torch.int32) if thin else None,
+            meta=take((3 if thin else 2,), torch.int32),
+            # the GEMMs' activation operands (h13, act) and gu in the T16 layout, which makes their loads contiguous
+            h13=take((R16, K), torch.float16), gu=take((R16, 2 * I), torch.float16), act=take((R16, I), torch.float16))
+
+    B = _prefill_buffers(dev, plan)
+    token_sorted, weight_sorted, expert_of_row = B["token_sorted"], B["weight_sorted"], B["expert_of_row"]
+    counts, expert_row0, route_index = B["counts"], B["expert_row0"], B["route_index"]
+    block_expert, block_row0, meta = B["block_expert"], B["block_row0"], B["meta"]
+    gp.sort_routes(ids, weights, E, token_sorted, weight_sorted, expert_of_row, counts, expert_row0,
+                   workspace=B["sort_ws"], route_index=route_index)
+    mark("sort_routes")
     out = None
     if thin:
         # each expert's last tile of <= 64 rows goes to a second table, run by the thin kernel; the same launch
         # clears the fp32 output the down scatter adds into
-        thin_expert = torch.empty(min(E, R), dtype=torch.int32, device=dev)
-        thin_row0 = torch.empty_like(thin_expert)
-        meta = torch.empty(3, dtype=torch.int32, device=dev)              # written whole by the kernel
+        thin_expert, thin_row0 = B["thin_expert"], B["thin_row0"]
         out = torch.empty(T, K, dtype=torch.float32, device=dev)
         gp.build_tiles_split(counts, block_expert, block_row0, thin_expert, thin_row0, meta, tr, THIN_ROWS, zero=out)
     else:
-        meta = torch.empty(2, dtype=torch.int32, device=dev)
         gp.build_tiles(counts, block_expert, block_row0, meta, tr)
     mark("build_blocks")
-    # the GEMMs' activation operands (h13, act) are written in the T16 layout, which makes their loads contiguous
-    h13 = torch.empty(gp.t16_rows(R), K, dtype=torch.float16, device=dev)
+    h13 = B["h13"]
     gp.row_had(x16, h13, token_sorted, expert_of_row, layer.w13_suh[:, 0], True, dst_layout=1, rows=R)
     mark("row_had")
-    # gu in the T16 layout too (mode 4), so act_had's loads are contiguous 16-row blocks
-    gu = torch.empty(gp.t16_rows(R), 2 * I, dtype=torch.float16, device=dev)
+    gu = B["gu"]
     w13 = (layer.w13_trellis[:, 0], layer.w13_trellis[:, 1], layer.w13_svh[:, 0], layer.w13_svh[:, 1])
     gp.grouped_gemm(h13, *w13, block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 4,
                     tile_rows=tr, a_layout=1, a_rows=R)
@@ -151,7 +206,7 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
         gp.grouped_gemm(h13, *w13, thin_expert, thin_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 4,
                         tile_rows=THIN_ROWS, a_layout=1, a_rows=R)
     mark("gemm_gate_up")
-    act = torch.empty(gp.t16_rows(R), I, dtype=torch.float16, device=dev)
+    act = B["act"]
     gp.act_had(gu, act, expert_of_row, layer.w2_suh, float(limit), dst_layout=1, gu_layout=1, rows=R)
     mark("act_had")
     if scatter == "atomic":
@@ -198,10 +253,6 @@ def decode_enabled() -> bool:
 # allocated once, by the first decode call on the device (or reserve_decode_workspace), and never replaced: a graph
 # captured later keeps its address, so a later call that would need a larger one raises instead of swapping buffers.
 _decode_ws: dict = {}
-
-
-def _device_index(dev: torch.device) -> int:
-    return dev.index if dev.index is not None else torch.cuda.current_device()
 
 
 def reserve_decode_workspace(device, tokens: int, topk: int, n_experts: int, hidden: int, inter: int) -> torch.Tensor:

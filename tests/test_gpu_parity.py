@@ -600,6 +600,26 @@ def test_thin_config_all_bits(dev, bits, svh_scale):
     assert O.rel_l2(out[tokens], sampled_loop(L, x, ids, w, tokens)) < 1e-3
 
 
+def test_prefill_workspace_reuse(dev, monkeypatch):
+    """The prefill intermediates come from one per-device buffer reused across calls of different sizes (grown when a
+    call needs more): results match the per-call-allocation path up to the atomic summation order."""
+    L, x, ids, w, cfg = synth.make_config("layer1k", seed=3, svh_scale=1 / 64)
+    TL = synth.to_device(L, dev)
+    xt, it, wt = t16(x, dev), t16(ids, dev), t16(w, dev)
+    rt._prefill_ws.clear()
+    sizes = (1024, 300, 1024, 700)
+    got = []
+    for n in sizes:
+        got.append(rt.grouped_prefill(xt[:n], it[:n], wt[:n], TL, LIMIT))
+    ws = rt._prefill_ws[torch.cuda.current_device()]
+    got.append(rt.grouped_prefill(xt[:500], it[:500], wt[:500], TL, LIMIT))
+    assert rt._prefill_ws[torch.cuda.current_device()].data_ptr() == ws.data_ptr()      # no growth for smaller calls
+    monkeypatch.setenv("EXL3_GROUPED_WORKSPACE", "0")
+    for n, g in zip(sizes + (500,), got):
+        ref = rt.grouped_prefill(xt[:n], it[:n], wt[:n], TL, LIMIT)
+        assert ((g - ref).norm() / ref.norm()).item() < 1e-6, n
+
+
 def test_install_engages_grouped_path(dev, monkeypatch):
     L, x, ids, w, cfg = synth.make_config("tiny", seed=5)
     ov = Fake()
