@@ -18,6 +18,8 @@
 #include <mutex>
 
 #include "exl3_common.h"
+#include "hadamard.h"
+#include "routes.h"
 
 // Scratch of exl3_moe_decode_noalloc: the workspace of a decode call, for callers that cannot allocate. Every GPU
 // the library runs on holds its own copy until the process ends.
@@ -118,6 +120,154 @@ int decode_scratch(void** ptr)
     return EXL3_OK;
 }
 
+// ------------------------------------------------------------------------------------------- fused preparation
+// Up to TINY_ROUTES routes are ranked by direct comparison: the stable sort by expert puts route i at row
+// #{valid j : e_j < e_i} + #{j < i : e_j == e_i}, which every workgroup can compute from the ids alone. So the
+// gathered input Hadamard need not wait for the sort: one launch does it all, with the rows and tables identical to
+// exl3_route_prep_small's and h13 identical to row_had's.
+constexpr int TINY_ROUTES = 128;
+constexpr int PREP_THREADS = 256;
+
+// Workgroup 0: the sorted routes (token, fp16 weight, expert; rows past the valid ones zeroed), counts and
+// expert_row0 of every expert, the 64-row tile table (entries past the last tile -1) and meta = {tiles, rows}.
+// Workgroups 1 .. n_had: h13 (T16 layout, width `hidden`) = fp16(H128(x[token] * suh[e]) / sqrt(128)) at each
+// route's row; a wave takes 16 routes x one 128-column block per step. The remaining workgroups clear two fp32
+// buffers (float4 counts na, nb).
+__global__ __launch_bounds__(PREP_THREADS)
+void decode_prep_tiny_kernel(const uint16_t* __restrict__ x, int hidden, const void* __restrict__ ids, int ids_dtype,
+                             const void* __restrict__ weights, int w_dtype, int R, int topk, int n_experts,
+                             const uint16_t* __restrict__ suh, int64_t suh_stride, int max_tiles, int n_had,
+                             int64_t* __restrict__ token_sorted, uint16_t* __restrict__ weight_sorted,
+                             int32_t* __restrict__ expert_of_row, int32_t* __restrict__ counts,
+                             int32_t* __restrict__ expert_row0, int32_t* __restrict__ tile_expert,
+                             int32_t* __restrict__ tile_row0, int32_t* __restrict__ meta, uint16_t* __restrict__ h13,
+                             float4* __restrict__ zero_a, int64_t na, float4* __restrict__ zero_b, int64_t nb)
+{
+    const int t = threadIdx.x;
+    if ((int) blockIdx.x > n_had)
+    {
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        const int64_t wgs = gridDim.x - 1 - n_had;
+        for (int64_t i = (int64_t) (blockIdx.x - 1 - n_had) * PREP_THREADS + t; i < na + nb; i += wgs * PREP_THREADS)
+        {
+            if (i < na) zero_a[i] = z;
+            else zero_b[i - na] = z;
+        }
+        return;
+    }
+    __shared__ int s_e[TINY_ROUTES], s_rank[TINY_ROUTES], s_cnt[TINY_ROUTES], s_first[TINY_ROUTES];
+    if (t < TINY_ROUTES) s_e[t] = t < R ? route_id(ids, ids_dtype, t, n_experts) : -1;
+    __syncthreads();
+    int n_rows = 0;                                     // valid routes (every thread)
+    if (t < TINY_ROUTES)
+    {
+        const int e = t < R ? s_e[t] : -1;
+        int before = 0, same_before = 0, same = 0;
+        for (int j = 0; j < R; ++j)
+        {
+            const int f = s_e[j];
+            n_rows += f >= 0;
+            before += f >= 0 && f < e;
+            same_before += f == e && j < t;
+            same += f == e;
+        }
+        s_rank[t] = e >= 0 ? before + same_before : -1;
+        s_cnt[t] = same;
+        s_first[t] = e >= 0 && same_before == 0;
+    }
+    else
+        for (int j = 0; j < R; ++j) n_rows += s_e[j] >= 0;
+    __syncthreads();
+
+    if (blockIdx.x == 0)
+    {
+        if (t < R)
+        {
+            const int r = s_rank[t];
+            if (r >= 0)
+            {
+                token_sorted[r] = t / topk;
+                weight_sorted[r] = route_weight_f16(weights, w_dtype, t);
+                expert_of_row[r] = s_e[t];
+            }
+            if (t >= n_rows)                            // rows past the valid ones (dropped routes)
+            {
+                token_sorted[t] = 0;
+                weight_sorted[t] = 0;
+                expert_of_row[t] = 0;
+            }
+        }
+        for (int e = t; e < n_experts; e += PREP_THREADS)
+        {
+            int c = 0, below = 0;
+            for (int j = 0; j < R; ++j)
+            {
+                const int f = s_e[j];
+                c += f == e;
+                below += f >= 0 && f < e;
+            }
+            counts[e] = c;
+            expert_row0[e] = below;
+        }
+        // tiles of 64 rows, experts in order: expert e's first tile follows those of every smaller active expert
+        int tile0 = 0, n_tiles = 0;
+        const int e = t < R ? s_e[t] : -1;
+        for (int j = 0; j < R; ++j)
+        {
+            if (!s_first[j]) continue;
+            const int nt = (s_cnt[j] + DECODE_TILE_ROWS - 1) / DECODE_TILE_ROWS;
+            n_tiles += nt;
+            if (s_e[j] < e) tile0 += nt;
+        }
+        if (t < R && s_first[t])
+            for (int q = 0; q * DECODE_TILE_ROWS < s_cnt[t]; ++q)
+                if (tile0 + q < max_tiles)
+                {
+                    tile_expert[tile0 + q] = e;
+                    tile_row0[tile0 + q] = s_rank[t] + q * DECODE_TILE_ROWS;
+                }
+        for (int b = n_tiles + t; b < max_tiles; b += PREP_THREADS) tile_expert[b] = -1;
+        if (t == 0) { meta[0] = n_tiles; meta[1] = n_rows; }
+        return;
+    }
+
+    // the input Hadamard of every route, at its sorted row
+    const int lane = t & 63, wave = t >> 6, rl = lane & 15, cq = lane >> 4;
+    const int blocks = hidden / 128;
+    const int n_items = (R + 15) / 16 * blocks;
+    for (int it = (blockIdx.x - 1) * (PREP_THREADS / 64) + wave; it < n_items; it += n_had * (PREP_THREADS / 64))
+    {
+        const int g = it / blocks, blk = it - g * blocks;
+        const int i = g * 16 + rl;
+        const int r = i < R ? s_rank[i] : -1;
+        const int ic = r >= 0 ? i : 0;                  // lanes without a route still join the lane butterflies
+        const int e = max(s_e[ic], 0);
+        const int64_t tok = ic / topk;
+        float v[32];
+        #pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            const int c = blk * 128 + 8 * (4 * k + cq);
+            float xs[8], ss[8];
+            unpack8(*reinterpret_cast<const uint4*>(x + tok * hidden + c), xs);
+            unpack8(*reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + c), ss);
+            #pragma unroll
+            for (int j = 0; j < 8; ++j) v[8 * k + j] = xs[j] * ss[j];
+        }
+        had128_t16(v, lane);
+        if (r >= 0)
+            #pragma unroll
+            for (int k = 0; k < 4; ++k)
+            {
+                float o[8];
+                #pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = v[8 * k + j];
+                const int64_t chunk = (int64_t) (r >> 4) * (hidden / 8) + blk * 16 + 4 * k + cq;
+                *reinterpret_cast<uint4*>(h13 + chunk * 128 + (r & 15) * 8) = pack8(o);
+            }
+    }
+}
+
 }  // namespace
 }  // namespace exl3
 
@@ -171,7 +321,23 @@ extern "C" int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, co
     // accumulation targets: out [tokens, hidden] and gu [R, 2 inter], both whole float4s
     const int64_t n_out = tokens * hidden, n_gu = R * 2 * inter;
     int rc;
-    if (R <= SMALL_ROUTES)
+    if (R <= TINY_ROUTES)
+    {
+        // sort, tile table, both clears and the input Hadamard in one launch
+        EXL3_CHECK(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(suh_gate)) & 15) == 0 &&
+                   suh13_stride % 8 == 0, "x and suh must be 16-byte aligned");
+        const int n_had = ((int) ((R + 15) / 16) * (hidden / 128) + PREP_THREADS / 64 - 1) / (PREP_THREADS / 64);
+        const int64_t n4 = n_out / 4 + n_gu / 4;
+        const int64_t zwgs = std::min<int64_t>((n4 + PREP_THREADS - 1) / PREP_THREADS, 1024);
+        decode_prep_tiny_kernel<<<(unsigned) (1 + n_had + zwgs), PREP_THREADS, 0, s>>>(
+            x, hidden, topk_ids, ids_dtype, topk_weights, weights_dtype, (int) R, topk, n_experts, suh_gate,
+            suh13_stride, L.max_blocks, n_had, token_sorted, weight_sorted, expert_of_row, counts, expert_row0,
+            block_expert, block_row0, meta, h13, reinterpret_cast<float4*>(out), n_out / 4,
+            reinterpret_cast<float4*>(gu), n_gu / 4);
+        rc = hip_status("moe_decode prep");
+        if (rc) return rc;
+    }
+    else if (R <= SMALL_ROUTES)
     {
         // sort, tile table and both clears in one launch
         rc = exl3_route_prep_small(topk_ids, ids_dtype, topk_weights, weights_dtype, tokens, topk, n_experts,
@@ -194,9 +360,12 @@ extern "C" int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, co
                               stream);
         if (rc) return rc;
     }
-    rc = exl3_row_had_ex(x, h13, token_sorted, expert_of_row, suh_gate, suh13_stride, hidden, R, hidden, 1,
-                         EXL3_LAYOUT_T16, stream);
-    if (rc) return rc;
+    if (R > TINY_ROUTES)
+    {
+        rc = exl3_row_had_ex(x, h13, token_sorted, expert_of_row, suh_gate, suh13_stride, hidden, R, hidden, 1,
+                             EXL3_LAYOUT_T16, stream);
+        if (rc) return rc;
+    }
     const int target = target_workgroups();
     const int gu_split = k_split_for((int64_t) L.max_blocks * 2 * (inter / 128), hidden / 32, target);
     rc = exl3_grouped_gemm_split(h13, R, hidden, EXL3_LAYOUT_T16, packed_gate, packed_up, w13_expert_stride_words,

@@ -9,7 +9,7 @@
 //      order is exactly the stable order.
 // build_blocks restates kernel/exl3_grouped_prefill.cu:63-96 with a parallel scan instead of the serial one.
 // route_topk is the router glue in front of the sort (GLM-5.3-Flash's noaux_tc top-k): one wave per token.
-#include "exl3_common.h"
+#include "routes.h"
 
 #include <math.h>
 
@@ -22,28 +22,6 @@ constexpr int SORT_THREADS = 256;
 constexpr int SORT_WAVES = SORT_THREADS / 64;
 constexpr int ROUTES_PER_THREAD = 8;
 constexpr int CHUNK = SORT_THREADS * ROUTES_PER_THREAD;    // routes per workgroup in passes 1 and 3
-
-template <typename T>
-__device__ __forceinline__ int load_id(const void* ids, int64_t i)
-{
-    const int64_t v = (int64_t) reinterpret_cast<const T*>(ids)[i];
-    return (int) v == v ? (int) v : -1;
-}
-
-__device__ __forceinline__ int route_id(const void* ids, int ids_dtype, int64_t i, int n_experts)
-{
-    const int e = (ids_dtype == EXL3_DTYPE_I64) ? load_id<int64_t>(ids, i) : load_id<int32_t>(ids, i);
-    return (e >= 0 && e < n_experts) ? e : -1;
-}
-
-__device__ __forceinline__ uint16_t route_weight_f16(const void* w, int dtype, int64_t i)
-{
-    float f;
-    if (dtype == EXL3_DTYPE_F32) f = reinterpret_cast<const float*>(w)[i];
-    else if (dtype == EXL3_DTYPE_F16) return reinterpret_cast<const uint16_t*>(w)[i];
-    else f = __uint_as_float((uint32_t) reinterpret_cast<const uint16_t*>(w)[i] << 16);   // bf16
-    return f2h(f);
-}
 
 __global__ __launch_bounds__(SORT_THREADS)
 void sort_hist_kernel(const void* __restrict__ ids, int ids_dtype, int64_t R, int n_experts,

@@ -132,6 +132,59 @@ def test_route_prep_small_bit_exact(dev, kind, T, E, k, tile_rows):
         assert not za.any() and not zb.any()
 
 
+def decode_workspace_views(ws, T, k, E, H, I):
+    """The decode workspace's sorted routes, tables, meta and h13, at the offsets exl3_moe_decode lays them out
+    (moe_decode.hip decode_layout: each buffer 256-byte aligned, in this order)."""
+    R = T * k
+    mb = min(E, R) + R // 64
+    sizes = [("sort", gp.sort_routes_workspace_bytes(T, k, E)), ("ts", R * 8), ("ws", R * 2), ("eor", R * 4),
+             ("counts", E * 4), ("row0", E * 4), ("be", mb * 4), ("br", mb * 4), ("meta", 8),
+             ("h13", gp.t16_rows(R) * H * 2)]
+    views, o = {}, 0
+    for name, n in sizes:
+        views[name] = ws[o:o + n]
+        o += (n + 255) // 256 * 256
+    return (views["ts"].view(torch.int64), views["ws"].view(torch.float16), views["eor"].view(torch.int32),
+            views["counts"].view(torch.int32), views["row0"].view(torch.int32), views["be"].view(torch.int32),
+            views["br"].view(torch.int32), views["meta"].view(torch.int32)[:2],
+            views["h13"].view(torch.float16).view(gp.t16_rows(R), H), mb)
+
+
+@pytest.mark.parametrize("T,drop", [(1, False), (5, True), (16, False), (16, True)])
+def test_decode_fused_prep_matches_separate_launches(dev, T, drop):
+    """Up to 128 routes the decode op sorts, builds the tile table, clears and runs the input Hadamard in one launch,
+    ranking each route by direct comparison. Its rows, tables and h13 must equal the closed-form stable sort, the
+    block table (kernel/exl3_grouped_prefill.cu:63-96) and row_had over those rows (:101-115), bit for bit."""
+    L, cfg = layer_case("layer1k", svh_scale=1 / 64)
+    TL = device_layer("layer1k", svh_scale=1 / 64)
+    E, H, I, k = cfg["E"], cfg["H"], cfg["I"], cfg["topk"]
+    x, ids, w = inputs(cfg, T, 40 + T)
+    ids = ids.copy()
+    if drop:
+        ids[0, 1] = -1
+        ids[T - 1, k - 1] = E + 2
+    wt = torch.from_numpy(w).to(torch.bfloat16)
+    R = T * k
+    ws = torch.full((gp.moe_decode_workspace_bytes(T, k, E, H, I),), 0x5A, dtype=torch.uint8, device=dev)
+    x16 = dt(x, dev).to(torch.float16)
+    gp.moe_decode(x16, dt(ids, dev).to(torch.int32), wt.to(dev), TL.w13_trellis, TL.w13_suh, TL.w13_svh,
+                  TL.w2_trellis, TL.w2_suh, TL.w2_svh, LIMIT, workspace=ws)
+    torch.cuda.synchronize()
+    ts, wsrt, eor, counts, row0, be, br, meta, h13, mb = decode_workspace_views(ws, T, k, E, H, I)
+    ref = closed_form_sort(ids, wt.float().numpy(), E)
+    for g, r in zip((ts, wsrt, eor, counts, row0), ref):
+        assert np.array_equal(g.cpu().numpy().view(np.uint8), np.asarray(r).view(np.uint8))
+    rbe, rbr, rmeta = O.build_blocks(ref[3], mb, init=-7, tile_rows=64)
+    n = int(rmeta[0])
+    assert meta.tolist() == [int(v) for v in rmeta]
+    assert np.array_equal(be.cpu().numpy(), rbe) and np.array_equal(br.cpu().numpy()[:n], rbr[:n])
+    h_ref = torch.zeros(gp.t16_rows(R), H, dtype=torch.float16, device=dev)
+    gp.row_had(x16, h_ref, dt(ref[0], dev), dt(ref[2], dev), TL.w13_suh[:, 0], True, dst_layout=1, rows=R)
+    rows = int(rmeta[1])                     # the valid rows: the tail's h13 is never read
+    t16 = lambda a: a.view(-1, H // 8, 16, 8).permute(0, 2, 1, 3).reshape(-1, H)[:rows]
+    assert torch.equal(t16(h13).view(torch.int16), t16(h_ref).view(torch.int16))
+
+
 def sorted_case(cfg, T, seed, dev, tile_rows=128, routing="softmax"):
     x, ids, w = inputs(cfg, T, seed, routing)
     E = cfg["E"]
