@@ -75,6 +75,9 @@ def parse():
     ap.add_argument("--stages", action="store_true", help="print per-stage ms to stderr")
     ap.add_argument("--scatter", choices=["atomic", "combine"], default=None,
                     help="down-projection output method (default: the runtime's, EXL3_GROUPED_SCATTER or atomic)")
+    ap.add_argument("--atomic-probe", action="store_true",
+                    help="only time fp32 atomic adds of the down scatter's volume (65536 rows x 4096 floats into 8192 "
+                         "token rows, torch index_add_) against a plain copy of the same rows, and exit")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB a few times (calibrates rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE against known bytes) and exit")
@@ -91,6 +94,34 @@ def copy_probe(mib: int):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_probe_bytes_per_launch": n * 4, "launches": 5}), flush=True)
+
+
+def atomic_probe():
+    """The scatter's fp32 atomic volume alone: out[token[r]] += src[r] for 65536 rows of 4096 floats (1.07 GB of fp32
+    adds, the down scatter at the headline shape) with torch's index_add_ (one hardware fp32 atomic per element), and a
+    plain device copy of the same 1.07 GB for comparison (it also reads them: twice the bytes). HIP events, median of
+    5."""
+    import torch
+    g = torch.Generator(device="cuda:0").manual_seed(0)
+    rows, width, tokens = 65536, 4096, 8192
+    src = torch.randn(rows, width, device="cuda:0", generator=g)
+    idx = torch.randint(0, tokens, (rows,), device="cuda:0", generator=g)
+    out = torch.zeros(tokens, width, device="cuda:0")
+    dst = torch.empty_like(src)
+    res = {}
+    for name, fn in (("atomic_add", lambda: out.index_add_(0, idx, src)), ("copy", lambda: dst.copy_(src))):
+        ts = []
+        for _ in range(7):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        ms = statistics.median(ts[2:])
+        res[name] = {"ms": round(ms, 4), "fp32_elements_per_s": round(rows * width / (ms * 1e-3), 1),
+                     "bytes_per_s": round(rows * width * 4 / (ms * 1e-3), 1)}
+    print(json.dumps({"atomic_probe": res, "elements": rows * width}), flush=True)
 
 
 def profile_json(name: str):
@@ -465,6 +496,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.atomic_probe:
+        atomic_probe()
+        return
     if args.copy_probe:
         copy_probe(args.copy_probe)
         return

@@ -155,28 +155,42 @@ void decode_prep_tiny_kernel(const uint16_t* __restrict__ x, int hidden, const v
         }
         return;
     }
-    __shared__ int s_e[TINY_ROUTES], s_rank[TINY_ROUTES], s_cnt[TINY_ROUTES], s_first[TINY_ROUTES];
+    // route j's expert (-1: dropped or past R), in int4 steps; its row; its expert's tile count if j is the expert's
+    // first route (else 0)
+    __shared__ __align__(16) int s_e[TINY_ROUTES];
+    __shared__ __align__(16) int s_nt[TINY_ROUTES];
+    __shared__ int s_rank[TINY_ROUTES];
     if (t < TINY_ROUTES) s_e[t] = t < R ? route_id(ids, ids_dtype, t, n_experts) : -1;
     __syncthreads();
+    const int R4 = (R + 3) / 4;
+    const int4* e4 = reinterpret_cast<const int4*>(s_e);
     int n_rows = 0;                                     // valid routes (every thread)
     if (t < TINY_ROUTES)
     {
-        const int e = t < R ? s_e[t] : -1;
+        const int e = s_e[t];
         int before = 0, same_before = 0, same = 0;
-        for (int j = 0; j < R; ++j)
+        for (int q = 0; q < R4; ++q)
         {
-            const int f = s_e[j];
-            n_rows += f >= 0;
-            before += f >= 0 && f < e;
-            same_before += f == e && j < t;
-            same += f == e;
+            const int4 f4 = e4[q];
+            const int f[4] = {f4.x, f4.y, f4.z, f4.w};
+            #pragma unroll
+            for (int k = 0; k < 4; ++k)
+            {
+                n_rows += f[k] >= 0;
+                before += f[k] >= 0 && f[k] < e;
+                same_before += f[k] == e && 4 * q + k < t;
+                same += f[k] == e;
+            }
         }
         s_rank[t] = e >= 0 ? before + same_before : -1;
-        s_cnt[t] = same;
-        s_first[t] = e >= 0 && same_before == 0;
+        s_nt[t] = e >= 0 && same_before == 0 ? (same + DECODE_TILE_ROWS - 1) / DECODE_TILE_ROWS : 0;
     }
     else
-        for (int j = 0; j < R; ++j) n_rows += s_e[j] >= 0;
+        for (int q = 0; q < R4; ++q)
+        {
+            const int4 f4 = e4[q];
+            n_rows += (f4.x >= 0) + (f4.y >= 0) + (f4.z >= 0) + (f4.w >= 0);
+        }
     __syncthreads();
 
     if (blockIdx.x == 0)
@@ -200,27 +214,32 @@ void decode_prep_tiny_kernel(const uint16_t* __restrict__ x, int hidden, const v
         for (int e = t; e < n_experts; e += PREP_THREADS)
         {
             int c = 0, below = 0;
-            for (int j = 0; j < R; ++j)
+            for (int q = 0; q < R4; ++q)
             {
-                const int f = s_e[j];
-                c += f == e;
-                below += f >= 0 && f < e;
+                const int4 f4 = e4[q];
+                const int f[4] = {f4.x, f4.y, f4.z, f4.w};
+                #pragma unroll
+                for (int k = 0; k < 4; ++k)
+                {
+                    c += f[k] == e;
+                    below += f[k] >= 0 && f[k] < e;
+                }
             }
             counts[e] = c;
             expert_row0[e] = below;
         }
         // tiles of 64 rows, experts in order: expert e's first tile follows those of every smaller active expert
+        const int e = t < TINY_ROUTES ? s_e[t] : -1;
+        const int4* nt4 = reinterpret_cast<const int4*>(s_nt);
         int tile0 = 0, n_tiles = 0;
-        const int e = t < R ? s_e[t] : -1;
-        for (int j = 0; j < R; ++j)
+        for (int q = 0; q < R4; ++q)
         {
-            if (!s_first[j]) continue;
-            const int nt = (s_cnt[j] + DECODE_TILE_ROWS - 1) / DECODE_TILE_ROWS;
-            n_tiles += nt;
-            if (s_e[j] < e) tile0 += nt;
+            const int4 f4 = e4[q], n4 = nt4[q];
+            n_tiles += n4.x + n4.y + n4.z + n4.w;
+            tile0 += (f4.x < e ? n4.x : 0) + (f4.y < e ? n4.y : 0) + (f4.z < e ? n4.z : 0) + (f4.w < e ? n4.w : 0);
         }
-        if (t < R && s_first[t])
-            for (int q = 0; q * DECODE_TILE_ROWS < s_cnt[t]; ++q)
+        if (t < R)
+            for (int q = 0; q < s_nt[t]; ++q)
                 if (tile0 + q < max_tiles)
                 {
                     tile_expert[tile0 + q] = e;
