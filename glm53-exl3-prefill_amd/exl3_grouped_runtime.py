@@ -81,8 +81,12 @@ THIN_ROWS = 64
 # The prefill intermediates (sorted routes, tile tables, h13, gu, act: ~0.85 GB at 8192 tokens) live in one buffer per
 # device, reused by every call and grown (never shrunk) when a call needs more: steady-state calls allocate nothing but
 # their output, and the kernels keep working on memory they have touched before. Calls on one device must be ordered on
-# one stream (the model runner's); EXL3_GROUPED_WORKSPACE=0 allocates per call instead.
+# one stream (the model runner's); EXL3_GROUPED_WORKSPACE=0 allocates per call instead. A buffer that a larger call
+# outgrows is kept, not freed: a HIP graph captured over an earlier call still addresses it
+# (release_outgrown_prefill_workspaces frees them once no such graph is in use; reserve_prefill_workspace sizes the
+# buffer for the largest chunk up front so it never grows).
 _prefill_ws: dict = {}
+_prefill_ws_outgrown: dict = {}
 
 
 def _device_index(dev: torch.device) -> int:
@@ -103,7 +107,7 @@ class _Carve:
         n = 1
         for d in shape:
             n *= int(d)
-        nbytes = n * torch.empty((), dtype=dtype).element_size()
+        nbytes = n * dtype.itemsize
         start = (self.off + 255) // 256 * 256
         self.off = start + nbytes
         if self.buf is None:
@@ -118,13 +122,59 @@ def _prefill_buffers(dev, plan):
         return plan(_Carve(None, dev))
     sizing = _Carve()
     plan(sizing)
+    return plan(_Carve(_prefill_workspace(dev, sizing.off)))
+
+
+def _prefill_workspace(dev, nbytes: int) -> torch.Tensor:
     key = _device_index(dev)
     ws = _prefill_ws.get(key)
-    if ws is None or ws.numel() < sizing.off:
-        _prefill_ws.pop(key, None)
-        ws = torch.empty(max(sizing.off, 256), dtype=torch.uint8, device=dev)
+    if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _prefill_ws_outgrown.setdefault(key, []).append(ws)
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
         _prefill_ws[key] = ws
-    return plan(_Carve(ws))
+    return ws
+
+
+def release_outgrown_prefill_workspaces(device=None) -> None:
+    """Free the prefill workspaces that larger calls replaced (on every device, or one), once no HIP graph captured
+    over an earlier, smaller call is replayed any more."""
+    for key in ([_device_index(torch.device(device))] if device is not None else list(_prefill_ws_outgrown)):
+        _prefill_ws_outgrown.pop(key, None)
+
+
+def reserve_prefill_workspace(device, tokens: int, topk: int, n_experts: int, hidden: int, inter: int,
+                              scatter: str | None = None, rows_per_tile: int | None = None) -> torch.Tensor:
+    """Size the device's prefill workspace for a chunk of `tokens` (the largest the scheduler sends) before the first
+    call, e.g. ahead of memory profiling or graph capture, so that no later call grows it. Returns the buffer."""
+    scatter = scatter or scatter_mode()
+    tr = rows_per_tile or tile_rows()
+    thin = thin_tiles_enabled() and scatter == "atomic"
+    sizing = _Carve()
+    _prefill_plan(_load_ext(), tokens, hidden, topk, n_experts, inter, tr, scatter, thin)(sizing)
+    return _prefill_workspace(torch.device(device), sizing.off)
+
+
+def _prefill_plan(gp, T: int, K: int, topk: int, E: int, I: int, tr: int, scatter: str, thin: bool):
+    """The intermediates of one grouped_prefill call of T tokens, requested in a fixed order through take(shape, dtype):
+    the sorted routes, the tile tables (rows_per_tile tr, plus the thin table), and h13 / gu / act in the T16 layout."""
+    R = T * topk
+    max_blocks = R // tr + E
+    R16 = gp.t16_rows(R)
+
+    def plan(take):
+        return dict(
+            token_sorted=take((R,), torch.int64), weight_sorted=take((R,), torch.float16),
+            expert_of_row=take((R,), torch.int32), counts=take((E,), torch.int32), expert_row0=take((E,), torch.int32),
+            route_index=take((R,), torch.int32) if scatter == "combine" else None,
+            sort_ws=take((gp.sort_routes_workspace_bytes(T, topk, E),), torch.uint8),
+            block_expert=take((max_blocks,), torch.int32), block_row0=take((max_blocks,), torch.int32),
+            thin_expert=take((min(E, R),), torch.int32) if thin else None,
+            thin_row0=take((min(E, R),), torch.int32) if thin else None,
+            meta=take((3 if thin else 2,), torch.int32),
+            # the GEMMs' activation operands (h13, act) and gu in the T16 layout, which makes their loads contiguous
+            h13=take((R16, K), torch.float16), gu=take((R16, 2 * I), torch.float16), act=take((R16, I), torch.float16))
+    return plan
 
 
 def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, layer, limit: float,
@@ -161,24 +211,8 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     tr = rows_per_tile or tile_rows()
     if tr not in TILE_ROWS_CHOICES:
         raise RuntimeError(f"rows_per_tile must be one of {TILE_ROWS_CHOICES}, got {tr}")
-    max_blocks = R // tr + E
     thin = (thin_tiles_enabled() if thin_tiles is None else thin_tiles) and scatter == "atomic"
-    R16 = gp.t16_rows(R)
-
-    def plan(take):
-        return dict(
-            token_sorted=take((R,), torch.int64), weight_sorted=take((R,), torch.float16),
-            expert_of_row=take((R,), torch.int32), counts=take((E,), torch.int32), expert_row0=take((E,), torch.int32),
-            route_index=take((R,), torch.int32) if scatter == "combine" else None,
-            sort_ws=take((gp.sort_routes_workspace_bytes(T, topk, E),), torch.uint8),
-            block_expert=take((max_blocks,), torch.int32), block_row0=take((max_blocks,), torch.int32),
-            thin_expert=take((min(E, R),), torch.int32) if thin else None,
-            thin_row0=take((min(E, R),), torch.int32) if thin else None,
-            meta=take((3 if thin else 2,), torch.int32),
-            # the GEMMs' activation operands (h13, act) and gu in the T16 layout, which makes their loads contiguous
-            h13=take((R16, K), torch.float16), gu=take((R16, 2 * I), torch.float16), act=take((R16, I), torch.float16))
-
-    B = _prefill_buffers(dev, plan)
+    B = _prefill_buffers(dev, _prefill_plan(gp, T, K, topk, E, I, tr, scatter, thin))
     token_sorted, weight_sorted, expert_of_row = B["token_sorted"], B["weight_sorted"], B["expert_of_row"]
     counts, expert_row0, route_index = B["counts"], B["expert_row0"], B["route_index"]
     block_expert, block_row0, meta = B["block_expert"], B["block_row0"], B["meta"]

@@ -607,15 +607,26 @@ def test_prefill_workspace_reuse(dev, monkeypatch):
     TL = synth.to_device(L, dev)
     xt, it, wt = t16(x, dev), t16(ids, dev), t16(w, dev)
     rt._prefill_ws.clear()
-    sizes = (1024, 300, 1024, 700)
-    got = []
-    for n in sizes:
+    rt._prefill_ws_outgrown.clear()
+    key = torch.cuda.current_device()
+    sizes = (300, 1024, 300, 1024, 700)
+    got = [rt.grouped_prefill(xt[:sizes[0]], it[:sizes[0]], wt[:sizes[0]], TL, LIMIT)]
+    first = rt._prefill_ws[key].data_ptr()
+    for n in sizes[1:]:
         got.append(rt.grouped_prefill(xt[:n], it[:n], wt[:n], TL, LIMIT))
-    ws = rt._prefill_ws[torch.cuda.current_device()]
+    ws = rt._prefill_ws[key]
+    assert [b.data_ptr() for b in rt._prefill_ws_outgrown[key]] == [first]     # outgrown, kept for captured graphs
     got.append(rt.grouped_prefill(xt[:500], it[:500], wt[:500], TL, LIMIT))
-    assert rt._prefill_ws[torch.cuda.current_device()].data_ptr() == ws.data_ptr()      # no growth for smaller calls
+    assert rt._prefill_ws[key].data_ptr() == ws.data_ptr()                     # no growth for smaller calls
+    rt.release_outgrown_prefill_workspaces()
+    assert not rt._prefill_ws_outgrown
+    big = rt.reserve_prefill_workspace(dev, 2 * x.shape[0], cfg["topk"], cfg["E"], cfg["H"], cfg["I"])
+    assert big.numel() > ws.numel() and rt._prefill_ws[key].data_ptr() == big.data_ptr()
+    rt.grouped_prefill(xt, it, wt, TL, LIMIT)
+    assert rt._prefill_ws[key].data_ptr() == big.data_ptr()                    # reserved: the full chunk fits
+    sizes = sizes + (500,)
     monkeypatch.setenv("EXL3_GROUPED_WORKSPACE", "0")
-    for n, g in zip(sizes + (500,), got):
+    for n, g in zip(sizes, got):
         ref = rt.grouped_prefill(xt[:n], it[:n], wt[:n], TL, LIMIT)
         assert ((g - ref).norm() / ref.norm()).item() < 1e-6, n
 
