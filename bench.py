@@ -217,7 +217,7 @@ def run(args, T=None, emit=True):
                           "gemm_tflops_both": round(both_gemm_tflops, 1),
                           "layer_tflops": round(layer_tflops, 1)}), file=sys.stderr, flush=True)
     workload = f"{cfg_name}: E={E} H={H} I={I} {bits}bpw T={T_} top{k} {cfg['routing']}"
-    thin = rt.thin_tiles_enabled() and scatter == "atomic"
+    thin = rt.thin_tiles_enabled()
     kernels_of = {st: [kn.format(bits=bits) for kn in (ks if thin or not st.startswith("gemm") else ks[:1])]
                   for st, ks in STAGE_KERNELS.items()}
     gate_up_kernels = kernels_of["gemm_gate_up"]

@@ -637,7 +637,7 @@ void trellis_gemm_kernel(const GemmParams p)
 }
 
 // 512-row tiles run the 8-wave variant, 128- and 256-row tiles the 4-wave kernel (the only one built for ATOMIC_F32,
-// whose split-K launches serve small batches), 64-row tiles of grouped modes 0, 1 and 3 the thin 4-wave variant.
+// whose split-K launches serve small batches), 64-row tiles the thin 4-wave variant.
 template <int BITS, int MODE, bool DENSE>
 int launch_gemm(const GemmParams& p, hipStream_t s)
 {
@@ -645,13 +645,10 @@ int launch_gemm(const GemmParams& p, hipStream_t s)
     const int64_t grid = (int64_t) groups8 * p.n_slots * (p.k_split > 1 ? p.k_split : 1);
     if (grid == 0) return EXL3_OK;
     if (grid > 0x7FFFFFFF) return fail("grid too large");
-    if constexpr (MODE != MODE_STORE_ROUTE_F32)
+    if (p.tile_rows == 64)
     {
-        if (p.tile_rows == 64)
-        {
-            trellis_gemm_kernel<BITS, MODE, DENSE, 1><<<(unsigned) grid, 256, 0, s>>>(p);
-            return EXL3_OK;
-        }
+        trellis_gemm_kernel<BITS, MODE, DENSE, 1><<<(unsigned) grid, 256, 0, s>>>(p);
+        return EXL3_OK;
     }
     if constexpr (MODE == MODE_ATOMIC_F32)
     {

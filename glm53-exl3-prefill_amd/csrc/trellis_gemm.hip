@@ -9,30 +9,56 @@ namespace exl3 {
 namespace {
 
 // out[t, :] = sum_j partial[t*topk + j, :] in order j = 0 .. topk-1 (deterministic), skipping routes whose id is
-// outside [0, n_experts) (their partial rows were never written).
-__global__ __launch_bounds__(256)
+// outside [0, n_experts) (their partial rows were never written). A workgroup per token (grid-strided): the token's
+// route ids are read once; each thread loads its columns of all topk rows before adding them (a skipped route's row is
+// loaded and discarded by a select, so no load waits behind a branch). TOPK > 0 fixes topk at compile time.
+constexpr int COMBINE_THREADS = 256;
+constexpr int COMBINE_MAX_TOPK = 32;
+
+template <int TOPK>
+__global__ __launch_bounds__(COMBINE_THREADS)
 void combine_routes_kernel(const float4* __restrict__ partial, float4* __restrict__ out, const void* __restrict__ ids,
-                           int ids_dtype, int n_experts, int64_t tokens, int topk, int64_t n4)
+                           int ids_dtype, int n_experts, int64_t tokens, int topk_rt, int64_t n4)
 {
-    const int64_t total = tokens * n4;
-    for (int64_t idx = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-         idx += (int64_t) gridDim.x * blockDim.x)
+    const int topk = TOPK > 0 ? TOPK : topk_rt;
+    for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x)
     {
-        const int64_t t = idx / n4, c = idx - t * n4;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        uint32_t live = 0;                              // bit j: route j of the token contributes
         for (int j = 0; j < topk; ++j)
         {
             const int64_t i = t * topk + j;
+            int64_t e = 0;
             if (ids)
-            {
-                const int64_t e = ids_dtype == EXL3_DTYPE_I64 ? reinterpret_cast<const int64_t*>(ids)[i]
-                                                             : reinterpret_cast<const int32_t*>(ids)[i];
-                if (e < 0 || e >= n_experts) continue;
-            }
-            const float4 v = partial[i * n4 + c];
-            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+                e = ids_dtype == EXL3_DTYPE_I64 ? reinterpret_cast<const int64_t*>(ids)[i]
+                                                : reinterpret_cast<const int32_t*>(ids)[i];
+            if (e >= 0 && e < n_experts) live |= 1u << j;
         }
-        out[idx] = acc;
+        const float4* rows = partial + t * topk * n4;
+        for (int64_t c = threadIdx.x; c < n4; c += COMBINE_THREADS)
+        {
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (TOPK > 0)
+            {
+                float4 v[TOPK];
+                #pragma unroll
+                for (int j = 0; j < TOPK; ++j) v[j] = rows[j * n4 + c];
+                #pragma unroll
+                for (int j = 0; j < TOPK; ++j)
+                {
+                    const bool on = live >> j & 1;
+                    acc.x += on ? v[j].x : 0.f; acc.y += on ? v[j].y : 0.f;
+                    acc.z += on ? v[j].z : 0.f; acc.w += on ? v[j].w : 0.f;
+                }
+            }
+            else
+                for (int j = 0; j < topk; ++j)
+                {
+                    if (!(live >> j & 1)) continue;
+                    const float4 v = rows[j * n4 + c];
+                    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+                }
+            out[t * n4 + c] = acc;
+        }
     }
 }
 
@@ -114,9 +140,8 @@ extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int si
                                        const int32_t* route_index, void* out, int64_t out_rows, int mode,
                                        int k_split, void* stream)
 {
-    EXL3_CHECK(tile_rows == 128 || tile_rows == 256 || tile_rows == 512 ||
-               (tile_rows == 64 && mode != EXL3_GEMM_STORE_ROUTE_F32),
-               "tile_rows must be 128, 256 or 512 (or 64 in modes 0, 1, 3 and 4)");
+    EXL3_CHECK(tile_rows == 64 || tile_rows == 128 || tile_rows == 256 || tile_rows == 512,
+               "tile_rows must be 64, 128, 256 or 512");
     EXL3_CHECK(a_layout == EXL3_LAYOUT_ROWS || a_layout == EXL3_LAYOUT_T16, "unknown layout");
     EXL3_CHECK(bits >= 2 && bits <= 4, "unsupported bits %d (2, 3 or 4)", bits);
     EXL3_CHECK(size_k == tiles_k * 16 && size_k % 64 == 0 && size_k > 0, "K mismatch");
@@ -407,11 +432,16 @@ extern "C" int exl3_combine_routes(const float* partial, float* out, const void*
     if (tokens == 0) return EXL3_OK;
     EXL3_CHECK(partial && out, "null pointer");
     EXL3_CHECK(aligned16(partial) && aligned16(out), "partial/out must be 16-byte aligned");
-    const int64_t total = tokens * (n / 4);
-    const int64_t blocks = (total + 255) / 256;
-    combine_routes_kernel<<<(unsigned) (blocks < 65536 ? blocks : 65536), 256, 0, as_stream(stream)>>>(
-        reinterpret_cast<const float4*>(partial), reinterpret_cast<float4*>(out), topk_ids, ids_dtype, n_experts,
-        tokens, topk, n / 4);
+    EXL3_CHECK(topk <= COMBINE_MAX_TOPK, "combine: topk above %d", COMBINE_MAX_TOPK);
+    const int64_t blocks = std::min<int64_t>(tokens, 65536);
+    const auto* p4 = reinterpret_cast<const float4*>(partial);
+    auto* o4 = reinterpret_cast<float4*>(out);
+    if (topk == 8)
+        combine_routes_kernel<8><<<(unsigned) blocks, COMBINE_THREADS, 0, as_stream(stream)>>>(
+            p4, o4, topk_ids, ids_dtype, n_experts, tokens, topk, n / 4);
+    else
+        combine_routes_kernel<0><<<(unsigned) blocks, COMBINE_THREADS, 0, as_stream(stream)>>>(
+            p4, o4, topk_ids, ids_dtype, n_experts, tokens, topk, n / 4);
     return hip_status("combine_routes");
 }
 

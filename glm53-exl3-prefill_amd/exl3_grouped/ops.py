@@ -255,11 +255,10 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
     out[r] (out [rows, n_tensors*N], caller-zeroed); mode 4 (new): mode 0 into a T16-layout out (what act_had reads
     with gu_layout=1). tile_rows (new): rows per block-table entry, 128 for
     build_blocks' table (the reference's), 256 or 512 for a build_tiles(..., 256 | 512) table (512 runs the 8-wave
-    kernel), 64 in modes 0, 1 and 3 (a thin kernel for small tiles, 16 rows per wave). a_layout (new): 0 row-major a,
+    kernel), 64 (a thin kernel for small tiles, 16 rows per wave). a_layout (new): 0 row-major a,
     1 T16 (a from row_had / act_had with dst_layout=1; a_rows gives its logical rows). k_split (new): slices of K
     whose partial products are added into out (modes 1 and 3 only)."""
-    _check(int(tile_rows) in (128, 256, 512) or (int(tile_rows) == 64 and mode in (0, 1, 3, 4)),
-           "tile_rows must be 128, 256 or 512 (or 64 in modes 0, 1, 3 and 4)")
+    _check(int(tile_rows) in (64, 128, 256, 512), "tile_rows must be 64, 128, 256 or 512")
     _check(int(k_split) >= 1 and int(k_split) <= a.size(1) // 64, "k_split must be in [1, K / 64]")
     _check(int(k_split) == 1 or mode in (1, 3), "k_split > 1 needs mode 1 or 3")
     _check(a_layout in (0, 1), "unknown layout")

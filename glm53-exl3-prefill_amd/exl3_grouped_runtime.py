@@ -12,7 +12,7 @@ Env:
   EXL3_GROUPED_PREFILL=1     enable (read by the hook)
   EXL3_GROUPED_DECODE=0      leave decode calls (tokens <= cap) to the original path (default: moe_decode)
   EXL3_GROUPED_THIN=0        run every expert tile on the main GEMM kernel (default: an expert's last tile of <= 64
-                             rows runs on the thin kernel, four workgroups per CU, in a second launch; atomic scatter)
+                             rows runs on the thin kernel, four workgroups per CU, in a second launch)
   EXL3_GROUPED_SCATTER=...   down-projection output: "atomic" (fp32 atomic scatter by token, the reference's
                              method) or "combine" (per-route fp32 rows + a fixed-order sum per token: deterministic)
   EXL3_GROUPED_WORKSPACE=0   allocate the prefill intermediates per call (default: one reused buffer per device)
@@ -149,7 +149,7 @@ def reserve_prefill_workspace(device, tokens: int, topk: int, n_experts: int, hi
     call, e.g. ahead of memory profiling or graph capture, so that no later call grows it. Returns the buffer."""
     scatter = scatter or scatter_mode()
     tr = rows_per_tile or tile_rows()
-    thin = thin_tiles_enabled() and scatter == "atomic"
+    thin = thin_tiles_enabled()
     sizing = _Carve()
     _prefill_plan(_load_ext(), tokens, hidden, topk, n_experts, inter, tr, scatter, thin)(sizing)
     return _prefill_workspace(torch.device(device), sizing.off)
@@ -173,7 +173,9 @@ def _prefill_plan(gp, T: int, K: int, topk: int, E: int, I: int, tr: int, scatte
             thin_row0=take((min(E, R),), torch.int32) if thin else None,
             meta=take((3 if thin else 2,), torch.int32),
             # the GEMMs' activation operands (h13, act) and gu in the T16 layout, which makes their loads contiguous
-            h13=take((R16, K), torch.float16), gu=take((R16, 2 * I), torch.float16), act=take((R16, I), torch.float16))
+            h13=take((R16, K), torch.float16), gu=take((R16, 2 * I), torch.float16), act=take((R16, I), torch.float16),
+            # the combine mode's per-route fp32 rows of the down projection
+            partial=take((R, K), torch.float32) if scatter == "combine" else None)
     return plan
 
 
@@ -211,7 +213,7 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     tr = rows_per_tile or tile_rows()
     if tr not in TILE_ROWS_CHOICES:
         raise RuntimeError(f"rows_per_tile must be one of {TILE_ROWS_CHOICES}, got {tr}")
-    thin = (thin_tiles_enabled() if thin_tiles is None else thin_tiles) and scatter == "atomic"
+    thin = thin_tiles_enabled() if thin_tiles is None else thin_tiles
     B = _prefill_buffers(dev, _prefill_plan(gp, T, K, topk, E, I, tr, scatter, thin))
     token_sorted, weight_sorted, expert_of_row = B["token_sorted"], B["weight_sorted"], B["expert_of_row"]
     counts, expert_row0, route_index = B["counts"], B["expert_row0"], B["route_index"]
@@ -222,9 +224,9 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     out = None
     if thin:
         # each expert's last tile of <= 64 rows goes to a second table, run by the thin kernel; the same launch
-        # clears the fp32 output the down scatter adds into
+        # clears the fp32 output the atomic down scatter adds into
         thin_expert, thin_row0 = B["thin_expert"], B["thin_row0"]
-        out = torch.empty(T, K, dtype=torch.float32, device=dev)
+        out = torch.empty(T, K, dtype=torch.float32, device=dev) if scatter == "atomic" else None
         gp.build_tiles_split(counts, block_expert, block_row0, thin_expert, thin_row0, meta, tr, THIN_ROWS, zero=out)
     else:
         gp.build_tiles(counts, block_expert, block_row0, meta, tr)
@@ -256,10 +258,14 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
                             tile_rows=THIN_ROWS, a_layout=1, a_rows=R)
         mark("gemm_down_scatter")
         return out
-    partial = torch.empty(R, K, dtype=torch.float32, device=dev)
+    partial = B["partial"]
     gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
                     block_expert, block_row0, counts, expert_row0, None, weight_sorted, partial, 2,
                     route_index=route_index, tile_rows=tr, a_layout=1, a_rows=R)
+    if thin:
+        gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
+                        thin_expert, thin_row0, counts, expert_row0, None, weight_sorted, partial, 2,
+                        route_index=route_index, tile_rows=THIN_ROWS, a_layout=1, a_rows=R)
     mark("gemm_down_routes")
     out = torch.empty(T, K, dtype=torch.float32, device=dev)
     gp.combine_routes(partial, out, topk, ids, E)

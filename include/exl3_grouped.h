@@ -113,7 +113,7 @@ int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_rows, int ma
 /*
  * Two row-tile tables for one launch pair (new): tile_rows-row tiles (128, 256 or 512), except that each expert's
  * last tile goes to a second table of thin_rows-row tiles (64) when it holds at most thin_rows rows;
- * the grouped GEMM runs the second table on its thin kernel (modes 0, 1, 3 with tile_rows 64). Tails are -1 as in
+ * the grouped GEMM runs the second table on its thin kernel (tile_rows 64, any mode). Tails are -1 as in
  * exl3_build_tiles; meta int32[3] = {full tiles, rows, thin tiles}. Bounds: max_full >= R/tile_rows + n_experts,
  * max_thin >= min(n_experts, R). The same launch also zeroes zero[0 .. zero_floats) (16-byte aligned, a multiple of 4
  * floats; 0 and NULL for none): the fp32 output the down GEMM's atomic scatter adds into.
@@ -192,7 +192,8 @@ int exl3_grouped_gemm(const uint16_t* a, int64_t a_rows, int size_k,
  * exl3_grouped_gemm with two extensions (new): a_layout (EXL3_LAYOUT_ROWS, or EXL3_LAYOUT_T16 for an `a` written by
  * the _ex Hadamard passes) and tile_rows, the rows per block-table entry (128: the reference's build_blocks table,
  * what exl3_grouped_gemm passes; 256 or 512: a table from exl3_build_tiles(..., 256 | 512, ...); 512-row tiles run
- * an 8-wave kernel). Same modes and outputs.
+ * an 8-wave kernel; 64: a table from exl3_build_tiles(..., 64, ...) or the thin table of exl3_build_tiles_split, run
+ * by a thin kernel with 16 rows per wave). Same modes and outputs.
  */
 int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,
                          const uint16_t* packed_gate, const uint16_t* packed_up, int64_t expert_stride_words,
@@ -209,8 +210,8 @@ int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_k, int a_la
  * partial product and adds it to the output, so k_split > 1 needs an accumulating mode: EXL3_GEMM_SCATTER_F32, or
  * EXL3_GEMM_ATOMIC_F32 -- out fp32 [a_rows, n_tensors*N_each], caller-zeroed,
  *        out[r, which*N_each + n] += H128_n(a[r] @ W'_e,which) / sqrt(128) * svh_e,which[n]
- * (valid with k_split == 1 too; tile_rows 128 or 256). Modes 0, 1 and 3 also take tile_rows 64: a table from
- * exl3_build_tiles(..., 64, ...), run by a thin kernel (16 rows per wave, four workgroups per CU) for small tiles.
+ * (valid with k_split == 1 too; tile_rows 64, 128 or 256; 64 runs the thin kernel, 16 rows per wave and four
+ * workgroups per CU, for small tiles).
  * 1 <= k_split <= size_k / 64; the slice count used is
  * ceil(K_stages / per_slice) with per_slice = ceil(K_stages / k_split) rounded up to even (K_stages = size_k / 32).
  */

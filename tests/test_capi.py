@@ -85,9 +85,6 @@ def test_grouped_gemm_contract():
              sg=FAKE, su=None, ss=256, be=FAKE, br=FAKE, mb=10, tile_rows=96, counts=FAKE, row0=FAKE, E=8, tok=FAKE,
              rw=FAKE, ri=None, out=FAKE, out_rows=64, mode=1)
     assert "tile_rows" in rc_and_msg("exl3_grouped_gemm_ex", *a.values(), None)[1]
-    a.update(tile_rows=64, mode=2)                                      # no 64-row tiles for per-route rows
-    assert "tile_rows" in rc_and_msg("exl3_grouped_gemm_ex", *a.values(), None)[1]
-    a.update(mode=1)
     a.update(tile_rows=256, a_layout=2)
     assert "layout" in rc_and_msg("exl3_grouped_gemm_ex", *a.values(), None)[1]
     assert "layout" in rc_and_msg("exl3_row_had_ex", FAKE, FAKE, FAKE, FAKE, FAKE, 256, 256, 4, 256, 1, 5, None)[1]

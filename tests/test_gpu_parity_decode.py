@@ -264,8 +264,8 @@ def test_split_rejections(dev):
         gp.grouped_gemm(*args, torch.zeros(R, 2 * I, device=dev), 3, a_layout=1, a_rows=R, k_split=H // 64 + 1)
     with pytest.raises(RuntimeError, match="mode 3"):
         gp.grouped_gemm(*args, torch.zeros(R, 2 * I, device=dev), 3, a_layout=1, a_rows=R, tile_rows=512)
-    with pytest.raises(RuntimeError, match="64 in modes 0, 1, 3 and 4"):
-        gp.grouped_gemm(*args, torch.zeros(R, I, device=dev), 2, a_layout=1, a_rows=R, tile_rows=64)
+    with pytest.raises(RuntimeError, match="tile_rows must be 64, 128, 256 or 512"):
+        gp.grouped_gemm(*args, torch.zeros(R, I, device=dev), 2, a_layout=1, a_rows=R, tile_rows=96)
 
 
 # ------------------------------------------------------------------------------------------- the decode op
