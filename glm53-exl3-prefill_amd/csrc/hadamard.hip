@@ -144,22 +144,16 @@ void row_had_t16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__
         for (int i = 0; i < 4; ++i)
         {
             const int c = blk * 128 + 8 * (4 * i + cq);
-            float xs[8], ss[8];
-            unpack8(*reinterpret_cast<const uint4*>(src + srow * K + c), xs);
-            unpack8(*reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + c), ss);
-            #pragma unroll
-            for (int j = 0; j < 8; ++j) x[8 * i + j] = xs[j] * ss[j];
+            mul8_stage1(*reinterpret_cast<const uint4*>(src + srow * K + c),
+                        *reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + c), x + 8 * i);
         }
-        had128_t16(x, lane);
+        had128_t16_from2_unscaled(x);
         if (g * 16 + rl < rows)
             #pragma unroll
             for (int i = 0; i < 4; ++i)
             {
-                float o[8];
-                #pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = x[8 * i + j];
                 const int64_t chunk = g * (K / 8) + blk * 16 + 4 * i + cq;
-                *reinterpret_cast<uint4*>(dst + chunk * 128 + rl * 8) = pack8(o);
+                *reinterpret_cast<uint4*>(dst + chunk * 128 + rl * 8) = pack8_scaled(x + 8 * i);
             }
     }
 }

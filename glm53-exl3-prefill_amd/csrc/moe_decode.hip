@@ -267,22 +267,16 @@ void decode_prep_tiny_kernel(const uint16_t* __restrict__ x, int hidden, const v
         for (int k = 0; k < 4; ++k)
         {
             const int c = blk * 128 + 8 * (4 * k + cq);
-            float xs[8], ss[8];
-            unpack8(*reinterpret_cast<const uint4*>(x + tok * hidden + c), xs);
-            unpack8(*reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + c), ss);
-            #pragma unroll
-            for (int j = 0; j < 8; ++j) v[8 * k + j] = xs[j] * ss[j];
+            mul8_stage1(*reinterpret_cast<const uint4*>(x + tok * hidden + c),
+                        *reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + c), v + 8 * k);
         }
-        had128_t16(v, lane);
+        had128_t16_from2_unscaled(v);
         if (r >= 0)
             #pragma unroll
             for (int k = 0; k < 4; ++k)
             {
-                float o[8];
-                #pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = v[8 * k + j];
                 const int64_t chunk = (int64_t) (r >> 4) * (hidden / 8) + blk * 16 + 4 * k + cq;
-                *reinterpret_cast<uint4*>(h13 + chunk * 128 + (r & 15) * 8) = pack8(o);
+                *reinterpret_cast<uint4*>(h13 + chunk * 128 + (r & 15) * 8) = pack8_scaled(v + 8 * k);
             }
     }
 }
