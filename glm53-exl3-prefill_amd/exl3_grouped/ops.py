@@ -333,6 +333,7 @@ def combine_routes(partial: torch.Tensor, out: torch.Tensor, topk: int, topk_ids
            out.is_contiguous(), "combine: fp32 contiguous tensors")
     _check(partial.dim() == 2 and partial.size(0) == T * topk and partial.size(1) == n and n % 4 == 0,
            "combine: partial must be [T*topk, N], N % 4 == 0")
+    _check(1 <= int(topk) <= 32, "combine: topk must be in [1, 32]")
     if topk_ids is not None:
         _check(topk_ids.dtype in (torch.int64, torch.int32) and topk_ids.is_contiguous() and
                topk_ids.numel() == T * topk and 0 < n_experts <= 1024, "combine: topk_ids [T, topk] int64/int32")

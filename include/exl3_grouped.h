@@ -227,7 +227,7 @@ int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a
 /*
  * Deterministic route combine (new; pairs with grouped_gemm mode 2): out[t, :] = sum_{j < topk} partial[t*topk + j, :]
  * in order j = 0, 1, ..., skipping routes whose id in topk_ids (optional, int64 or int32 [tokens, topk]) lies outside
- * [0, n_experts). partial fp32 [tokens*topk, n], out fp32 [tokens, n] (overwritten), n % 4 == 0.
+ * [0, n_experts). partial fp32 [tokens*topk, n], out fp32 [tokens, n] (overwritten), n % 4 == 0, 1 <= topk <= 32.
  */
 int exl3_combine_routes(const float* partial, float* out, const void* topk_ids, int ids_dtype, int n_experts,
                         int64_t tokens, int topk, int64_t n, void* stream);
