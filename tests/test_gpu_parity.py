@@ -642,6 +642,35 @@ def test_prefill_workspace_reuse(dev, monkeypatch):
         assert ((g - ref).norm() / ref.norm()).item() < 1e-6, n
 
 
+def test_prefill_graph_capture_replays(dev):
+    """grouped_prefill captured in a HIP graph (the prefill workspace already sized; the output clear is a kernel, no
+    memset node): replays with fresh inputs in the captured buffers match eager calls, with eager work between the
+    replays."""
+    L, x, ids, w, cfg = synth.make_config("tiny", seed=11)
+    TL = synth.to_device(L, dev)
+    xs, it, wt = t16(x, dev), t16(ids, dev), t16(w, dev)
+    rt.grouped_prefill(xs, it, wt, TL, LIMIT)
+    torch.cuda.synchronize()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(g, stream=cap):
+            out = rt.grouped_prefill(xs, it, wt, TL, LIMIT)
+    torch.cuda.current_stream().wait_stream(cap)
+    for seed in (1, 2, 3):
+        ids2, w2 = synth.make_routing(cfg["routing"], cfg["T"], cfg["E"], cfg["topk"], seed=seed)
+        xs.copy_(t16(synth.make_x(cfg["T"], cfg["H"], seed), dev))
+        it.copy_(t16(ids2, dev))
+        wt.copy_(t16(w2, dev))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        ref = rt.grouped_prefill(xs.clone(), it.clone(), wt.clone(), TL, LIMIT)
+        torch.cuda.synchronize()
+        assert ((got - ref).norm() / ref.norm()).item() < 1e-6, seed
+
+
 def test_install_engages_grouped_path(dev, monkeypatch):
     L, x, ids, w, cfg = synth.make_config("tiny", seed=5)
     ov = Fake()
