@@ -150,13 +150,15 @@ def decode_workspace_views(ws, T, k, E, H, I):
             views["h13"].view(torch.float16).view(gp.t16_rows(R), H), mb)
 
 
-@pytest.mark.parametrize("T,drop", [(1, False), (5, True), (16, False), (16, True)])
-def test_decode_fused_prep_matches_separate_launches(dev, T, drop):
+@pytest.mark.parametrize("name,T,drop", [("layer1k", 1, False), ("layer1k", 5, True), ("layer1k", 16, False),
+                                         ("layer1k", 16, True), ("tiny", 1, False), ("tiny", 63, True)])
+def test_decode_fused_prep_matches_separate_launches(dev, name, T, drop):
     """Up to 128 routes the decode op sorts, builds the tile table, clears and runs the input Hadamard in one launch,
     ranking each route by direct comparison. Its rows, tables and h13 must equal the closed-form stable sort, the
-    block table (kernel/exl3_grouped_prefill.cu:63-96) and row_had over those rows (:101-115), bit for bit."""
-    L, cfg = layer_case("layer1k", svh_scale=1 / 64)
-    TL = device_layer("layer1k", svh_scale=1 / 64)
+    block table (kernel/exl3_grouped_prefill.cu:63-96) and row_had over those rows (:101-115), bit for bit (also for
+    2 routes, and 126, not a multiple of the four ids read per step, on 8 experts)."""
+    L, cfg = layer_case(name, svh_scale=1 / 64)
+    TL = device_layer(name, svh_scale=1 / 64)
     E, H, I, k = cfg["E"], cfg["H"], cfg["I"], cfg["topk"]
     x, ids, w = inputs(cfg, T, 40 + T)
     ids = ids.copy()
