@@ -417,6 +417,20 @@ struct Mma
 };
 
 // ------------------------------------------------------------------------------------------- epilogue
+// pa = {fp16(a0 * s0), fp16(a1 * s1)}, pb = {fp16(b0 * t0), fp16(b1 * t1)}: each product rounded once, straight to
+// fp16, packed in place. A high half is written two instructions after the low half it keeps (gfx950 forwards a
+// partial register write stale to the next instruction), and an s_nop guards the last one for the code after.
+__device__ __forceinline__ void f16_products_4(float a0, float a1, float b0, float b1, float s0, float s1, float t0,
+                                               float t1, uint32_t& pa, uint32_t& pb)
+{
+    asm("v_fma_mixlo_f16 %0, %2, %6, 0\n\t"
+        "v_fma_mixlo_f16 %1, %4, %8, 0\n\t"
+        "v_fma_mixhi_f16 %0, %3, %7, 0\n\t"
+        "v_fma_mixhi_f16 %1, %5, %9, 0\n\t"
+        "s_nop 1"
+        : "=&v"(pa), "=&v"(pb) : "v"(a0), "v"(a1), "v"(b0), "v"(b1), "v"(s0), "v"(s1), "v"(t0), "v"(t1));
+}
+
 // Per 16-row group of multiplying wave mw (16 MBN rows per wave): H128 over the 128 columns of each row (lane l holds columns
 // 16 nb + 4 (l >> 4) + r: 5 butterfly stages in registers, column bit 2 across lanes l ^ 16, bit 3 across l ^ 32),
 // scale by svh / sqrt(128) (and the route weight), then store / scatter. The scatter stages each group through LDS
@@ -486,9 +500,9 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
                 uint16_t* o = reinterpret_cast<uint16_t*>(p.out) +
                               (p.out_t16 ? ((((orow >> 4) * (p.out_ld >> 3) + (c >> 3)) * 16 + (orow & 15)) * 8 + (c & 7))
                                          : orow * p.out_ld + c);
-                uint2 pk;
-                pk.x = (uint32_t) f2h(v[0]) | ((uint32_t) f2h(v[1]) << 16);
-                pk.y = (uint32_t) f2h(v[2]) | ((uint32_t) f2h(v[3]) << 16);
+                uint2 pk;                                       // fp16(x * svh / sqrt(128)), one rounding each
+                f16_products_4(x[4 * nb], x[4 * nb + 1], x[4 * nb + 2], x[4 * nb + 3], sv[4 * nb], sv[4 * nb + 1],
+                               sv[4 * nb + 2], sv[4 * nb + 3], pk.x, pk.y);
                 *reinterpret_cast<uint2*>(o) = pk;
             }
             else
