@@ -59,6 +59,27 @@ inline int device_cus()
     return n;
 }
 
+// The decode path's activation pass fused into its split-K gate|up GEMM (ATOMIC_F32 over both tensors, 64-row tiles;
+// trellis_gemm.h, act_after_last_slice): arrive is int32 [max_blocks * N / 128], zero before the call; act is fp16
+// T16 [a_rows rounded up to 16, N]; suh is suh_down with row e at suh + e * suh_stride (16-byte aligned).
+struct ActFuse
+{
+    int* arrive;
+    uint16_t* act;
+    const uint16_t* suh;
+    int64_t suh_stride;
+    float limit;
+};
+
+// exl3_grouped_gemm_split, plus the fused activation pass when `act` is not null (trellis_gemm.hip).
+int grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layout, const uint16_t* packed_gate,
+                       const uint16_t* packed_up, int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
+                       const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                       const int32_t* block_expert, const int32_t* block_row0, int max_blocks, int tile_rows,
+                       const int32_t* counts, const int32_t* expert_row0, int n_experts, const int64_t* token_sorted,
+                       const uint16_t* route_weight, const int32_t* route_index, void* out, int64_t out_rows, int mode,
+                       int k_split, const ActFuse* act, hipStream_t s);
+
 // ------------------------------------------------------------------------------------------- device helpers
 constexpr float HAD_SCALE = 0.088388347648f;     // 1/sqrt(128)
 constexpr int MAX_EXPERTS = 1024;

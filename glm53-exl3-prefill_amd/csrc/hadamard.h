@@ -1,5 +1,6 @@
 // Hadamard helpers shared by the row Hadamard passes (hadamard.hip) and the decode path's fused preparation
-// (moe_decode.hip): fp16 packing and the 128-point transform of the T16 passes.
+// (moe_decode.hip), and the activation pass shared with the decode path's gate|up GEMM (trellis_gemm.h): fp16
+// packing, the 128-point transform of the T16 passes and the clamped SwiGLU.
 #pragma once
 #include "exl3_common.h"
 
@@ -88,16 +89,88 @@ __device__ __forceinline__ uint4 pack8_scaled(const float* x)
     return r;
 }
 
-__device__ __forceinline__ void had128_t16(float (&x)[32], int lane)
+__device__ __forceinline__ void had128_t16(float (&x)[32])
 {
-    fwht_regs<1, 8>(x);
-    #pragma unroll
-    for (int i = 0; i < 32; i += 2) pair_butterfly16(x[i], x[i + 1]);
-    #pragma unroll
-    for (int i = 0; i < 32; i += 2) pair_butterfly32(x[i], x[i + 1]);
-    fwht_regs<8, 32>(x);
+    fwht_regs<1, 2>(x);
+    had128_t16_from2_unscaled(x);
     #pragma unroll
     for (int i = 0; i < 32; ++i) x[i] *= HAD_SCALE;
+}
+
+// silu(g) * u in fp32 with the hardware exp and reciprocal: the reference builds with --use_fast_math, so its
+// g / (1 + __expf(-g)) is an approximate division too (kernel/exl3_grouped_prefill.cu:135); the result is rounded to
+// fp16 next. An IEEE division here cost ~10 VALU per value in a VALU-heavy pass.
+__device__ __forceinline__ float silu_mul(float g, float u)
+{
+#if EXL3_EXACT_SILU_DIV
+    return g / (1.0f + __expf(-g)) * u;
+#else
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+#endif
+}
+
+// 8 consecutive gate|up values: fp16 as stored, or fp32 partial sums rounded to fp16 first (the reference's gu is fp16).
+// idx is the element offset of the first (8-aligned) value in gu's layout. COHERENT (fp32 only): device-scope atomic
+// loads, which read sums that other workgroups' atomic adds completed during the same launch.
+template <bool GU_F32, bool COHERENT = false>
+__device__ __forceinline__ void load_gu8(const void* gu, int64_t idx, float (&x)[8])
+{
+    if constexpr (GU_F32)
+    {
+        float v[8];
+        if constexpr (COHERENT)
+        {
+            const float* q = reinterpret_cast<const float*>(gu) + idx;
+            #pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = __hip_atomic_load(q + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        else
+        {
+            const float4* q = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(gu) + idx);
+            const float4 a = q[0], b = q[1];
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        }
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = h2f(f2h(v[j]));
+    }
+    else
+        unpack8(*reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(gu) + idx), x);
+}
+
+// Element offset of (r, c) in a T16 [*, W] matrix (c a multiple of 8 here).
+__device__ __forceinline__ int64_t t16_index(int64_t r, int64_t c, int64_t W)
+{
+    return (((r >> 4) * (W >> 3) + (c >> 3)) * 16 + (r & 15)) * 8 + (c & 7);
+}
+
+// act_had of row r over the 128-column block blk, in the T16 lane mapping (lane group cq holds columns
+// blk * 128 + 8 (4 i + cq) + j as x[8 i + j]): clamped SwiGLU of gate column c and up column I + c, rounded to fp16,
+// times suh_down, H128, times 1/sqrt(128) (pack8 rounds the result). gu is [rows, 2I]: fp16, or fp32 sums (GU_F32),
+// row-major or T16 (GU_T16); COHERENT reads fp32 sums with device-scope atomic loads (load_gu8). suh_e is the row's
+// expert's suh_down.
+template <bool GU_F32, bool GU_T16, bool COHERENT = false>
+__device__ __forceinline__ void act_had_row(const void* gu, int64_t r, int blk, int cq, int I, const uint16_t* suh_e,
+                                            float limit, float (&x)[32])
+{
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const int c = blk * 128 + 8 * (4 * i + cq);
+        float gs[8], us[8], ss[8];
+        const int64_t W = 2 * (int64_t) I;
+        load_gu8<GU_F32, COHERENT>(gu, GU_T16 ? t16_index(r, c, W) : r * W + c, gs);
+        load_gu8<GU_F32, COHERENT>(gu, GU_T16 ? t16_index(r, I + c, W) : r * W + I + c, us);
+        unpack8(*reinterpret_cast<const uint4*>(suh_e + c), ss);
+        #pragma unroll
+        for (int j = 0; j < 8; ++j)
+        {
+            const float gc = fminf(gs[j], limit);
+            const float uc = fminf(fmaxf(us[j], -limit), limit);
+            const float a = silu_mul(gc, uc);
+            x[8 * i + j] = h2f(f2h(a)) * ss[j];                 // fp16 rounding point of the reference
+        }
+    }
+    had128_t16(x);
 }
 
 }  // namespace exl3

@@ -65,18 +65,6 @@ void row_had_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst
     }
 }
 
-// silu(g) * u in fp32 with the hardware exp and reciprocal: the reference builds with --use_fast_math, so its
-// g / (1 + __expf(-g)) is an approximate division too (kernel/exl3_grouped_prefill.cu:135); the result is rounded to
-// fp16 next. An IEEE division here cost ~10 VALU per value in a VALU-heavy pass.
-__device__ __forceinline__ float silu_mul(float g, float u)
-{
-#if EXL3_EXACT_SILU_DIV
-    return g / (1.0f + __expf(-g)) * u;
-#else
-    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
-#endif
-}
-
 __global__ __launch_bounds__(HAD_THREADS)
 void act_had_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ act, const int32_t* __restrict__ expert_of_row,
                     const uint16_t* __restrict__ suh, int64_t suh_stride, int64_t rows, int I, float limit)
@@ -158,29 +146,6 @@ void row_had_t16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__
     }
 }
 
-// 8 consecutive gate|up values: fp16 as stored, or fp32 partial sums rounded to fp16 first (the reference's gu is fp16).
-// idx is the element offset of the first (8-aligned) value in gu's layout.
-template <bool GU_F32>
-__device__ __forceinline__ void load_gu8(const void* gu, int64_t idx, float (&x)[8])
-{
-    if constexpr (GU_F32)
-    {
-        const float4* q = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(gu) + idx);
-        const float4 a = q[0], b = q[1];
-        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = h2f(f2h(v[j]));
-    }
-    else
-        unpack8(*reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(gu) + idx), x);
-}
-
-// Element offset of (r, c) in a T16 [*, W] matrix (c a multiple of 8 here).
-__device__ __forceinline__ int64_t t16_index(int64_t r, int64_t c, int64_t W)
-{
-    return (((r >> 4) * (W >> 3) + (c >> 3)) * 16 + (r & 15)) * 8 + (c & 7);
-}
-
 template <bool GU_F32, bool GU_T16 = false>
 __global__ __launch_bounds__(HAD_THREADS)
 void act_had_t16_kernel(const void* __restrict__ gu, uint16_t* __restrict__ act,
@@ -200,25 +165,7 @@ void act_had_t16_kernel(const void* __restrict__ gu, uint16_t* __restrict__ act,
         const int64_t r = min(g * 16 + rl, rows - 1);
         const int e = expert_of_row ? expert_of_row[r] : 0;
         float x[32];
-        #pragma unroll
-        for (int i = 0; i < 4; ++i)
-        {
-            const int c = blk * 128 + 8 * (4 * i + cq);
-            float gs[8], us[8], ss[8];
-            const int64_t W = 2 * (int64_t) I;
-            load_gu8<GU_F32>(gu, GU_T16 ? t16_index(r, c, W) : r * W + c, gs);
-            load_gu8<GU_F32>(gu, GU_T16 ? t16_index(r, I + c, W) : r * W + I + c, us);
-            unpack8(*reinterpret_cast<const uint4*>(suh + (int64_t) e * suh_stride + c), ss);
-            #pragma unroll
-            for (int j = 0; j < 8; ++j)
-            {
-                const float gc = fminf(gs[j], limit);
-                const float uc = fminf(fmaxf(us[j], -limit), limit);
-                const float a = silu_mul(gc, uc);
-                x[8 * i + j] = h2f(f2h(a)) * ss[j];                 // fp16 rounding point of the reference
-            }
-        }
-        had128_t16(x, lane);
+        act_had_row<GU_F32, GU_T16>(gu, r, blk, cq, I, suh + (int64_t) e * suh_stride, limit, x);
         if (g * 16 + rl < rows)
             #pragma unroll
             for (int i = 0; i < 4; ++i)

@@ -48,7 +48,8 @@ int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
 struct DecodeLayout
 {
     int64_t sort_ws, token_sorted, weight_sorted, expert_of_row, counts, expert_row0, block_expert, block_row0, meta,
-        h13, gu, act, total;
+        h13, gu, act_arrive, act, total;
+    int64_t gu_clear_floats;       // gu and the act arrival counts after it: one region the preparation clears
     int64_t sort_ws_bytes;
     int max_blocks;
 };
@@ -72,7 +73,11 @@ DecodeLayout decode_layout(int64_t tokens, int topk, int n_experts, int hidden, 
     L.block_row0 = take((int64_t) L.max_blocks * 4);
     L.meta = take(8);
     L.h13 = take(r16 * hidden * 2);
-    L.gu = take(R * 2 * (int64_t) inter * 4);
+    const int64_t gu_bytes = R * 2 * (int64_t) inter * 4;                     // a multiple of 16
+    const int64_t arrive_bytes = ((int64_t) L.max_blocks * (inter / 128) * 4 + 15) / 16 * 16;
+    L.gu = take(gu_bytes + arrive_bytes);
+    L.act_arrive = L.gu + gu_bytes;
+    L.gu_clear_floats = (gu_bytes + arrive_bytes) / 4;
     L.act = take(r16 * inter * 2);
     L.total = o;
     return L;
@@ -329,10 +334,12 @@ extern "C" int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, co
     auto* meta = reinterpret_cast<int32_t*>(at(L.meta));
     auto* h13 = reinterpret_cast<uint16_t*>(at(L.h13));
     auto* gu = reinterpret_cast<float*>(at(L.gu));
+    auto* act_arrive = reinterpret_cast<int*>(at(L.act_arrive));
     auto* act = reinterpret_cast<uint16_t*>(at(L.act));
 
-    // accumulation targets: out [tokens, hidden] and gu [R, 2 inter], both whole float4s
-    const int64_t n_out = tokens * hidden, n_gu = R * 2 * inter;
+    // accumulation targets, cleared by the preparation: out [tokens, hidden] and gu [R, 2 inter] followed by the
+    // activation pass's arrival counts, both whole float4s
+    const int64_t n_out = tokens * hidden, n_gu = L.gu_clear_floats;
     int rc;
     if (R <= TINY_ROUTES)
     {
@@ -381,12 +388,13 @@ extern "C" int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, co
     }
     const int target = target_workgroups();
     const int gu_split = k_split_for((int64_t) L.max_blocks * 2 * (inter / 128), hidden / 32, target);
-    rc = exl3_grouped_gemm_split(h13, R, hidden, EXL3_LAYOUT_T16, packed_gate, packed_up, w13_expert_stride_words,
-                                 hidden / 16, inter / 16, bits, svh_gate, svh_up, svh13_stride, block_expert,
-                                 block_row0, L.max_blocks, DECODE_TILE_ROWS, counts, expert_row0, n_experts,
-                                 token_sorted, weight_sorted, nullptr, gu, R, EXL3_GEMM_ATOMIC_F32, gu_split, stream);
-    if (rc) return rc;
-    rc = exl3_act_had_f32(gu, 2 * (int64_t) inter, act, expert_of_row, suh_down, suh2_stride, R, inter, limit, stream);
+    // gate|up slices add into the fp32 gu; the last workgroup of each (row tile, 128-column block) computes that block
+    // of act from the finished sums (the activation pass, without a launch of its own)
+    const ActFuse fuse{act_arrive, act, suh_down, suh2_stride, limit};
+    rc = grouped_gemm_split(h13, R, hidden, EXL3_LAYOUT_T16, packed_gate, packed_up, w13_expert_stride_words,
+                            hidden / 16, inter / 16, bits, svh_gate, svh_up, svh13_stride, block_expert, block_row0,
+                            L.max_blocks, DECODE_TILE_ROWS, counts, expert_row0, n_experts, token_sorted, weight_sorted,
+                            nullptr, gu, R, EXL3_GEMM_ATOMIC_F32, gu_split, &fuse, s);
     if (rc) return rc;
     const int down_split = k_split_for((int64_t) L.max_blocks * (hidden / 128), inter / 32, target);
     return exl3_grouped_gemm_split(act, R, inter, EXL3_LAYOUT_T16, packed_down, nullptr, w2_expert_stride_words,

@@ -19,12 +19,15 @@
 //     store, fp32 per-route store, or fp32 atomics staged through LDS so each atomic instruction covers 64 consecutive
 //     floats of one output row.
 //   * Workgroups are laid out XCD-aware: the column tiles of one row tile share an XCD (and its L2).
+//   * Optionally (the decode path's split-K gate|up on 64-row tiles) the workgroup that adds the last K slice of a
+//     (row tile, 128-column block) pair of gate and up computes that block of the activation (act_had) itself.
 //   * Activations and trellis words are read through buffer resources: fixed per-lane offsets plus a scalar stage
 //     offset, and zero instead of a fault outside the operand.
 // Variants of the same kernel: 16 rows per wave (64-row tiles, four workgroups per CU) for small tiles, and 8 waves
 // (512-row tiles, one workgroup per CU, each wave decoding one chunk per lane) for 512-row tiles and large dense GEMMs.
 #pragma once
 #include "exl3_common.h"
+#include "hadamard.h"
 #include "trellis_decode.h"
 
 #include <algorithm>
@@ -98,6 +101,12 @@ struct GemmParams
     void* out;
     int64_t out_ld;                // elements per output row
     int out_t16;                   // STORE_F16: out in the T16 layout (16-row x 8-column blocks), width out_ld
+    // act_had fused into ATOMIC_F32 gate|up on 64-row tiles (act_arrive null: not fused)
+    int* act_arrive;               // arrivals per (row tile, 128-column block), zero before the launch
+    uint16_t* act_out;             // act fp16, T16 layout, width n_tiles_each * 128
+    const uint16_t* act_suh;       // suh_down, row e at act_suh + e * act_suh_stride
+    int64_t act_suh_stride;
+    float act_limit;
 };
 
 // In-place Walsh-Hadamard transform of 32 values (Sylvester order over the index bits).
@@ -533,6 +542,45 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
     }
 }
 
+// act_had fused into the split-K gate|up GEMM of 64-row tiles (ATOMIC_F32 into fp32 gu, both tensors). Every
+// workgroup of a (row tile, column block nt) pair -- gate and up, each K slice -- counts its arrival after its adds;
+// the one that arrives last (2 k_split arrivals) computes act for the tile's rows over block nt with the activation
+// pass's own per-row arithmetic (act_had_row), so the result is the separate pass's. Wave w takes rows 16 w .. + 15.
+// No workgroup waits for another: the last one simply goes on.
+// Ordering without device-wide cache maintenance (an agent-scope fence writes back and invalidates the whole L2 of
+// the XCD, which every workgroup here would pay): an arriving workgroup waits until its adds are acknowledged
+// (vmcnt), then counts with a returning device-scope atomic; the last one reads the sums with device-scope atomic
+// loads (global loads at device scope, which is also what the compiler makes of an idempotent device-scope
+// read-modify-write), so it sees every add that was acknowledged before its arrival count.
+__device__ __forceinline__ void act_after_last_slice(const GemmParams& p, const Tile& t, int group, int wave, int lane)
+{
+    __shared__ int last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's adds are performed before the arrival
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(p.act_arrive + (int64_t) group * p.n_tiles_each + t.nt, 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == 2 * max(p.k_split, 1) - 1;
+    __syncthreads();
+    if (!last) return;                                  // uniform over the workgroup
+    const int I = p.n_tiles_each * TILE_N;
+    const int rl = lane & 15, cq = lane >> 4;
+    const int g0 = 16 * wave;
+    if (g0 >= t.rows_valid) return;
+    const int64_t r = (int64_t) t.row0 + min(g0 + rl, t.rows_valid - 1);
+    float x[32];
+    act_had_row<true, false, true>(p.out, r, t.nt, cq, I, p.act_suh + (int64_t) t.e * p.act_suh_stride, p.act_limit, x);
+    if (g0 + rl >= t.rows_valid) return;
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        float o[8];
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = x[8 * i + j];
+        const int64_t chunk = (r >> 4) * (I / 8) + t.nt * 16 + 4 * i + cq;
+        *reinterpret_cast<uint4*>(p.act_out + chunk * 128 + (r & 15) * 8) = pack8(o);
+    }
+}
+
 // ------------------------------------------------------------------------------------------- kernel
 // 128- and 256-row tiles: every wave decodes a quarter of each stage and multiplies its own 64 rows; two workgroups
 // share a CU. Pipeline of stage s: barrier; read stage s's weight fragments; decode stage s+1 while stage s's MFMAs run;
@@ -646,8 +694,18 @@ void trellis_gemm_kernel(const GemmParams p)
     else mainloop(std::integral_constant<int, 0>{});
 
     if constexpr (atomic_mode(MODE)) __syncthreads();            // decoded tiles are dead; LDS becomes staging
+    float* const stage = reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW);
+    if constexpr (MODE == MODE_ATOMIC_F32 && MBN == 1 && WAVES == 4)
+    {
+        if (p.act_arrive)                                        // every wave goes on to the arrival barrier
+        {
+            if (n_w > 0) epilogue<MODE, MBN, GSTRIDE>(p, t, wave, lane, acc, stage);
+            act_after_last_slice(p, t, group, wave, lane);
+            return;
+        }
+    }
     if (n_w == 0) return;
-    epilogue<MODE, MBN, GSTRIDE>(p, t, wave, lane, acc, reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW));
+    epilogue<MODE, MBN, GSTRIDE>(p, t, wave, lane, acc, stage);
 }
 
 // 512-row tiles run the 8-wave variant, 128- and 256-row tiles the 4-wave kernel (the only one built for ATOMIC_F32,

@@ -130,15 +130,14 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15)
 
 using namespace exl3;
 
-extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,
-                                       const uint16_t* packed_gate, const uint16_t* packed_up,
-                                       int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
-                                       const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
-                                       const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
-                                       int tile_rows, const int32_t* counts, const int32_t* expert_row0,
-                                       int n_experts, const int64_t* token_sorted, const uint16_t* route_weight,
-                                       const int32_t* route_index, void* out, int64_t out_rows, int mode,
-                                       int k_split, void* stream)
+namespace exl3 {
+int grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layout, const uint16_t* packed_gate,
+                       const uint16_t* packed_up, int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
+                       const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                       const int32_t* block_expert, const int32_t* block_row0, int max_blocks, int tile_rows,
+                       const int32_t* counts, const int32_t* expert_row0, int n_experts, const int64_t* token_sorted,
+                       const uint16_t* route_weight, const int32_t* route_index, void* out, int64_t out_rows, int mode,
+                       int k_split, const ActFuse* act, hipStream_t s)
 {
     EXL3_CHECK(tile_rows == 64 || tile_rows == 128 || tile_rows == 256 || tile_rows == 512,
                "tile_rows must be 64, 128, 256 or 512");
@@ -176,7 +175,19 @@ extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int si
                "k_split > 1 needs an accumulating mode (1: fp32 atomic scatter, 3: fp32 atomic rows)");
     p.kb_per_split = ((total_kb + k_split - 1) / k_split + 1) / 2 * 2;
     p.k_split = (total_kb + p.kb_per_split - 1) / p.kb_per_split;
-    hipStream_t s = as_stream(stream);
+    if (act)
+    {
+        EXL3_CHECK(mode == EXL3_GEMM_ATOMIC_F32 && n_tensors == 2 && tile_rows == 64,
+                   "internal: the fused activation pass runs on mode 3 over gate|up with 64-row tiles");
+        EXL3_CHECK(act->arrive && act->act && act->suh, "null pointer");
+        EXL3_CHECK(aligned16(act->act) && aligned16(act->suh) && act->suh_stride % 8 == 0,
+                   "act and suh_down must be 16-byte aligned");
+        p.act_arrive = act->arrive;
+        p.act_out = act->act;
+        p.act_suh = act->suh;
+        p.act_suh_stride = act->suh_stride;
+        p.act_limit = act->limit;
+    }
     int rc;
     if (mode == EXL3_GEMM_STORE_F16 || mode == EXL3_GEMM_STORE_F16_T16)
     {
@@ -215,6 +226,23 @@ extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int si
                     "rows) or 4 (fp16 store, T16 layout)");
     if (rc != EXL3_OK) return rc;
     return hip_status("grouped_gemm");
+}
+}  // namespace exl3
+
+extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,
+                                       const uint16_t* packed_gate, const uint16_t* packed_up,
+                                       int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
+                                       const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                                       const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
+                                       int tile_rows, const int32_t* counts, const int32_t* expert_row0,
+                                       int n_experts, const int64_t* token_sorted, const uint16_t* route_weight,
+                                       const int32_t* route_index, void* out, int64_t out_rows, int mode,
+                                       int k_split, void* stream)
+{
+    return grouped_gemm_split(a, a_rows, size_k, a_layout, packed_gate, packed_up, expert_stride_words, tiles_k,
+                              tiles_n, bits, svh_gate, svh_up, svh_stride, block_expert, block_row0, max_blocks,
+                              tile_rows, counts, expert_row0, n_experts, token_sorted, route_weight, route_index, out,
+                              out_rows, mode, k_split, nullptr, as_stream(stream));
 }
 
 extern "C" int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,

@@ -132,18 +132,28 @@ def test_route_prep_small_bit_exact(dev, kind, T, E, k, tile_rows):
         assert not za.any() and not zb.any()
 
 
-def decode_workspace_views(ws, T, k, E, H, I):
-    """The decode workspace's sorted routes, tables, meta and h13, at the offsets exl3_moe_decode lays them out
-    (moe_decode.hip decode_layout: each buffer 256-byte aligned, in this order)."""
+def decode_workspace_buffers(ws, T, k, E, H, I):
+    """The decode workspace's buffers by name, at the offsets exl3_moe_decode lays them out (moe_decode.hip
+    decode_layout: each buffer 256-byte aligned, in this order; gu is followed by the activation pass's arrival
+    counts, one int32 per (row tile, 128-column block), in the same buffer)."""
     R = T * k
     mb = min(E, R) + R // 64
     sizes = [("sort", gp.sort_routes_workspace_bytes(T, k, E)), ("ts", R * 8), ("ws", R * 2), ("eor", R * 4),
              ("counts", E * 4), ("row0", E * 4), ("be", mb * 4), ("br", mb * 4), ("meta", 8),
-             ("h13", gp.t16_rows(R) * H * 2)]
+             ("h13", gp.t16_rows(R) * H * 2), ("gu", R * 2 * I * 4 + (mb * (I // 128) * 4 + 15) // 16 * 16),
+             ("act", gp.t16_rows(R) * I * 2)]
     views, o = {}, 0
     for name, n in sizes:
         views[name] = ws[o:o + n]
         o += (n + 255) // 256 * 256
+    assert ws.numel() >= o
+    return views, mb
+
+
+def decode_workspace_views(ws, T, k, E, H, I):
+    """The decode workspace's sorted routes, tables, meta and h13."""
+    R = T * k
+    views, mb = decode_workspace_buffers(ws, T, k, E, H, I)
     return (views["ts"].view(torch.int64), views["ws"].view(torch.float16), views["eor"].view(torch.int32),
             views["counts"].view(torch.int32), views["row0"].view(torch.int32), views["be"].view(torch.int32),
             views["br"].view(torch.int32), views["meta"].view(torch.int32)[:2],
@@ -185,6 +195,41 @@ def test_decode_fused_prep_matches_separate_launches(dev, name, T, drop):
     rows = int(rmeta[1])                     # the valid rows: the tail's h13 is never read
     t16 = lambda a: a.view(-1, H // 8, 16, 8).permute(0, 2, 1, 3).reshape(-1, H)[:rows]
     assert torch.equal(t16(h13).view(torch.int16), t16(h_ref).view(torch.int16))
+
+
+@pytest.mark.parametrize("name,T,drop", [("layer1k", 1, False), ("layer1k", 3, True), ("layer1k", 16, False),
+                                         ("layer1k", 40, False), ("tiny", 1, False), ("tiny", 63, True)])
+def test_decode_fused_act_matches_act_had(dev, name, T, drop):
+    """The decode op has no activation launch: the gate|up workgroup that adds the last K slice of a (row tile,
+    128-column block) computes that block of act from the finished fp32 sums. It must equal the activation pass
+    (kernel/exl3_grouped_prefill.cu:118-141, here act_had over the same fp32 gu) bit for bit on every routed row --
+    with K split into slices (1 and 3 tokens: up to 10 slices on layer1k) and unsplit (16 and 40 tokens), dropped
+    routes, and the tiny layer's 2 column blocks."""
+    L, cfg = layer_case(name, svh_scale=1 / 64)
+    TL = device_layer(name, svh_scale=1 / 64)
+    E, H, I, k = cfg["E"], cfg["H"], cfg["I"], cfg["topk"]
+    x, ids, w = inputs(cfg, T, 70 + T)
+    ids = ids.copy()
+    if drop:
+        ids[0, 0] = -1
+        ids[T - 1, k - 1] = E + 5
+    R = T * k
+    ws = torch.full((gp.moe_decode_workspace_bytes(T, k, E, H, I),), 0x5A, dtype=torch.uint8, device=dev)
+    out = gp.moe_decode(dt(x, dev).to(torch.float16), dt(ids, dev), dt(w, dev).float(), TL.w13_trellis, TL.w13_suh,
+                        TL.w13_svh, TL.w2_trellis, TL.w2_suh, TL.w2_svh, LIMIT, workspace=ws)
+    torch.cuda.synchronize()
+    views, mb = decode_workspace_buffers(ws, T, k, E, H, I)
+    gu = views["gu"][:R * 2 * I * 4].view(torch.float32).view(R, 2 * I)
+    act = views["act"].view(torch.float16).view(gp.t16_rows(R), I)
+    eor = views["eor"].view(torch.int32)
+    rows = int(views["meta"].view(torch.int32)[1].item())         # routed rows; dropped routes sit past them
+    assert rows == R - (2 if drop else 0)
+    ref = torch.full_like(act, float("nan"))
+    gp.act_had(gu, ref, eor, TL.w2_suh, LIMIT, dst_layout=1, rows=R)
+    torch.cuda.synchronize()
+    t16 = lambda a: a.view(-1, I // 8, 16, 8).permute(0, 2, 1, 3).reshape(-1, I)[:rows]
+    assert torch.equal(t16(act).view(torch.int16), t16(ref).view(torch.int16))
+    assert torch.isfinite(out).all()
 
 
 def sorted_case(cfg, T, seed, dev, tile_rows=128, routing="softmax"):
