@@ -44,8 +44,7 @@ HBM_PEAK_GBS = 8000.0
 # of the committed profile summaries): the GEMMs run full expert tiles on the main kernel and each expert's last tile
 # of <= 64 rows on the thin one.
 STAGE_KERNELS = {
-    "sort_routes": ("sort_hist_kernel", "sort_offsets_kernel", "sort_scatter_kernel"),
-    "build_blocks": ("build_tiles_split_kernel",),
+    "sort_routes": ("sort_hist_kernel", "sort_scatter_tiles_kernel"),         # + tile tables and the output clear
     "row_had": ("row_had_t16_kernel<true>",),
     "gemm_gate_up": ("trellis_gemm_kernel<{bits}, 0, false, 4, 4>", "trellis_gemm_kernel<{bits}, 0, false, 1, 4>"),
     "act_had": ("act_had_t16_kernel<false, true>",),

@@ -7,6 +7,8 @@
 //   3. scatter: each chunk re-walks its routes in index order; ranks among equal ids inside a wave come from
 //      a ballot match over the id bits, across the chunk's waves from per-wave counts in LDS, so the write
 //      order is exactly the stable order.
+// The prefill path runs passes 2 and 3 and its tile tables as one launch (sort_scatter_tiles_kernel): every scatter
+// workgroup derives its own cursors from the histograms.
 // build_blocks restates kernel/exl3_grouped_prefill.cu:63-96 with a parallel scan instead of the serial one.
 // route_topk is the router glue in front of the sort (GLM-5.3-Flash's noaux_tc top-k): one wave per token.
 #include "routes.h"
@@ -22,6 +24,10 @@ constexpr int SORT_THREADS = 256;
 constexpr int SORT_WAVES = SORT_THREADS / 64;
 constexpr int ROUTES_PER_THREAD = 8;
 constexpr int CHUNK = SORT_THREADS * ROUTES_PER_THREAD;    // routes per workgroup in passes 1 and 3
+#ifndef EXL3_PREP_CLEAR_WGS
+#define EXL3_PREP_CLEAR_WGS 8192
+#endif
+constexpr int PREP_CLEAR_WGS = EXL3_PREP_CLEAR_WGS;         // workgroups clearing the output beside the scatter
 
 __global__ __launch_bounds__(SORT_THREADS)
 void sort_hist_kernel(const void* __restrict__ ids, int ids_dtype, int64_t R, int n_experts,
@@ -223,6 +229,152 @@ void sort_scatter_kernel(const void* __restrict__ ids, int ids_dtype, const void
     scatter_chunk(ids, ids_dtype, weights, w_dtype, R, topk, n_experts, (int64_t) blockIdx.x * CHUNK, s_cursor,
                   s_wave_cnt, token_sorted, weight_sorted, expert_of_row, route_index);
     fill_tail(counts, expert_row0, n_experts, R, token_sorted, weight_sorted, expert_of_row, route_index);
+}
+
+// The prefill path's pass 2 and tile tables in one launch, after sort_hist_kernel (no offsets launch). Workgroup c <
+// n_chunks scatters chunk c: it sums the per-chunk histograms itself -- every expert's total over all chunks and over
+// the chunks before c -- and scans the totals into expert_row0, which gives the cursors sort_offsets_kernel would
+// have handed it, then writes the chunk's rows (scatter_chunk) and its share of the tail rows. Workgroup n_chunks
+// writes counts, expert_row0, the dropped count and the two tables of build_tiles_split_kernel (meta = {full tiles,
+// rows, thin tiles}); the rest clear the caller's fp32 buffer. No workgroup waits for another. Thread t owns experts
+// 4t .. 4t + 3.
+__global__ __launch_bounds__(SORT_THREADS)
+void sort_scatter_tiles_kernel(const void* __restrict__ ids, int ids_dtype, const void* __restrict__ weights,
+                               int w_dtype, int64_t R, int topk, int n_experts, int n_chunks,
+                               const int32_t* __restrict__ hist, const int32_t* __restrict__ bad_per_chunk,
+                               int32_t* __restrict__ dropped, int64_t* __restrict__ token_sorted,
+                               uint16_t* __restrict__ weight_sorted, int32_t* __restrict__ expert_of_row,
+                               int32_t* __restrict__ route_index, int32_t* __restrict__ counts,
+                               int32_t* __restrict__ expert_row0, int tile_rows, int thin_rows, int max_full,
+                               int max_thin, int32_t* __restrict__ full_expert, int32_t* __restrict__ full_row0,
+                               int32_t* __restrict__ thin_expert, int32_t* __restrict__ thin_row0,
+                               int32_t* __restrict__ meta, float4* __restrict__ zero, int64_t zero4)
+{
+    static_assert(4 * SORT_THREADS >= MAX_EXPERTS, "four experts per thread");
+    const int t = threadIdx.x;
+    const int wg = blockIdx.x;
+    if (wg > n_chunks)                                    // clear the caller's fp32 buffer
+    {
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        const int64_t step = (int64_t) (gridDim.x - n_chunks - 1) * SORT_THREADS;
+        for (int64_t i = (int64_t) (wg - n_chunks - 1) * SORT_THREADS + t; i < zero4; i += step) zero[i] = z;
+        return;
+    }
+    // totals over all chunks and over the chunks before this one (the tables workgroup: wg == n_chunks, all of them);
+    // 16 chunks per step, the thread's four experts in one 16-byte load per chunk when rows are 16-byte multiples
+    int tot[4] = {0, 0, 0, 0}, pre[4] = {0, 0, 0, 0};
+    const bool vec = (n_experts & 3) == 0;
+    for (int c0 = 0; c0 < n_chunks; c0 += 16)
+    {
+        int4 h[16];
+        #pragma unroll
+        for (int i = 0; i < 16; ++i)
+        {
+            const int c = c0 + i, e = 4 * t;
+            const int32_t* row = hist + (int64_t) c * n_experts;
+            if (c >= n_chunks || e >= n_experts) h[i] = make_int4(0, 0, 0, 0);
+            else if (vec) h[i] = *reinterpret_cast<const int4*>(row + e);
+            else h[i] = make_int4(row[e], e + 1 < n_experts ? row[e + 1] : 0, e + 2 < n_experts ? row[e + 2] : 0,
+                                  e + 3 < n_experts ? row[e + 3] : 0);
+        }
+        #pragma unroll
+        for (int i = 0; i < 16; ++i)
+        {
+            const int m = (c0 + i < wg) ? -1 : 0;          // chunks before this one count towards its cursors
+            tot[0] += h[i].x; tot[1] += h[i].y; tot[2] += h[i].z; tot[3] += h[i].w;
+            pre[0] += h[i].x & m; pre[1] += h[i].y & m; pre[2] += h[i].z & m; pre[3] += h[i].w & m;
+        }
+    }
+    int nfull[4], nthin[4];
+    #pragma unroll
+    for (int j = 0; j < 4; ++j)
+    {
+        const int rem = tot[j] % tile_rows;
+        nthin[j] = (rem > 0 && rem <= thin_rows) ? 1 : 0;
+        nfull[j] = tot[j] / tile_rows + ((rem > thin_rows) ? 1 : 0);
+    }
+    const int my_rows = tot[0] + tot[1] + tot[2] + tot[3];
+    const int my_full = nfull[0] + nfull[1] + nfull[2] + nfull[3];
+    const int my_thin = nthin[0] + nthin[1] + nthin[2] + nthin[3];
+    __shared__ int32_t s_rows[SORT_THREADS], s_full[SORT_THREADS], s_thin[SORT_THREADS];
+    s_rows[t] = my_rows;
+    s_full[t] = my_full;
+    s_thin[t] = my_thin;
+    __syncthreads();
+    for (int d = 1; d < SORT_THREADS; d <<= 1)            // inclusive scans over the threads
+    {
+        const int vr = (t >= d) ? s_rows[t - d] : 0;
+        const int vf = (t >= d) ? s_full[t - d] : 0;
+        const int vt = (t >= d) ? s_thin[t - d] : 0;
+        __syncthreads();
+        s_rows[t] += vr;
+        s_full[t] += vf;
+        s_thin[t] += vt;
+        __syncthreads();
+    }
+    int row0 = s_rows[t] - my_rows;
+    const int64_t n_rows = s_rows[SORT_THREADS - 1];
+    if (wg == n_chunks)
+    {
+        int f0 = s_full[t] - my_full, t0 = s_thin[t] - my_thin;
+        #pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+            const int e = 4 * t + j;
+            if (e < n_experts)
+            {
+                counts[e] = tot[j];
+                expert_row0[e] = row0;
+                for (int i = 0; i < nfull[j]; ++i)
+                    if (f0 + i < max_full) { full_expert[f0 + i] = e; full_row0[f0 + i] = row0 + i * tile_rows; }
+                if (nthin[j] && t0 < max_thin)
+                {
+                    thin_expert[t0] = e;
+                    thin_row0[t0] = row0 + (tot[j] / tile_rows) * tile_rows;
+                }
+            }
+            row0 += tot[j];
+            f0 += nfull[j];
+            t0 += nthin[j];
+        }
+        const int n_full = s_full[SORT_THREADS - 1], n_thin = s_thin[SORT_THREADS - 1];
+        if (t == 0)
+        {
+            meta[0] = n_full;
+            meta[1] = (int) n_rows;
+            meta[2] = n_thin;
+            int d = 0;
+            for (int c = 0; c < n_chunks; ++c) d += bad_per_chunk[c];
+            *dropped = d;
+        }
+        for (int b = n_full + t; b < max_full; b += SORT_THREADS) full_expert[b] = -1;
+        for (int b = n_thin + t; b < max_thin; b += SORT_THREADS) thin_expert[b] = -1;
+        return;
+    }
+    __shared__ int32_t s_cursor[MAX_EXPERTS];
+    __shared__ int32_t s_wave_cnt[SORT_WAVES][MAX_EXPERTS];
+    #pragma unroll
+    for (int j = 0; j < 4; ++j)
+    {
+        const int e = 4 * t + j;
+        if (e < n_experts)
+        {
+            s_cursor[e] = row0 + pre[j];
+            for (int w = 0; w < SORT_WAVES; ++w) s_wave_cnt[w][e] = 0;
+        }
+        row0 += tot[j];
+    }
+    __syncthreads();
+    scatter_chunk(ids, ids_dtype, weights, w_dtype, R, topk, n_experts, (int64_t) wg * CHUNK, s_cursor, s_wave_cnt,
+                  token_sorted, weight_sorted, expert_of_row, route_index);
+    // rows past the routed ones (dropped routes): token 0, weight 0, expert 0, route 0, as fill_tail writes them
+    for (int64_t r = n_rows + (int64_t) wg * SORT_THREADS + t; r < R; r += (int64_t) n_chunks * SORT_THREADS)
+    {
+        token_sorted[r] = 0;
+        weight_sorted[r] = 0;
+        expert_of_row[r] = 0;
+        if (route_index) route_index[r] = 0;
+    }
 }
 
 // The decode path's route preparation in one launch, for R <= CHUNK routes. Workgroup 0 sorts: expert histogram in
@@ -601,6 +753,52 @@ extern "C" int exl3_build_tiles_split(const int32_t* counts, int n_experts, int 
         counts, n_experts, tile_rows, thin_rows, max_full, max_thin, full_expert, full_row0, thin_expert, thin_row0,
         meta, reinterpret_cast<float4*>(zero), zero4);
     return hip_status("build_tiles_split");
+}
+
+extern "C" int exl3_sort_routes_split_tiles(const void* topk_ids, int ids_dtype, const void* topk_weights,
+                                            int weights_dtype, int64_t tokens, int topk, int n_experts,
+                                            int64_t* token_sorted, uint16_t* weight_sorted, int32_t* expert_of_row,
+                                            int32_t* route_index, int32_t* counts, int32_t* expert_row0,
+                                            void* workspace, size_t workspace_bytes, int tile_rows, int thin_rows,
+                                            int max_full, int max_thin, int32_t* full_expert, int32_t* full_row0,
+                                            int32_t* thin_expert, int32_t* thin_row0, int32_t* meta, float* zero,
+                                            int64_t zero_floats, void* stream)
+{
+    EXL3_CHECK(ids_dtype == EXL3_DTYPE_I64 || ids_dtype == EXL3_DTYPE_I32, "topk_ids must be int64 or int32");
+    EXL3_CHECK(weights_dtype == EXL3_DTYPE_F32 || weights_dtype == EXL3_DTYPE_F16 || weights_dtype == EXL3_DTYPE_BF16,
+               "topk_weights must be float32, float16 or bfloat16");
+    EXL3_CHECK(tokens >= 0 && topk > 0, "bad routing shape");
+    EXL3_CHECK(n_experts > 0 && n_experts <= MAX_EXPERTS, "too many experts");
+    const int64_t R = tokens * topk;
+    EXL3_CHECK(R < (int64_t) 1 << 31, "too many routes");
+    const size_t need = exl3_sort_routes_workspace_bytes(tokens, topk, n_experts);
+    EXL3_CHECK(workspace != nullptr && workspace_bytes >= need, "sort workspace too small (%zu < %zu bytes)",
+               workspace_bytes, need);
+    EXL3_CHECK(counts && expert_row0, "null output pointer");
+    EXL3_CHECK(R == 0 || (topk_ids && topk_weights && token_sorted && weight_sorted && expert_of_row),
+               "null pointer");
+    EXL3_CHECK((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, "sort workspace must be 16-byte aligned");
+    EXL3_CHECK((tile_rows == 128 || tile_rows == 256 || tile_rows == 512) && thin_rows == 64,
+               "tile_rows must be 128, 256 or 512 and thin_rows 64");
+    EXL3_CHECK(max_full >= 0 && max_thin >= 0, "bad table sizes");
+    EXL3_CHECK(meta && (max_full == 0 || (full_expert && full_row0)) && (max_thin == 0 || (thin_expert && thin_row0)),
+               "null pointer");
+    EXL3_CHECK(zero_floats >= 0 && zero_floats % 4 == 0 && (zero_floats == 0 || zero) &&
+               (reinterpret_cast<uintptr_t>(zero) & 15) == 0, "zero must be 16-byte aligned, a multiple of 4 floats");
+    hipStream_t s = as_stream(stream);
+    int32_t* dropped = reinterpret_cast<int32_t*>(workspace);
+    int32_t* hist = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + 256);
+    const int n_chunks = (int) ((R + CHUNK - 1) / CHUNK);
+    int32_t* bad = hist + (int64_t) n_chunks * n_experts;
+    if (n_chunks > 0)
+        sort_hist_kernel<<<n_chunks, SORT_THREADS, 0, s>>>(topk_ids, ids_dtype, R, n_experts, hist, bad);
+    const int64_t zero4 = zero_floats / 4;
+    const int64_t zwgs = zero4 > 0 ? std::min<int64_t>((zero4 + SORT_THREADS - 1) / SORT_THREADS, PREP_CLEAR_WGS) : 0;
+    sort_scatter_tiles_kernel<<<(unsigned) (n_chunks + 1 + zwgs), SORT_THREADS, 0, s>>>(
+        topk_ids, ids_dtype, topk_weights, weights_dtype, R, topk, n_experts, n_chunks, hist, bad, dropped,
+        token_sorted, weight_sorted, expert_of_row, route_index, counts, expert_row0, tile_rows, thin_rows, max_full,
+        max_thin, full_expert, full_row0, thin_expert, thin_row0, meta, reinterpret_cast<float4*>(zero), zero4);
+    return hip_status("sort_routes_split_tiles");
 }
 
 extern "C" int exl3_build_blocks(const int32_t* counts, int n_experts, int max_blocks,

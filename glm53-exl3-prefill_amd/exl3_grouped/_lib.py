@@ -33,6 +33,8 @@ SIGNATURES = {
     "exl3_build_blocks": (I32, [P, I32, I32, P, P, P, P]),
     "exl3_build_tiles": (I32, [P, I32, I32, I32, P, P, P, P]),
     "exl3_build_tiles_split": (I32, [P, I32, I32, I32, I32, I32, P, P, P, P, P, P, I64, P]),
+    "exl3_sort_routes_split_tiles": (I32, [P, I32, P, I32, I64, I32, I32, P, P, P, P, P, P, P, SZ, I32, I32, I32, I32,
+                                           P, P, P, P, P, P, I64, P]),
     "exl3_row_had": (I32, [P, P, P, P, P, I64, I64, I64, I32, I32, P]),
     "exl3_row_had_ex": (I32, [P, P, P, P, P, I64, I64, I64, I32, I32, I32, P]),
     "exl3_act_had": (I32, [P, I64, P, P, P, I64, I64, I32, F32, P]),

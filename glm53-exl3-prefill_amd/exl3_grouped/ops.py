@@ -174,6 +174,55 @@ def build_tiles_split(counts: torch.Tensor, full_expert: torch.Tensor, full_row0
                   zero.numel() if zero is not None else 0, s)
 
 
+def sort_routes_split_tiles(topk_ids: torch.Tensor, topk_weights: torch.Tensor, n_experts: int,
+                            token_sorted: torch.Tensor, weight_sorted: torch.Tensor, expert_of_row: torch.Tensor,
+                            counts: torch.Tensor, expert_row0: torch.Tensor, full_expert: torch.Tensor,
+                            full_row0: torch.Tensor, thin_expert: torch.Tensor, thin_row0: torch.Tensor,
+                            meta: torch.Tensor, tile_rows: int = 256, thin_rows: int = 64,
+                            zero: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+                            route_index: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """sort_routes followed by build_tiles_split on its counts, in two launches instead of four (new): the same
+    outputs bit for bit. Returns the sort workspace (first int32: the dropped routes)."""
+    _check(topk_ids.dim() == 2 and topk_weights.shape == topk_ids.shape, "topk_ids / topk_weights must be [T, topk]")
+    _check(topk_ids.dtype in (torch.int64, torch.int32), "topk_ids must be int64 or int32")
+    _check(topk_weights.dtype in (torch.float32, torch.float16, torch.bfloat16),
+           "topk_weights must be float32, float16 or bfloat16")
+    _check(topk_ids.is_contiguous() and topk_weights.is_contiguous(), "routing tensors must be contiguous")
+    T, k = topk_ids.shape
+    R = T * k
+    _check(token_sorted.dtype == torch.int64 and weight_sorted.dtype == torch.float16 and
+           expert_of_row.dtype == torch.int32, "sorted outputs: int64 tokens, fp16 weights, int32 experts")
+    _check(token_sorted.numel() == R and weight_sorted.numel() == R and expert_of_row.numel() == R,
+           "sorted outputs must have T*topk elements")
+    _check(counts.dtype == torch.int32 and expert_row0.dtype == torch.int32 and counts.numel() == n_experts and
+           expert_row0.numel() == n_experts, "counts / expert_row0 must be int32 [E]")
+    _check(0 < n_experts <= 1024, "too many experts")
+    if route_index is not None:
+        _check(route_index.dtype == torch.int32 and route_index.numel() == R and route_index.is_contiguous(),
+               "route_index must be contiguous int32 [T*topk]")
+    for t in (full_expert, full_row0, thin_expert, thin_row0, meta):
+        _check(t.dtype == torch.int32 and t.is_contiguous(), "int32 contiguous tensors")
+    _check(full_row0.numel() >= full_expert.numel() and thin_row0.numel() >= thin_expert.numel() and
+           meta.numel() >= 3, "tables: row0 at least as long as expert, meta int32[3]")
+    _check(zero is None or (zero.dtype == torch.float32 and zero.is_contiguous() and zero.numel() % 4 == 0),
+           "zero must be fp32 contiguous with a multiple of 4 elements")
+    need = sort_routes_workspace_bytes(T, k, n_experts)
+    tensors = (topk_ids, topk_weights, token_sorted, weight_sorted, expert_of_row, counts, expert_row0, full_expert,
+               full_row0, thin_expert, thin_row0, meta) + ((zero,) if zero is not None else ())
+    dev = _require_cuda(*tensors)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    _check(workspace.numel() * workspace.element_size() >= need, "sort workspace too small")
+    with _On(dev) as s:
+        _lib.call("exl3_sort_routes_split_tiles", _p(topk_ids), _DT[topk_ids.dtype], _p(topk_weights),
+                  _DT[topk_weights.dtype], T, k, n_experts, _p(token_sorted), _p(weight_sorted), _p(expert_of_row),
+                  _p(route_index), _p(counts), _p(expert_row0), _p(workspace),
+                  workspace.numel() * workspace.element_size(), int(tile_rows), int(thin_rows), full_expert.numel(),
+                  thin_expert.numel(), _p(full_expert), _p(full_row0), _p(thin_expert), _p(thin_row0), _p(meta),
+                  _p(zero) if zero is not None else None, zero.numel() if zero is not None else 0, s)
+    return workspace
+
+
 def t16_rows(rows: int) -> int:
     """Rows a T16-layout buffer of `rows` logical rows holds (whole 16-row groups)."""
     return (rows + 15) // 16 * 16

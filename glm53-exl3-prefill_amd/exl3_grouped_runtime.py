@@ -218,19 +218,22 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     token_sorted, weight_sorted, expert_of_row = B["token_sorted"], B["weight_sorted"], B["expert_of_row"]
     counts, expert_row0, route_index = B["counts"], B["expert_row0"], B["route_index"]
     block_expert, block_row0, meta = B["block_expert"], B["block_row0"], B["meta"]
-    gp.sort_routes(ids, weights, E, token_sorted, weight_sorted, expert_of_row, counts, expert_row0,
-                   workspace=B["sort_ws"], route_index=route_index)
-    mark("sort_routes")
     out = None
     if thin:
-        # each expert's last tile of <= 64 rows goes to a second table, run by the thin kernel; the same launch
-        # clears the fp32 output the atomic down scatter adds into
+        # the sort, then the two tile tables (each expert's last tile of <= 64 rows goes to a second table, run by the
+        # thin kernel) and the clear of the fp32 output the atomic down scatter adds into: two launches in all
         thin_expert, thin_row0 = B["thin_expert"], B["thin_row0"]
         out = torch.empty(T, K, dtype=torch.float32, device=dev) if scatter == "atomic" else None
-        gp.build_tiles_split(counts, block_expert, block_row0, thin_expert, thin_row0, meta, tr, THIN_ROWS, zero=out)
+        gp.sort_routes_split_tiles(ids, weights, E, token_sorted, weight_sorted, expert_of_row, counts, expert_row0,
+                                   block_expert, block_row0, thin_expert, thin_row0, meta, tr, THIN_ROWS, zero=out,
+                                   workspace=B["sort_ws"], route_index=route_index)
+        mark("sort_routes")                               # sort, tile tables and output clear
     else:
+        gp.sort_routes(ids, weights, E, token_sorted, weight_sorted, expert_of_row, counts, expert_row0,
+                       workspace=B["sort_ws"], route_index=route_index)
+        mark("sort_routes")
         gp.build_tiles(counts, block_expert, block_row0, meta, tr)
-    mark("build_blocks")
+        mark("build_blocks")
     h13 = B["h13"]
     gp.row_had(x16, h13, token_sorted, expert_of_row, layer.w13_suh[:, 0], True, dst_layout=1, rows=R)
     mark("row_had")

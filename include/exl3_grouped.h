@@ -121,6 +121,20 @@ int exl3_build_tiles(const int32_t* counts, int n_experts, int tile_rows, int ma
 int exl3_build_tiles_split(const int32_t* counts, int n_experts, int tile_rows, int thin_rows, int max_full,
                            int max_thin, int32_t* full_expert, int32_t* full_row0, int32_t* thin_expert,
                            int32_t* thin_row0, int32_t* meta, float* zero, int64_t zero_floats, void* stream);
+/*
+ * exl3_sort_routes followed by exl3_build_tiles_split on its counts, in two launches instead of four (new; the torch
+ * glue of kernel/exl3_grouped_runtime.py:59-68 and the block table of kernel/exl3_grouped_prefill.cu:63-96 as one
+ * prefill-path preparation): the same sorted routes, counts, expert_row0, dropped count (the workspace's first int32),
+ * tables, meta and cleared buffer, bit for bit. Arguments and checks are those of the two entry points, and the
+ * workspace must be 16-byte aligned.
+ */
+int exl3_sort_routes_split_tiles(const void* topk_ids, int ids_dtype, const void* topk_weights, int weights_dtype,
+                                 int64_t tokens, int topk, int n_experts, int64_t* token_sorted,
+                                 uint16_t* weight_sorted, int32_t* expert_of_row, int32_t* route_index,
+                                 int32_t* counts, int32_t* expert_row0, void* workspace, size_t workspace_bytes,
+                                 int tile_rows, int thin_rows, int max_full, int max_thin, int32_t* full_expert,
+                                 int32_t* full_row0, int32_t* thin_expert, int32_t* thin_row0, int32_t* meta,
+                                 float* zero, int64_t zero_floats, void* stream);
 
 /*
  * Input Hadamard (pybind op row_had, kernel/exl3_grouped_prefill.cu:101-115 and :296-311):

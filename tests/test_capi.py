@@ -362,3 +362,34 @@ def test_build_tiles_split_contract():
         rc, msg = rc_and_msg("exl3_build_tiles_split", FAKE, 8, 256, 64, 10, 8, FAKE, FAKE, FAKE, FAKE, FAKE, zero, n,
                              None)
         assert rc == _lib.EXL3_ERR_ARG and "zero must be" in msg, (zero, n)
+
+
+def test_sort_routes_split_tiles_contract():
+    """The fused preparation validates like exl3_sort_routes and exl3_build_tiles_split, before any launch."""
+    need = _lib.load().exl3_sort_routes_workspace_bytes(100, 8, 288)
+
+    def call(ids_dtype=_lib.DTYPE_I64, experts=288, ws_bytes=need, tile_rows=256, thin_rows=64, fe=FAKE, zero=None,
+             n=0):
+        return rc_and_msg("exl3_sort_routes_split_tiles", FAKE, ids_dtype, FAKE, _lib.DTYPE_F32, 100, 8, experts, FAKE,
+                          FAKE, FAKE, None, FAKE, FAKE, FAKE, ws_bytes, tile_rows, thin_rows, 10, 8, fe, FAKE, FAKE,
+                          FAKE, FAKE, zero, n, None)
+
+    rc, msg = call(ws_bytes=need - 1)
+    assert rc == _lib.EXL3_ERR_ARG and "workspace" in msg
+    rc, msg = rc_and_msg("exl3_sort_routes_split_tiles", FAKE, _lib.DTYPE_I64, FAKE, _lib.DTYPE_F32, 100, 8, 288, FAKE,
+                         FAKE, FAKE, None, FAKE, FAKE, ctypes.c_void_p(0x1008), need, 256, 64, 10, 8, FAKE, FAKE, FAKE,
+                         FAKE, FAKE, None, 0, None)
+    assert rc == _lib.EXL3_ERR_ARG and "16-byte aligned" in msg
+    rc, msg = call(ids_dtype=_lib.DTYPE_F32)
+    assert rc == _lib.EXL3_ERR_ARG and "int64 or int32" in msg
+    rc, msg = call(experts=1025)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "too many experts"
+    rc, msg = call(tile_rows=64)
+    assert rc == _lib.EXL3_ERR_ARG and "tile_rows" in msg
+    rc, msg = call(thin_rows=128)
+    assert rc == _lib.EXL3_ERR_ARG and "thin_rows 64" in msg
+    rc, msg = call(fe=None)
+    assert rc == _lib.EXL3_ERR_ARG and msg == "null pointer"
+    for zero, n in ((None, 8), (FAKE, 6), (ctypes.c_void_p(0x1004), 8), (FAKE, -4)):
+        rc, msg = call(zero=zero, n=n)
+        assert rc == _lib.EXL3_ERR_ARG and "zero must be" in msg, (zero, n)

@@ -184,6 +184,82 @@ def test_build_tiles_split_bit_exact(dev, kind, T, E, k, tile_rows):
     assert (fe[len(full):] == -1).all() and (te[len(thin):] == -1).all()
 
 
+def fused_prep(ids_t, w_t, E, tile_rows, fused, zero_n=0):
+    """The prefill preparation as sort_routes + build_tiles_split (fused=False) or as sort_routes_split_tiles: every
+    output, from buffers pre-filled with sentinels."""
+    dev = ids_t.device
+    R = ids_t.numel()
+    mf, mt = R // tile_rows + E, min(E, R)
+    out = dict(ts=torch.full((R,), -3, dtype=torch.int64, device=dev),
+               ws=torch.full((R,), 7.0, dtype=torch.float16, device=dev),
+               eor=torch.full((R,), -3, dtype=torch.int32, device=dev),
+               counts=torch.full((E,), -3, dtype=torch.int32, device=dev),
+               row0=torch.full((E,), -3, dtype=torch.int32, device=dev),
+               ri=torch.full((R,), -3, dtype=torch.int32, device=dev),
+               fe=torch.full((mf,), -7, dtype=torch.int32, device=dev),
+               fr=torch.full((mf,), -7, dtype=torch.int32, device=dev),
+               te=torch.full((mt,), -7, dtype=torch.int32, device=dev),
+               tr=torch.full((mt,), -7, dtype=torch.int32, device=dev),
+               meta=torch.full((3,), -5, dtype=torch.int32, device=dev),
+               zero=torch.full((zero_n + 8,), float("nan"), dtype=torch.float32, device=dev))
+    o = out
+    z = o["zero"][4:-4] if zero_n else None
+    if fused:
+        work = gp.sort_routes_split_tiles(ids_t, w_t, E, o["ts"], o["ws"], o["eor"], o["counts"], o["row0"], o["fe"],
+                                          o["fr"], o["te"], o["tr"], o["meta"], tile_rows, 64, zero=z,
+                                          route_index=o["ri"])
+    else:
+        work = gp.sort_routes(ids_t, w_t, E, o["ts"], o["ws"], o["eor"], o["counts"], o["row0"], route_index=o["ri"])
+        gp.build_tiles_split(o["counts"], o["fe"], o["fr"], o["te"], o["tr"], o["meta"], tile_rows, 64, zero=z)
+    torch.cuda.synchronize()
+    res = {n: t.cpu().numpy() for n, t in out.items()}
+    res["dropped"] = int(work[:4].view(torch.int32).item())
+    return res
+
+
+@pytest.mark.parametrize("tile_rows", [256, 128, 512])
+@pytest.mark.parametrize("kind,T,E,k", ROUTINGS)
+def test_sort_routes_split_tiles_matches_two_ops(dev, kind, T, E, k, tile_rows):
+    """The prefill path's two-launch preparation (histogram; scatter with per-workgroup cursors + tile tables +
+    output clear) writes exactly what sort_routes followed by build_tiles_split writes (kernel/exl3_grouped_runtime.py
+    :59-68, kernel/exl3_grouped_prefill.cu:63-96), bit for bit, with int64 and int32 ids; the clear covers exactly the
+    given range."""
+    if tile_rows != 256 and kind not in ("zipf", "softmax"):
+        pytest.skip("other tile sizes: two routings suffice")
+    ids, w = synth.make_routing(kind, T, E, k, seed=T + 9)
+    wt = torch.from_numpy(w).to(dev)
+    for ids_dt in (torch.int64, torch.int32):
+        it = torch.from_numpy(ids).to(ids_dt).to(dev)
+        a = fused_prep(it, wt, E, tile_rows, fused=False, zero_n=T * 4 * 37)
+        b = fused_prep(it, wt, E, tile_rows, fused=True, zero_n=T * 4 * 37)
+        for n in a:
+            assert np.array_equal(np.atleast_1d(a[n]).view(np.uint8), np.atleast_1d(b[n]).view(np.uint8)), n
+        assert (b["zero"][4:-4] == 0).all() and np.isnan(b["zero"][:4]).all() and np.isnan(b["zero"][-4:]).all()
+    ref = O.sort_routes(ids, w, E)                      # and both against the oracle
+    for g, r in zip((b["ts"], b["ws"], b["eor"], b["counts"], b["row0"]), ref):
+        assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(r).view(np.uint8))
+
+
+def test_sort_routes_split_tiles_empty_and_dropped(dev):
+    """No routes (tables all -1, meta zero) and dropped ids (the tail rows, the dropped count), as the two ops give."""
+    a = fused_prep(torch.zeros(0, 8, dtype=torch.int64, device=dev), torch.zeros(0, 8, device=dev), 16, 256, False)
+    b = fused_prep(torch.zeros(0, 8, dtype=torch.int64, device=dev), torch.zeros(0, 8, device=dev), 16, 256, True)
+    assert b["meta"].tolist() == [0, 0, 0] and (b["fe"] == -1).all() and b["counts"].tolist() == [0] * 16
+    for n in a:
+        assert np.array_equal(np.atleast_1d(a[n]).view(np.uint8), np.atleast_1d(b[n]).view(np.uint8)), n
+    rng = np.random.default_rng(4)
+    ids = rng.integers(0, 40, (3000, 8)).astype(np.int64)
+    ids[::7, 3] = -1                                    # dropped: negative and out-of-range ids
+    ids[5::11, 6] = 40
+    w = rng.random((3000, 8)).astype(np.float32)
+    args = (torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev), 40, 256)
+    a = fused_prep(*args, fused=False, zero_n=64)
+    b = fused_prep(*args, fused=True, zero_n=64)
+    assert b["dropped"] == int((ids < 0).sum() + (ids >= 40).sum()) > 0
+    for n in a:
+        assert np.array_equal(np.atleast_1d(a[n]).view(np.uint8), np.atleast_1d(b[n]).view(np.uint8)), n
+
+
 def test_prefill_thin_tiles_match_one_table(dev):
     """Each expert's small last tile on the thin kernel gives the one-table result (the per-row arithmetic is the
     same; the down scatter's atomics may add in another order)."""
