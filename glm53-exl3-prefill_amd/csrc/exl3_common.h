@@ -71,14 +71,16 @@ struct ActFuse
     float limit;
 };
 
-// exl3_grouped_gemm_split, plus the fused activation pass when `act` is not null (trellis_gemm.hip).
+// exl3_grouped_gemm_split, plus the fused activation pass when `act` is not null and the clear of zero[0 ..
+// zero_floats) as a side job of the same launch (trellis_gemm.hip).
 int grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layout, const uint16_t* packed_gate,
                        const uint16_t* packed_up, int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
                        const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
                        const int32_t* block_expert, const int32_t* block_row0, int max_blocks, int tile_rows,
                        const int32_t* counts, const int32_t* expert_row0, int n_experts, const int64_t* token_sorted,
                        const uint16_t* route_weight, const int32_t* route_index, void* out, int64_t out_rows, int mode,
-                       int k_split, const ActFuse* act, hipStream_t s);
+                       int k_split, const ActFuse* act, hipStream_t s, float* zero = nullptr,
+                       int64_t zero_floats = 0);
 
 // ------------------------------------------------------------------------------------------- device helpers
 constexpr float HAD_SCALE = 0.088388347648f;     // 1/sqrt(128)

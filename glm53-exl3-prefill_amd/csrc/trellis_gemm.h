@@ -107,6 +107,9 @@ struct GemmParams
     const uint16_t* act_suh;       // suh_down, row e at act_suh + e * act_suh_stride
     int64_t act_suh_stride;
     float act_limit;
+    // a side job of the launch: clear zero[0 .. zero4) (float4s), a buffer a later launch accumulates into
+    float4* zero;
+    int64_t zero4;
 };
 
 // In-place Walsh-Hadamard transform of 32 values (Sylvester order over the index bits).
@@ -602,6 +605,13 @@ void trellis_gemm_kernel(const GemmParams p)
     __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
     uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
 
+    if (p.zero4 > 0)                    // every workgroup, tile or not, clears its grid-strided share up front; the
+    {                                   // stores drain while the tile computes
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < p.zero4;
+             i += (int64_t) gridDim.x * blockDim.x)
+            p.zero[i] = z;
+    }
     int group, slot;
     xcd_group_slot((int) blockIdx.x, p.k_split > 1 ? p.n_slots * p.k_split : p.n_slots, group, slot);
     Tile t;

@@ -137,7 +137,7 @@ int grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layo
                        const int32_t* block_expert, const int32_t* block_row0, int max_blocks, int tile_rows,
                        const int32_t* counts, const int32_t* expert_row0, int n_experts, const int64_t* token_sorted,
                        const uint16_t* route_weight, const int32_t* route_index, void* out, int64_t out_rows, int mode,
-                       int k_split, const ActFuse* act, hipStream_t s)
+                       int k_split, const ActFuse* act, hipStream_t s, float* zero, int64_t zero_floats)
 {
     EXL3_CHECK(tile_rows == 64 || tile_rows == 128 || tile_rows == 256 || tile_rows == 512,
                "tile_rows must be 64, 128, 256 or 512");
@@ -175,6 +175,11 @@ int grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layo
                "k_split > 1 needs an accumulating mode (1: fp32 atomic scatter, 3: fp32 atomic rows)");
     p.kb_per_split = ((total_kb + k_split - 1) / k_split + 1) / 2 * 2;
     p.k_split = (total_kb + p.kb_per_split - 1) / p.kb_per_split;
+    EXL3_CHECK(zero_floats >= 0 && zero_floats % 4 == 0 && (zero_floats == 0 || zero) && aligned16(zero),
+               "zero must be 16-byte aligned, a multiple of 4 floats");
+    EXL3_CHECK(zero_floats == 0 || max_blocks > 0, "the clear runs on the GEMM's workgroups: max_blocks must be > 0");
+    p.zero = reinterpret_cast<float4*>(zero);
+    p.zero4 = zero_floats / 4;
     if (act)
     {
         EXL3_CHECK(mode == EXL3_GEMM_ATOMIC_F32 && n_tensors == 2 && tile_rows == 64,
@@ -243,6 +248,22 @@ extern "C" int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int si
                               tiles_n, bits, svh_gate, svh_up, svh_stride, block_expert, block_row0, max_blocks,
                               tile_rows, counts, expert_row0, n_experts, token_sorted, route_weight, route_index, out,
                               out_rows, mode, k_split, nullptr, as_stream(stream));
+}
+
+extern "C" int exl3_grouped_gemm_clear(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,
+                                       const uint16_t* packed_gate, const uint16_t* packed_up,
+                                       int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
+                                       const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
+                                       const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
+                                       int tile_rows, const int32_t* counts, const int32_t* expert_row0,
+                                       int n_experts, const int64_t* token_sorted, const uint16_t* route_weight,
+                                       const int32_t* route_index, void* out, int64_t out_rows, int mode,
+                                       int k_split, float* zero, int64_t zero_floats, void* stream)
+{
+    return grouped_gemm_split(a, a_rows, size_k, a_layout, packed_gate, packed_up, expert_stride_words, tiles_k,
+                              tiles_n, bits, svh_gate, svh_up, svh_stride, block_expert, block_row0, max_blocks,
+                              tile_rows, counts, expert_row0, n_experts, token_sorted, route_weight, route_index, out,
+                              out_rows, mode, k_split, nullptr, as_stream(stream), zero, zero_floats);
 }
 
 extern "C" int exl3_grouped_gemm_ex(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,

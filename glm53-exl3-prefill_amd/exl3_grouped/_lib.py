@@ -47,6 +47,8 @@ SIGNATURES = {
                                    I32, P, P, P, P, I64, I32, P]),
     "exl3_grouped_gemm_split": (I32, [P, I64, I32, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, I32, P, P,
                                       I32, P, P, P, P, I64, I32, I32, P]),
+    "exl3_grouped_gemm_clear": (I32, [P, I64, I32, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, I32, P, P,
+                                      I32, P, P, P, P, I64, I32, I32, P, I64, P]),
     "exl3_combine_routes": (I32, [P, P, P, I32, I32, I64, I32, I64, P]),
     "exl3_fat_gemm": (I32, [P, I64, I32, P, I32, I32, I32, P, I64, P, I64, I32, I32, I32, I32, P]),
     "exl3_fat_gemm_scatter": (I32, [P, I64, I32, P, I32, I32, I32, P, I64, P, I64, P, P, I32, I32, I32, I32, P]),

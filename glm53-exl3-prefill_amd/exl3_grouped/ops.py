@@ -297,7 +297,7 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
                  block_row0: torch.Tensor, counts: torch.Tensor, expert_row0: torch.Tensor,
                  token_sorted: Optional[torch.Tensor], route_weight: Optional[torch.Tensor], out: torch.Tensor,
                  mode: int, route_index: Optional[torch.Tensor] = None, tile_rows: int = 128, a_layout: int = 0,
-                 a_rows: Optional[int] = None, k_split: int = 1) -> None:
+                 a_rows: Optional[int] = None, k_split: int = 1, zero: Optional[torch.Tensor] = None) -> None:
     """kernel/exl3_grouped_prefill.cu:326-378. mode 0: fp16 store; mode 1: fp32 atomic scatter into
     out[token_sorted[r]]; mode 2 (new): fp32 store of the weighted row into out[route_index[r]] (out [T*topk, N]),
     summed per token by combine_routes in a fixed order; mode 3 (new): fp32 atomic add of the unweighted row into
@@ -306,7 +306,8 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
     build_blocks' table (the reference's), 256 or 512 for a build_tiles(..., 256 | 512) table (512 runs the 8-wave
     kernel), 64 (a thin kernel for small tiles, 16 rows per wave). a_layout (new): 0 row-major a,
     1 T16 (a from row_had / act_had with dst_layout=1; a_rows gives its logical rows). k_split (new): slices of K
-    whose partial products are added into out (modes 1 and 3 only)."""
+    whose partial products are added into out (modes 1 and 3 only). zero (new, optional fp32 contiguous, numel % 4 ==
+    0, not overlapping a or out): cleared by the same launch, e.g. the output a later mode-1 launch adds into."""
     _check(int(tile_rows) in (64, 128, 256, 512), "tile_rows must be 64, 128, 256 or 512")
     _check(int(k_split) >= 1 and int(k_split) <= a.size(1) // 64, "k_split must be in [1, K / 64]")
     _check(int(k_split) == 1 or mode in (1, 3), "k_split > 1 needs mode 1 or 3")
@@ -360,17 +361,22 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
         _check(int(tile_rows) <= 256, "mode 3 takes row tiles of 64, 128 or 256 rows")
     else:
         raise RuntimeError("mode must be 0, 1, 2, 3 or 4")
+    _check(zero is None or (zero.dtype == torch.float32 and zero.is_contiguous() and zero.numel() % 4 == 0),
+           "zero must be fp32 contiguous with a multiple of 4 elements")
     weighted = mode in (1, 2)
     dev = _require_cuda(a, packed_gate, packed_up, svh_gate, svh_up, block_expert, block_row0, counts,
                         expert_row0, out, token_sorted if mode == 1 else None, route_weight if weighted else None,
-                        route_index if mode == 2 else None)
+                        route_index if mode == 2 else None, zero)
+    args = (_p(a), int(a_rows), size_k, int(a_layout), _p(packed_gate), _p(packed_up), expert_stride, tiles_k, tiles_n,
+            bits, _p(svh_gate), _p(svh_up), svh_stride, _p(block_expert), _p(block_row0), max_blocks, int(tile_rows),
+            _p(counts), _p(expert_row0), E, _p(token_sorted) if mode == 1 else None,
+            _p(route_weight) if weighted else None, _p(route_index) if mode == 2 else None, _p(out), out.size(0), mode,
+            int(k_split))
     with _On(dev) as s:
-        _lib.call("exl3_grouped_gemm_split", _p(a), int(a_rows), size_k, int(a_layout), _p(packed_gate),
-                  _p(packed_up), expert_stride, tiles_k, tiles_n, bits, _p(svh_gate), _p(svh_up), svh_stride,
-                  _p(block_expert), _p(block_row0), max_blocks, int(tile_rows), _p(counts), _p(expert_row0), E,
-                  _p(token_sorted) if mode == 1 else None,
-                  _p(route_weight) if weighted else None, _p(route_index) if mode == 2 else None, _p(out),
-                  out.size(0), mode, int(k_split), s)
+        if zero is None:
+            _lib.call("exl3_grouped_gemm_split", *args, s)
+        else:
+            _lib.call("exl3_grouped_gemm_clear", *args, _p(zero), zero.numel(), s)
 
 
 def combine_routes(partial: torch.Tensor, out: torch.Tensor, topk: int, topk_ids: Optional[torch.Tensor] = None,

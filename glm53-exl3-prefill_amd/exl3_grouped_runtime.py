@@ -220,14 +220,15 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     block_expert, block_row0, meta = B["block_expert"], B["block_row0"], B["meta"]
     out = None
     if thin:
-        # the sort, then the two tile tables (each expert's last tile of <= 64 rows goes to a second table, run by the
-        # thin kernel) and the clear of the fp32 output the atomic down scatter adds into: two launches in all
+        # the sort and the two tile tables (each expert's last tile of <= 64 rows goes to a second table, run by the
+        # thin kernel) in two launches; the fp32 output the atomic down scatter adds into is cleared by the gate|up
+        # launch, whose MFMA-bound workgroups hide the stores
         thin_expert, thin_row0 = B["thin_expert"], B["thin_row0"]
         out = torch.empty(T, K, dtype=torch.float32, device=dev) if scatter == "atomic" else None
         gp.sort_routes_split_tiles(ids, weights, E, token_sorted, weight_sorted, expert_of_row, counts, expert_row0,
-                                   block_expert, block_row0, thin_expert, thin_row0, meta, tr, THIN_ROWS, zero=out,
+                                   block_expert, block_row0, thin_expert, thin_row0, meta, tr, THIN_ROWS,
                                    workspace=B["sort_ws"], route_index=route_index)
-        mark("sort_routes")                               # sort, tile tables and output clear
+        mark("sort_routes")                               # sort and tile tables
     else:
         gp.sort_routes(ids, weights, E, token_sorted, weight_sorted, expert_of_row, counts, expert_row0,
                        workspace=B["sort_ws"], route_index=route_index)
@@ -240,7 +241,7 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     gu = B["gu"]
     w13 = (layer.w13_trellis[:, 0], layer.w13_trellis[:, 1], layer.w13_svh[:, 0], layer.w13_svh[:, 1])
     gp.grouped_gemm(h13, *w13, block_expert, block_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 4,
-                    tile_rows=tr, a_layout=1, a_rows=R)
+                    tile_rows=tr, a_layout=1, a_rows=R, zero=out if thin else None)
     if thin:
         gp.grouped_gemm(h13, *w13, thin_expert, thin_row0, counts, expert_row0, token_sorted, weight_sorted, gu, 4,
                         tile_rows=THIN_ROWS, a_layout=1, a_rows=R)

@@ -237,6 +237,20 @@ int exl3_grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a
                             const int32_t* counts, const int32_t* expert_row0, int n_experts,
                             const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
                             void* out, int64_t out_rows, int mode, int k_split, void* stream);
+/*
+ * exl3_grouped_gemm_split that also clears zero[0 .. zero_floats) (fp32, 16-byte aligned, a multiple of 4 floats;
+ * max_blocks > 0) as a side job of the same launch (new): every workgroup stores its grid-strided share of zeros
+ * before its tile. The prefill path passes the down scatter's output to its gate|up launch, whose stores then drain
+ * under MFMA-bound work instead of holding a launch of their own. zero must not overlap a or out.
+ */
+int exl3_grouped_gemm_clear(const uint16_t* a, int64_t a_rows, int size_k, int a_layout,
+                            const uint16_t* packed_gate, const uint16_t* packed_up, int64_t expert_stride_words,
+                            int tiles_k, int tiles_n, int bits, const uint16_t* svh_gate, const uint16_t* svh_up,
+                            int64_t svh_stride, const int32_t* block_expert, const int32_t* block_row0, int max_blocks,
+                            int tile_rows, const int32_t* counts, const int32_t* expert_row0, int n_experts,
+                            const int64_t* token_sorted, const uint16_t* route_weight, const int32_t* route_index,
+                            void* out, int64_t out_rows, int mode, int k_split, float* zero, int64_t zero_floats,
+                            void* stream);
 
 /*
  * Deterministic route combine (new; pairs with grouped_gemm mode 2): out[t, :] = sum_{j < topk} partial[t*topk + j, :]

@@ -253,6 +253,14 @@ def test_split_gemm_contract():
     assert rc == _lib.EXL3_ERR_ARG and "mode 3" in msg
     rc, msg = call(mode=5, k_split=1)
     assert rc == _lib.EXL3_ERR_ARG and "mode must be" in msg
+    # the launch that also clears a buffer: the clear's contract is checked before anything runs
+    for zero, n, mb, text in ((None, 8, 10, "zero must be"), (FAKE, 6, 10, "zero must be"),
+                              (ctypes.c_void_p(0x1004), 8, 10, "zero must be"), (FAKE, -4, 10, "zero must be"),
+                              (FAKE, 8, 0, "max_blocks")):
+        a = dict(args)
+        a.update(mb=mb, k_split=1)
+        rc, msg = rc_and_msg("exl3_grouped_gemm_clear", *a.values(), zero, n, None)
+        assert rc == _lib.EXL3_ERR_ARG and text in msg, (zero, n, mb, msg)
     rc, msg = rc_and_msg("exl3_act_had_f32", FAKE, 300, FAKE, FAKE, FAKE, 128, 4, 128, ctypes.c_float(10.0), None)
     assert rc == _lib.EXL3_ERR_ARG and "2I" in msg
 

@@ -468,6 +468,15 @@ def test_grouped_gemm_gate_up(dev, name, T, bits, tile_rows):
                     TL.w13_svh[:, 1], be, br, t16(counts, dev), t16(row0, dev), None, None, gut, 4, tile_rows=tile_rows,
                     a_layout=1, a_rows=R)
     assert np.array_equal(from_t16(gut.cpu().numpy(), R).view(np.uint16), gu.cpu().numpy().view(np.uint16))   # mode 4
+    # the same launch clearing a buffer on the side (the prefill path's down scatter output): same gu, exactly the range
+    zero = torch.full((4 * 1237 + 8,), float("nan"), dtype=torch.float32, device=dev)
+    gz = torch.full_like(gut, float("nan"))
+    gp.grouped_gemm(t16(to_t16(h13), dev), TL.w13_trellis[:, 0], TL.w13_trellis[:, 1], TL.w13_svh[:, 0],
+                    TL.w13_svh[:, 1], be, br, t16(counts, dev), t16(row0, dev), None, None, gz, 4, tile_rows=tile_rows,
+                    a_layout=1, a_rows=R, zero=zero[4:-4])
+    torch.cuda.synchronize()
+    assert torch.equal(gz.view(torch.int16), gut.view(torch.int16))
+    assert (zero[4:-4] == 0).all() and zero[:4].isnan().all() and zero[-4:].isnan().all()
 
 
 @pytest.mark.parametrize("tile_rows", [128, 256, 512])
