@@ -90,13 +90,33 @@ DecodeLayout decode_layout(int64_t tokens, int topk, int n_experts, int hidden, 
 // Workgroups a launch should put on the device: four resident thin-kernel workgroups per CU.
 int target_workgroups() { return EXL3_DECODE_WG_PER_CU * device_cus(); }
 
-// K slices for a launch of `wgs` workgroups over `stages` 32-wide K stages: as many as fit in one round of `target`
-// resident workgroups (a partial second round would double the launch's time), each slice at least 2 stages.
+// K slices for a launch of `wgs` workgroups over `stages` 32-wide K stages. A slice holds an even number of stages
+// (per = ceil(stages / s) rounded up to even; ceil(stages / per) slices, as exl3_grouped_gemm_split lays them out),
+// and the dispatcher deals the workgroups out evenly over the CUs, so the launch lasts about as long as its busiest
+// CU's ceil(workgroups / CUs) * per stages of decoding. Take the slice count with the fewest such stages among those
+// whose workgroups fit one round of `target` resident ones (a partial second round would double the launch's time),
+// the most workgroups among equals (more resident waves hide more latency). At one token on the 288-expert layer:
+// 8 slices of 16 stages, 768 workgroups, 48 stages per CU (a plain fill of the round: 10 slices of 14 and 2, 960
+// workgroups, 56 stages on the busiest CUs).
 int k_split_for(int64_t wgs, int stages, int target)
 {
     if (wgs <= 0) return 1;
-    const int64_t s = std::max<int64_t>(1, std::min<int64_t>(target / wgs, stages / 2));
-    return (int) s;
+    const int64_t cus = device_cus();
+    int best = 1;
+    int64_t best_cost = -1;
+    for (int s = 1; s <= std::max(1, stages / 2); ++s)
+    {
+        const int per = ((stages + s - 1) / s + 1) / 2 * 2;
+        const int64_t n = wgs * ((stages + per - 1) / per);
+        if (s > 1 && n > target) break;
+        const int64_t cost = (n + cus - 1) / cus * per;
+        if (best_cost < 0 || cost <= best_cost)
+        {
+            best_cost = cost;
+            best = s;
+        }
+    }
+    return best;
 }
 
 // This device's address of `scratch`, looked up once per device with that device current. In host code the array's
