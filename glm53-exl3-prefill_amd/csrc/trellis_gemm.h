@@ -224,18 +224,22 @@ struct Decoder
     int stage_bytes, last_kb, tb, wcol0, wcol1;
     uint32_t off[NR];              // per-lane byte offsets of the raw words
 
-    __device__ __forceinline__ Decoder(const GemmParams& p, const Tile& t, int dw, int lane, int num_kb)
+    // cols: the thin tiles' column split -- wave dw decodes both k-tiles of n-tiles 2 dw and 2 dw + 1 (the weights of
+    // its own 32 output columns; k-tile lane >> 5, n-tile 2 dw + ((lane >> 4) & 1)) instead of the four n-tiles above.
+    __device__ __forceinline__ Decoder(const GemmParams& p, const Tile& t, int dw, int lane, int num_kb,
+                                       bool cols = false)
     {
         const int j16 = lane & 15;
         const int ta = j16 >> 1;
         tb = j16 & 1;
-        const int kt = dw >> 1;
-        const int nt8 = 4 * (dw & 1) + (lane >> 4);
+        const int kt = cols ? (lane >> 5) : (dw >> 1);
+        const int nt8 = cols ? 2 * dw + ((lane >> 4) & 1) : 4 * (dw & 1) + (lane >> 4);
         stage_bytes = 2 * p.tiles_n * NDW * 4;
-        const int64_t first = ((int64_t) (2 * t.kb0 + kt) * p.tiles_n + t.nt * 8 + 4 * (dw & 1)) * NDW;
+        const int64_t first = cols ? ((int64_t) (2 * t.kb0) * p.tiles_n + t.nt * 8 + 2 * dw) * NDW
+                                   : ((int64_t) (2 * t.kb0 + kt) * p.tiles_n + t.nt * 8 + 4 * (dw & 1)) * NDW;
         raw = buffer_rsrc(t.packed + first, ((int64_t) (p.size_k >> 4) * p.tiles_n * NDW - first) * 4);
         last_kb = num_kb - 1;
-        const int tile_off = (lane >> 4) * NDW;
+        const int tile_off = cols ? (kt * p.tiles_n + ((lane >> 4) & 1)) * NDW : (lane >> 4) * NDW;
         if constexpr (BITS == 3)
         {
             const int d0 = (16 * j16 * BITS + BITS - 16) >> 5;  // dword of the first window bit (may be -1)
@@ -416,6 +420,21 @@ struct Mma
         #pragma unroll
         for (int nb = 0; nb < 8; ++nb) w[nb] = *reinterpret_cast<const half8_t*>(lds + nb * LDS_BLK + wread);
     }
+    // The wave's own two column blocks 2 w, 2 w + 1 of the decoded stage (thin tiles' column split).
+    __device__ __forceinline__ void read_w2(const uint16_t* lds, int w, half8_t (&f)[2]) const
+    {
+        f[0] = *reinterpret_cast<const half8_t*>(lds + (2 * w) * LDS_BLK + wread);
+        f[1] = *reinterpret_cast<const half8_t*>(lds + (2 * w + 1) * LDS_BLK + wread);
+    }
+    template <int MBA>
+    __device__ __forceinline__ static void mfma2(const half8_t (&f)[2], const half8_t (&a)[4], floatx4 (&acc)[4][2])
+    {
+        #pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+            #pragma unroll
+            for (int mb = 0; mb < MBA; ++mb)
+                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[nb], a[mb], acc[mb][nb], 0, 0, 0);
+    }
     template <int MBA, int MBN>
     __device__ __forceinline__ static void mfma(const half8_t (&w)[8], const half8_t (&a)[MBN], floatx4 (&acc)[MBN][8])
     {
@@ -584,40 +603,96 @@ __device__ __forceinline__ void act_after_last_slice(const GemmParams& p, const 
     }
 }
 
-// ------------------------------------------------------------------------------------------- kernel
-// 128- and 256-row tiles: every wave decodes a quarter of each stage and multiplies its own 64 rows; two workgroups
-// share a CU. Pipeline of stage s: barrier; read stage s's weight fragments; decode stage s+1 while stage s's MFMAs run;
-// write stage s+1 into the other of two LDS buffers; issue loads for later stages.
-template <int WAVES> constexpr int lds_scatter_bytes() { return WAVES * 16 * SC_ROW * 4; }
-
-// MBN: 16-row groups per wave. 4 (the default): 256-row tiles, two workgroups per CU. 1 (thin): 64-row tiles of small
-// batches, where most waves only decode; a quarter of the accumulators lets four workgroups share a CU.
-// WAVES = 8: 512-row tiles, one workgroup per CU; each wave decodes half as much of every stage (one chunk per lane),
-// so a decoded weight feeds twice the rows for the same VALU work per wave.
-template <int BITS, int MODE, bool DENSE, int MBN = 4, int WAVES = 4>
-// (HIP's second launch bound is the minimum number of waves per SIMD: 2 leaves 256 VGPRs per wave, 4 leaves 128.)
-__global__ __launch_bounds__(64 * WAVES, MBN == 4 ? 2 : 4)
-void trellis_gemm_kernel(const GemmParams p)
+// Thin tiles of at most 16 rows (one row group; the MBN == 1 kernels, which run most of the decode path's tiles): every
+// wave decodes the weights of its own 32 output columns (Decoder cols) into its part of the double-buffered stage tile
+// and multiplies the row group by them, so no wave reads weights another wave decoded and the stages need no barrier
+// (the LDS accesses of one wave complete in order). Each output element still adds its K stages in order, as the
+// shared-tile loop does, so the results are its results bit for bit. Afterwards the accumulators go through LDS so that
+// wave 0 holds the group over all 128 columns, the layout of the shared epilogue. (Taller thin tiles keep the shared
+// loop: there every wave would load all of the tile's activation rows, and a 1024-token layer ran 3.5% slower.)
+template <int BITS, int MODE>
+__device__ __forceinline__ void thin_tile(const GemmParams& p, const Tile& t, int group, int wave, int lane,
+                                          unsigned char* lds_raw)
 {
-    static_assert(WAVES == 4 || (WAVES == 8 && MBN == 4), "8-wave workgroups run 64 rows per wave");
-    constexpr int SCB = lds_scatter_bytes<WAVES>();
-    constexpr int LDS_BYTES = (atomic_mode(MODE) && SCB > LDS_MAIN_BYTES) ? SCB : LDS_MAIN_BYTES;
-    __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
     uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
-
-    if (p.zero4 > 0)                    // every workgroup, tile or not, clears its grid-strided share up front; the
-    {                                   // stores drain while the tile computes
-        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < p.zero4;
-             i += (int64_t) gridDim.x * blockDim.x)
-            p.zero[i] = z;
+    const int num_kb = t.num_kb;
+    using Dec = Decoder<BITS>;
+    constexpr int NR = Dec::NR;
+    const Dec dec(p, t, wave, lane, num_kb, true);
+    const Mma mm(p, t, 0, lane, num_kb, 64);                       // the A operand of row group 0
+    floatx4 acc[4][2];
+    #pragma unroll
+    for (int nb = 0; nb < 2; ++nb) acc[0][nb] = {};
+    {
+        uint32_t raw[RAW_DEPTH][NR];
+        half8_t act[ACT_DEPTH][4];
+        {
+            uint32_t r0[NR];
+            dec.load(0, r0);
+            #pragma unroll
+            for (int s = 1; s <= RAW_DEPTH; ++s) dec.load(s, raw[s % RAW_DEPTH]);
+            #pragma unroll
+            for (int s = 0; s < ACT_DEPTH; ++s) mm.load_act<1>(s, act[s]);
+            typename Dec::Out o;
+            dec.decode(r0, o);
+            dec.store(o, lds_b);
+        }
+        auto trip = [&](int s0, auto n_tag) {
+            constexpr int N = decltype(n_tag)::value;
+            #pragma unroll
+            for (int u = 0; u < N; ++u)
+            {
+                const int s = s0 + u;
+                half8_t f[2];
+                mm.read_w2(lds_b + (u & 1) * LDS_TILE, wave, f);  // stage s, which this wave wrote
+                typename Dec::Out o;
+                dec.decode(raw[(u + 1) % RAW_DEPTH], o);          // stage s + 1
+                Mma::mfma2<1>(f, act[u % ACT_DEPTH], acc);
+                dec.store(o, lds_b + ((u + 1) & 1) * LDS_TILE);
+                dec.load(s + 1 + RAW_DEPTH, raw[(u + 1) % RAW_DEPTH]);
+                mm.load_act<1>(s + ACT_DEPTH, act[u % ACT_DEPTH]);
+            }
+        };
+        using full_trip = std::integral_constant<int, UNROLL>;
+        int s0 = 0;
+        if (num_kb >= UNROLL)
+        {
+            trip(0, full_trip{});
+            for (s0 = UNROLL; s0 + UNROLL <= num_kb; s0 += UNROLL) trip(s0, full_trip{});
+        }
+        if (s0 < num_kb) trip(s0, std::integral_constant<int, 2>{});
     }
-    int group, slot;
-    xcd_group_slot((int) blockIdx.x, p.k_split > 1 ? p.n_slots * p.k_split : p.n_slots, group, slot);
-    Tile t;
-    if (!resolve_tile<DENSE>(p, group, slot, t)) return;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+    // wave 0 collects the group: every wave puts its two column blocks in LDS
+    floatx4 full[1][8];
+    floatx4* xs = reinterpret_cast<floatx4*>(lds_raw);
+    __syncthreads();                                               // the stage tiles are dead
+    xs[(2 * wave) * 64 + lane] = acc[0][0];
+    xs[(2 * wave + 1) * 64 + lane] = acc[0][1];
+    __syncthreads();
+    if (wave == 0)
+        #pragma unroll
+        for (int nb = 0; nb < 8; ++nb) full[0][nb] = xs[nb * 64 + lane];
+    __syncthreads();                                               // LDS free for the epilogue's staging
+    float* const stage = reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW);
+    if constexpr (MODE == MODE_ATOMIC_F32)
+    {
+        if (p.act_arrive)                                          // every wave goes on to the arrival barrier
+        {
+            if (wave == 0) epilogue<MODE, 1, 0>(p, t, 0, lane, full, stage);
+            act_after_last_slice(p, t, group, wave, lane);
+            return;
+        }
+    }
+    if (wave == 0) epilogue<MODE, 1, 0>(p, t, 0, lane, full, stage);
+}
+
+// 128-, 256- and 512-row tiles: the waves share each decoded stage (a barrier per stage), each multiplying its own rows.
+template <int BITS, int MODE, int MBN, int WAVES>
+__device__ __forceinline__ void shared_tile(const GemmParams& p, const Tile& t, int group, int wave, int lane,
+                                            unsigned char* lds_raw)
+{
+    uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
     const int num_kb = t.num_kb;
     using Dec = typename std::conditional<WAVES == 8, Decoder1<BITS>, Decoder<BITS>>::type;
     constexpr int NR = Dec::NR;
@@ -716,6 +791,46 @@ void trellis_gemm_kernel(const GemmParams p)
     }
     if (n_w == 0) return;
     epilogue<MODE, MBN, GSTRIDE>(p, t, wave, lane, acc, stage);
+}
+
+// ------------------------------------------------------------------------------------------- kernel
+// 128- and 256-row tiles: every wave decodes a quarter of each stage and multiplies its own 64 rows; two workgroups
+// share a CU. Pipeline of stage s: barrier; read stage s's weight fragments; decode stage s+1 while stage s's MFMAs run;
+// write stage s+1 into the other of two LDS buffers; issue loads for later stages.
+template <int WAVES> constexpr int lds_scatter_bytes() { return WAVES * 16 * SC_ROW * 4; }
+
+// MBN: 16-row groups per wave. 4 (the default): 256-row tiles, two workgroups per CU. 1 (thin): 64-row tiles of small
+// batches (those of at most 16 rows split by columns over the waves, thin_tile); a quarter of the accumulators lets four
+// workgroups share a CU.
+// WAVES = 8: 512-row tiles, one workgroup per CU; each wave decodes half as much of every stage (one chunk per lane),
+// so a decoded weight feeds twice the rows for the same VALU work per wave.
+template <int BITS, int MODE, bool DENSE, int MBN = 4, int WAVES = 4>
+// (HIP's second launch bound is the minimum number of waves per SIMD: 2 leaves 256 VGPRs per wave, 4 leaves 128.)
+__global__ __launch_bounds__(64 * WAVES, MBN == 4 ? 2 : 4)
+void trellis_gemm_kernel(const GemmParams p)
+{
+    static_assert(WAVES == 4 || (WAVES == 8 && MBN == 4), "8-wave workgroups run 64 rows per wave");
+    constexpr int SCB = lds_scatter_bytes<WAVES>();
+    constexpr int LDS_BYTES = (atomic_mode(MODE) && SCB > LDS_MAIN_BYTES) ? SCB : LDS_MAIN_BYTES;
+    __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
+
+    if (p.zero4 > 0)                    // every workgroup, tile or not, clears its grid-strided share up front; the
+    {                                   // stores drain while the tile computes
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < p.zero4;
+             i += (int64_t) gridDim.x * blockDim.x)
+            p.zero[i] = z;
+    }
+    int group, slot;
+    xcd_group_slot((int) blockIdx.x, p.k_split > 1 ? p.n_slots * p.k_split : p.n_slots, group, slot);
+    Tile t;
+    if (!resolve_tile<DENSE>(p, group, slot, t)) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (MBN == 1 && t.rows_valid <= 16)                           // uniform over the workgroup
+        thin_tile<BITS, MODE>(p, t, group, wave, lane, lds_raw);
+    else
+        shared_tile<BITS, MODE, MBN, WAVES>(p, t, group, wave, lane, lds_raw);
 }
 
 // 512-row tiles run the 8-wave variant, 128- and 256-row tiles the 4-wave kernel (the only one built for ATOMIC_F32,
