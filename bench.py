@@ -4,7 +4,9 @@
 Workload (the shape the metric is quoted on): one TP rank's share of a 288-expert layer,
 H=4096, I=768, 4 bpw trellis, an 8192-token chunk, top-8 routing skewed by a Zipf(1.1) prior; synthetic seeded
 inputs resident in HBM before timing starts. A step is one full grouped_prefill call (route sort, block table,
-gather + input Hadamard, gate|up GEMM, SwiGLU + down Hadamard, down GEMM with fp32 atomic scatter).
+gather + input Hadamard, gate|up GEMM, SwiGLU + down Hadamard, down GEMM with fp32 atomic scatter). Python's garbage
+collector runs, and its surviving objects are frozen, right before every timed region (quiet_gc): a full collection
+inside the timed steps would stall the launching thread for 30-40 ms.
 
 Prints ONE JSON line: value = routed tokens/s (T*topk / step time); ms_per_step = per-layer MoE ms; stage_ms = the
 median over the timed steps of each stage's HIP-event time on the launch stream (stage_ms_mean beside it); roofline of
@@ -81,6 +83,16 @@ def parse():
                     help="only run a plain device copy of MIB MiB a few times (calibrates rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE against known bytes) and exit")
     return ap.parse_args()
+
+
+def quiet_gc():
+    """Run Python's cyclic garbage collector now and exempt the objects that exist so far from later collections.
+    In this process a full (generation 2) collection takes ~30-40 ms of host time; one that lands inside a timed region
+    stalls the launch stream (the GPU idles until the host resumes), which the per-step events show as one step of
+    ~30 ms. Serving processes freeze their start-up objects the same way. Called right before every timed region."""
+    import gc
+    gc.collect()
+    gc.freeze()
 
 
 def copy_probe(mib: int):
@@ -186,6 +198,7 @@ def run(args, T=None, emit=True):
     # timed region: exactly `steps` full steps, bracketed by device synchronisation
     events = []
     torch.cuda.synchronize()
+    quiet_gc()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         ev = []
@@ -199,8 +212,8 @@ def run(args, T=None, emit=True):
     for ev in events:
         for (name, e1), (_, e0) in zip(ev[1:], ev[:-1]):
             stage_ms.setdefault(name, []).append(e0.elapsed_time(e1))
-    # per-stage medians: the device has been seen to pause for ~30 ms about once in 20-40 s of work (one step of one
-    # stage); a mean over 20 steps then misreports that stage several-fold. The means are reported beside them.
+    # per-stage medians (a host stall that starves the launch stream -- e.g. a garbage collection the freeze above
+    # missed -- shows as one long step of one stage, which a mean over 20 steps misreports); the means beside them
     stage_avg = {n: statistics.median(v) for n, v in stage_ms.items()}
     stage_mean = {n: statistics.mean(v) for n, v in stage_ms.items()}
     gemm_ms = stage_avg["gemm_gate_up"]
@@ -398,6 +411,8 @@ def fat_bench(args):
         out = torch.empty(M, N, dtype=torch.float32, device=dev)
         for _ in range(args.warmup):
             gp.fat_gemm_v2(at, pt, out, st, 4, True, False, variant)
+        torch.cuda.synchronize()
+        quiet_gc()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         n = max(args.steps, 10)
         e0.record()
@@ -453,6 +468,7 @@ def decode_bench(args):
             for _ in range(args.warmup):
                 fn()
             torch.cuda.synchronize()
+            quiet_gc()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
             for _ in range(n):
