@@ -5,8 +5,8 @@ Workload (the shape the metric is quoted on): one TP r
 H=4096, I=768, 4 bpw trellis, an 8192-token chunk, top-8 routing skewed by a Zipf(1.1) prior; synthetic seeded
 inputs resident in HBM before timing starts. A step is one full grouped_prefill call (route sort, block table,
 gather + input Hadamard, gate|up GEMM, SwiGLU + down Hadamard, down GEMM with fp32 atomic scatter). Python's garbage
-collector runs, and its surviving objects are frozen, right before every timed region (quiet_gc): a full collection
-inside the timed steps would stall the launching thread for 30-40 ms.
+collector runs, and its surviving objects are frozen, before every warm-up and timed region (quiet_gc): a full
+collection inside the timed steps would stall the launching thread for 30-40 ms.
 
 Prints ONE JSON line: value = routed tokens/s (T*topk / step time); ms_per_step = per-layer MoE ms; stage_ms = the
 median over the timed steps of each stage's HIP-event time on the launch stream (stage_ms_mean beside it); roofline of
@@ -89,7 +89,8 @@ def quiet_gc():
     """Run Python's cyclic garbage collector now and exempt the objects that exist so far from later collections.
     In this process a full (generation 2) collection takes ~30-40 ms of host time; one that lands inside a timed region
     stalls the launch stream (the GPU idles until the host resumes), which the per-step events show as one step of
-    ~30 ms. Serving processes freeze their start-up objects the same way. Called right before every timed region."""
+    ~30 ms. Serving processes freeze their start-up objects the same way. Called before every warm-up (not between
+    the warm-up and the timed steps: the collection leaves the GPU idle for its duration)."""
     import gc
     gc.collect()
     gc.freeze()
@@ -191,6 +192,7 @@ def run(args, T=None, emit=True):
     limit = 10.0
 
     scatter = args.scatter or rt.scatter_mode()
+    quiet_gc()                          # before the warm-up, whose steps then bring the clocks back up
     for _ in range(args.warmup):
         rt.grouped_prefill(xt, it, wt, TL, limit, scatter=scatter)
     torch.cuda.synchronize()
@@ -198,7 +200,6 @@ def run(args, T=None, emit=True):
     # timed region: exactly `steps` full steps, bracketed by device synchronisation
     events = []
     torch.cuda.synchronize()
-    quiet_gc()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         ev = []
@@ -409,10 +410,10 @@ def fat_bench(args):
         a, packed, svh = synth.make_fat(0, M=M, K=K, N=N)
         at, pt, st = (torch.from_numpy(v).to(dev) for v in (a, packed, svh))
         out = torch.empty(M, N, dtype=torch.float32, device=dev)
+        quiet_gc()
         for _ in range(args.warmup):
             gp.fat_gemm_v2(at, pt, out, st, 4, True, False, variant)
         torch.cuda.synchronize()
-        quiet_gc()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         n = max(args.steps, 10)
         e0.record()
@@ -465,10 +466,10 @@ def decode_bench(args):
                           10.0, out=out, workspace=ws)
 
         def timed(fn, n):
+            quiet_gc()
             for _ in range(args.warmup):
                 fn()
             torch.cuda.synchronize()
-            quiet_gc()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
             for _ in range(n):
