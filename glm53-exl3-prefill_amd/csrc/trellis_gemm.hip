@@ -11,7 +11,9 @@ namespace {
 // out[t, :] = sum_j partial[t*topk + j, :] in order j = 0 .. topk-1 (deterministic), skipping routes whose id is
 // outside [0, n_experts) (their partial rows were never written). A workgroup per token (grid-strided): the token's
 // route ids are read once; each thread loads its columns of all topk rows before adding them (a skipped route's row is
-// loaded and discarded by a select, so no load waits behind a branch). TOPK > 0 fixes topk at compile time.
+// loaded and discarded by a select, so no load waits behind a branch). TOPK > 0 fixes topk at compile time. The
+// common case (topk 8, rows of a multiple of 1024 floats) runs combine_routes_cols_kernel, the same sum in the same
+// order.
 constexpr int COMBINE_THREADS = 256;
 constexpr int COMBINE_MAX_TOPK = 32;
 
@@ -60,6 +62,49 @@ void combine_routes_kernel(const float4* __restrict__ partial, float4* __restric
             out[t * n4 + c] = acc;
         }
     }
+}
+
+// The same sum for topk = TOPK when the row width is a multiple of COMBINE_THREADS float4s: one workgroup per (token,
+// COMBINE_THREADS float4 columns), so the token is uniform and its ids arrive through scalar loads issued after the
+// lane's TOPK row loads (rows read once: non-temporal). Grid = tokens x n4 / COMBINE_THREADS (fits 31 bits).
+template <int TOPK>
+__global__ __launch_bounds__(COMBINE_THREADS)
+void combine_routes_cols_kernel(const float4* __restrict__ partial, float4* __restrict__ out,
+                                const void* __restrict__ ids, int ids_dtype, int n_experts, int64_t n4)
+{
+    typedef float fv4 __attribute__((ext_vector_type(4)));
+    const uint32_t blocks_per_token = (uint32_t) (n4 / COMBINE_THREADS);
+    const uint32_t tb = blockIdx.x / blocks_per_token;
+    const int64_t t = tb;
+    const int64_t c = (int64_t) (blockIdx.x - tb * blocks_per_token) * COMBINE_THREADS + threadIdx.x;
+    const float4* rows = partial + t * TOPK * n4 + c;
+    fv4 v[TOPK];
+    #pragma unroll
+    for (int j = 0; j < TOPK; ++j) v[j] = __builtin_nontemporal_load(reinterpret_cast<const fv4*>(rows + j * n4));
+    uint32_t live = (1u << TOPK) - 1;
+    if (ids && ids_dtype == EXL3_DTYPE_I64)
+    {
+        const int64_t* q = reinterpret_cast<const int64_t*>(ids) + t * TOPK;
+        live = 0;
+        #pragma unroll
+        for (int j = 0; j < TOPK; ++j) live |= (q[j] >= 0 && q[j] < n_experts) ? 1u << j : 0u;
+    }
+    else if (ids)
+    {
+        const int32_t* q = reinterpret_cast<const int32_t*>(ids) + t * TOPK;
+        live = 0;
+        #pragma unroll
+        for (int j = 0; j < TOPK; ++j) live |= (q[j] >= 0 && q[j] < n_experts) ? 1u << j : 0u;
+    }
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    #pragma unroll
+    for (int j = 0; j < TOPK; ++j)
+    {
+        const bool on = live >> j & 1;
+        acc.x += on ? v[j][0] : 0.f; acc.y += on ? v[j][1] : 0.f;
+        acc.z += on ? v[j][2] : 0.f; acc.w += on ? v[j][3] : 0.f;
+    }
+    out[t * n4 + c] = acc;
 }
 
 // ------------------------------------------------------------------------------------------- reconstruct
@@ -485,7 +530,11 @@ extern "C" int exl3_combine_routes(const float* partial, float* out, const void*
     const int64_t blocks = std::min<int64_t>(tokens, 65536);
     const auto* p4 = reinterpret_cast<const float4*>(partial);
     auto* o4 = reinterpret_cast<float4*>(out);
-    if (topk == 8)
+    const int64_t n4 = n / 4, col_blocks = tokens * (n4 / COMBINE_THREADS);
+    if (topk == 8 && n4 % COMBINE_THREADS == 0 && col_blocks <= 0x7FFFFFFF)
+        combine_routes_cols_kernel<8><<<(unsigned) col_blocks, COMBINE_THREADS, 0, as_stream(stream)>>>(
+            p4, o4, topk_ids, ids_dtype, n_experts, n4);
+    else if (topk == 8)
         combine_routes_kernel<8><<<(unsigned) blocks, COMBINE_THREADS, 0, as_stream(stream)>>>(
             p4, o4, topk_ids, ids_dtype, n_experts, tokens, topk, n / 4);
     else

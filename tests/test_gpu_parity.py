@@ -520,20 +520,40 @@ def test_grouped_gemm_down_routes_and_combine(dev, name, T, tile_rows):
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))      # deterministic
 
 
-@pytest.mark.parametrize("k", [3, 8])
-def test_combine_skips_invalid_routes(dev, k):
+@pytest.mark.parametrize("k,N,id_dtype", [(3, 16, torch.int64), (8, 16, torch.int64), (8, 1024, torch.int64),
+                                          (8, 4096, torch.int32), (8, 2048, torch.int64)])
+def test_combine_skips_invalid_routes(dev, k, N, id_dtype):
     """Dropped routes' rows (never written by mode 2: NaN here) are skipped; the rest add in route order. k = 8 runs
-    the unrolled kernel, which loads every row and discards the dropped ones by a select."""
-    T, N = 5, 16
+    the unrolled kernels, which load every row and discard the dropped ones by a select (rows of a multiple of 1024
+    floats: one workgroup per token and 1024 columns)."""
+    T = 5
     partial = torch.arange(T * k * N, dtype=torch.float32, device=dev).reshape(T * k, N)
-    ids = torch.from_numpy(np.random.default_rng(k).integers(-1, 6, (T, k))).to(dev)     # ids 4 and 5 out of range
-    ids[0] = torch.arange(k, device=dev) % 4
+    ids = torch.from_numpy(np.random.default_rng(k + N).integers(-1, 6, (T, k))).to(device=dev, dtype=id_dtype)
+    ids[0] = torch.arange(k, device=dev) % 4                                     # ids 4 and 5 out of range
     keep = ((ids >= 0) & (ids < 4)).cpu()
     partial.view(T, k, N)[~keep.to(dev)] = float("nan")
     out = torch.empty(T, N, device=dev)
     gp.combine_routes(partial, out, k, ids, 4)
     p = partial.cpu().reshape(T, k, N)
     ref = torch.where(keep[:, :, None], p, torch.zeros(())).sum(1)
+    assert torch.equal(out.cpu(), ref)
+
+
+@pytest.mark.parametrize("N", [4096, 48])
+def test_combine_order_is_route_order(dev, N):
+    """Random fp32 rows add in route order j = 0 .. 7 exactly (a sequential fp32 sum on the CPU, bit for bit), for the
+    per-token-column kernel (N = 4096) and the general one (N = 48)."""
+    T, k = 37, 8
+    rng = np.random.default_rng(N)
+    partial = torch.from_numpy(rng.standard_normal((T * k, N)).astype(np.float32) * 1e3).to(dev)
+    ids = torch.from_numpy(rng.integers(-1, 9, (T, k))).to(dev)                       # 8 out of range
+    out = torch.empty(T, N, device=dev)
+    gp.combine_routes(partial, out, k, ids, 8)
+    p = partial.cpu().reshape(T, k, N)
+    keep = ((ids >= 0) & (ids < 8)).cpu()
+    ref = torch.zeros(T, N)
+    for j in range(k):
+        ref = ref + torch.where(keep[:, j, None], p[:, j], torch.zeros(()))
     assert torch.equal(out.cpu(), ref)
 
 
