@@ -4,7 +4,9 @@
 Workload (the shape the metric is quoted on): one TP rank's share of a 288-expert layer,
 H=4096, I=768, 4 bpw trellis, an 8192-token chunk, top-8 routing skewed by a Zipf(1.1) prior; synthetic seeded
 inputs resident in HBM before timing starts. A step is one full grouped_prefill call (route sort, block table,
-gather + input Hadamard, gate|up GEMM, SwiGLU + down Hadamard, down GEMM with fp32 atomic scatter). Python's garbage
+gather + input Hadamard, gate|up GEMM, SwiGLU + down Hadamard, down GEMM and its output by token: at this size the
+runtime's default picks per-route fp32 rows summed per token in a fixed order, below 16384 routes the fp32 atomic
+scatter; --scatter overrides). Python's garbage
 collector runs, and its surviving objects are frozen, before every warm-up and timed region (quiet_gc): a full
 collection inside the timed steps would stall the launching thread for 30-40 ms.
 
@@ -12,7 +14,7 @@ Prints ONE JSON line: value = routed tokens/s (T*topk / step time); ms_per_step 
 median over the timed steps of each stage's HIP-event time on the launch stream (stage_ms_mean beside it); roofline of
 the dominant stage (the gate|up grouped GEMM: full expert tiles on the main kernel, each expert's last tile of <= 64
 rows on the thin kernel; MFMA-bound: algorithmic 4*R*H*I flop per stage call over its median duration) and
-roofline_down for the down GEMM + scatter (2*R*H*I flop). From the committed rocprofv3 summaries of the same workload
+roofline_down for the down GEMM and its output stages (2*R*H*I flop). From the committed rocprofv3 summaries of the same workload
 (profiles/grouped_prefill_headline_*.md): traffic (calibrated FETCH_SIZE + WRITE_SIZE bytes per stage call),
 stage_hbm_gbs (those bytes over this run's stage time) and counters (matrix-pipe and VALU busy fractions from
 SQ_VALU_MFMA_BUSY_CYCLES / SQ_ACTIVE_INST_VALU over GRBM_GUI_ACTIVE). cpu_baseline = a PyTorch CPU expert loop (the
@@ -46,13 +48,20 @@ HBM_PEAK_GBS = 8000.0
 # of the committed profile summaries): the GEMMs run full expert tiles on the main kernel and each expert's last tile
 # of <= 64 rows on the thin one.
 STAGE_KERNELS = {
-    "sort_routes": ("sort_hist_kernel", "sort_scatter_tiles_kernel"),         # + tile tables and the output clear
+    "sort_routes": ("sort_hist_kernel", "sort_scatter_tiles_kernel"),         # + the tile tables
     "row_had": ("row_had_t16_kernel<true>",),
     "gemm_gate_up": ("trellis_gemm_kernel<{bits}, 0, false, 4, 4>", "trellis_gemm_kernel<{bits}, 0, false, 1, 4>"),
     "act_had": ("act_had_t16_kernel<false, true>",),
-    "gemm_down_scatter": ("trellis_gemm_kernel<{bits}, 1, false, 4, 4>", "trellis_gemm_kernel<{bits}, 1, false, 1, 4>"),
 }
-GATE_UP_KERNELS = STAGE_KERNELS["gemm_gate_up"]
+# The down projection's stages by output method: the fp32 atomic scatter by token (mode 1), or per-route fp32 rows
+# (mode 2) and their fixed-order sum per token.
+DOWN_STAGE_KERNELS = {
+    "atomic": {"gemm_down_scatter": ("trellis_gemm_kernel<{bits}, 1, false, 4, 4>",
+                                     "trellis_gemm_kernel<{bits}, 1, false, 1, 4>")},
+    "combine": {"gemm_down_routes": ("trellis_gemm_kernel<{bits}, 3, false, 4, 4>",
+                                     "trellis_gemm_kernel<{bits}, 3, false, 1, 4>"),
+                "combine": ("combine_routes_cols_kernel<8>",)},
+}
 
 
 def parse():
@@ -74,8 +83,8 @@ def parse():
     ap.add_argument("--decode-no-compare", action="store_true",
                     help="with --decode: skip the prefill-path comparison (clean kernel traces of the decode path)")
     ap.add_argument("--stages", action="store_true", help="print per-stage ms to stderr")
-    ap.add_argument("--scatter", choices=["atomic", "combine"], default=None,
-                    help="down-projection output method (default: the runtime's, EXL3_GROUPED_SCATTER or atomic)")
+    ap.add_argument("--scatter", choices=["atomic", "combine", "auto"], default=None,
+                    help="down-projection output method (default: the runtime's, EXL3_GROUPED_SCATTER or auto)")
     ap.add_argument("--atomic-probe", action="store_true",
                     help="only time fp32 atomic adds of the down scatter's volume (65536 rows x 4096 floats into 8192 "
                          "token rows, torch index_add_) against a plain copy of the same rows, and exit")
@@ -191,7 +200,7 @@ def run(args, T=None, emit=True):
     R = T_ * k
     limit = 10.0
 
-    scatter = args.scatter or rt.scatter_mode()
+    scatter = rt.resolve_scatter(args.scatter, R)
     quiet_gc()                          # before the warm-up, whose steps then bring the clocks back up
     for _ in range(args.warmup):
         rt.grouped_prefill(xt, it, wt, TL, limit, scatter=scatter)
@@ -221,7 +230,8 @@ def run(args, T=None, emit=True):
     gate_up_flop = 4.0 * R * H * I
     down_flop = 2.0 * R * H * I
     achieved = gate_up_flop / (gemm_ms * 1e-3) / 1e12
-    down_ms = stage_avg.get("gemm_down_scatter", stage_avg.get("gemm_down_routes", float("nan")))
+    down_stages = list(DOWN_STAGE_KERNELS[scatter])
+    down_ms = sum(stage_avg[st] for st in down_stages)
     both_gemm_tflops = (gate_up_flop + down_flop) / ((gemm_ms + down_ms) * 1e-3) / 1e12
     layer_tflops = (gate_up_flop + down_flop) / (ms_per_step * 1e-3) / 1e12
     if args.stages or not emit:
@@ -232,11 +242,14 @@ def run(args, T=None, emit=True):
     workload = f"{cfg_name}: E={E} H={H} I={I} {bits}bpw T={T_} top{k} {cfg['routing']}"
     thin = rt.thin_tiles_enabled()
     kernels_of = {st: [kn.format(bits=bits) for kn in (ks if thin or not st.startswith("gemm") else ks[:1])]
-                  for st, ks in STAGE_KERNELS.items()}
+                  for st, ks in {**STAGE_KERNELS, **DOWN_STAGE_KERNELS[scatter]}.items()}
     gate_up_kernels = kernels_of["gemm_gate_up"]
-    down_kernels = kernels_of["gemm_down_scatter"]
+    down_gemm_kernels = kernels_of[down_stages[0]]
+    down_kernels = [kn for st in down_stages for kn in kernels_of[st]]
     down_achieved = down_flop / (down_ms * 1e-3) / 1e12
     stage_bytes = {st: traffic_from_profiles(cfg_name, ks) for st, ks in kernels_of.items()}
+    down_bytes = (sum(stage_bytes[st] for st in down_stages)
+                  if all(stage_bytes[st] is not None for st in down_stages) else None)
     stage_gbs = {st: (round(b / (stage_avg[st] * 1e-3) / 1e9, 1) if b and st in stage_avg else None)
                  for st, b in stage_bytes.items()}
     result = {
@@ -266,7 +279,7 @@ def run(args, T=None, emit=True):
         # matrix-pipe and VALU busy fractions of the GEMM stages from the committed SQ counter summary (against the
         # clock the counters measured, not the datasheet's)
         "counters": {"gemm_gate_up": mfma_busy_from_profiles(cfg_name, gate_up_kernels),
-                     "gemm_down_scatter": mfma_busy_from_profiles(cfg_name, down_kernels)},
+                     down_stages[0]: mfma_busy_from_profiles(cfg_name, down_gemm_kernels)},
         "gemm_tflops_gate_up_and_down": round(both_gemm_tflops, 1),
         "mfma_frac_layer": round(layer_tflops / MFMA_F16_PEAK_TFLOPS, 4),
         "roofline": {"kernel": "grouped_gemm gate|up stage (" + " + ".join(gate_up_kernels) + ")", "bound": "mfma",
@@ -275,10 +288,12 @@ def run(args, T=None, emit=True):
                      "traffic": traffic_from_profiles(cfg_name, gate_up_kernels),
                      "work_per_launch": f"4*R*H*I = {gate_up_flop:.4g} flop (R={R} routed rows) per stage call",
                      "peak_source": "MI355X dense fp16 MFMA, AMD datasheet (256 CUs x 2.4 GHz x 4096 flop/clk)"},
-        "roofline_down": {"kernel": "grouped_gemm down + fp32 atomic scatter stage (" + " + ".join(down_kernels) + ")",
+        "roofline_down": {"kernel": ("grouped_gemm down + fp32 atomic scatter stage (" if scatter == "atomic" else
+                                     "grouped_gemm down to per-route fp32 rows + combine_routes stages (")
+                          + " + ".join(down_kernels) + ")",
                           "bound": "mfma", "achieved": round(down_achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(down_achieved / MFMA_F16_PEAK_TFLOPS, 4),
-                          "traffic": stage_bytes["gemm_down_scatter"],
+                          "traffic": down_bytes,
                           "work_per_launch": f"2*R*H*I = {down_flop:.4g} flop per stage call"},
         "device": device_info(),
     }

@@ -14,7 +14,8 @@ Env:
   EXL3_GROUPED_THIN=0        run every expert tile on the main GEMM kernel (default: an expert's last tile of <= 64
                              rows runs on the thin kernel, four workgroups per CU, in a second launch)
   EXL3_GROUPED_SCATTER=...   down-projection output: "atomic" (fp32 atomic scatter by token, the reference's
-                             method) or "combine" (per-route fp32 rows + a fixed-order sum per token: deterministic)
+                             method), "combine" (per-route fp32 rows + a fixed-order sum per token: deterministic) or
+                             "auto" (the default: combine for chunks of >= COMBINE_MIN_ROUTES routes, else atomic)
   EXL3_GROUPED_WORKSPACE=0   allocate the prefill intermediates per call (default: one reused buffer per device)
   EXL3_GROUPED_LIB=<path>    prebuilt libexl3_grouped.so (default: exl3_grouped/libexl3_grouped.so beside this file)
 """
@@ -48,15 +49,31 @@ def _load_ext():
     return _ext
 
 
-SCATTER_MODES = ("atomic", "combine")
+SCATTER_MODES = ("atomic", "combine", "auto")
+# "auto" takes the combine method from this many routes (tokens x topk) up: the per-route rows plus the sum per token
+# cost less than the atomic scatter once most rows sit in full 256-row expert tiles, whose epilogues are atomic-bound
+# (headline routing: 2.12-2.13 vs 2.17 ms at 8192 tokens, 0.802 vs 0.817 ms at 2048), and more when most tiles are
+# thin (1024 tokens, softmax routing: 0.74 vs 0.725 ms). The combine rows take routes x hidden fp32 of workspace.
+COMBINE_MIN_ROUTES = 16384
 TILE_ROWS_CHOICES = (128, 256, 512)
 TILE_ROWS = 256
 
 
 def scatter_mode() -> str:
-    m = os.environ.get("EXL3_GROUPED_SCATTER", "atomic")
+    m = os.environ.get("EXL3_GROUPED_SCATTER", "auto")
     if m not in SCATTER_MODES:
         raise RuntimeError(f"EXL3_GROUPED_SCATTER must be one of {SCATTER_MODES}, got {m!r}")
+    return m
+
+
+def resolve_scatter(scatter: str | None, routes: int) -> str:
+    """The down-projection output method of a call of `routes` routes: "atomic" or "combine" ("auto" and None, which
+    means the EXL3_GROUPED_SCATTER setting, resolve by COMBINE_MIN_ROUTES)."""
+    m = scatter or scatter_mode()
+    if m not in SCATTER_MODES:
+        raise RuntimeError(f"scatter must be one of {SCATTER_MODES}, got {m!r}")
+    if m == "auto":
+        return "combine" if routes >= COMBINE_MIN_ROUTES else "atomic"
     return m
 
 
@@ -147,7 +164,7 @@ def reserve_prefill_workspace(device, tokens: int, topk: int, n_experts: int, hi
                               scatter: str | None = None, rows_per_tile: int | None = None) -> torch.Tensor:
     """Size the device's prefill workspace for a chunk of `tokens` (the largest the scheduler sends) before the first
     call, e.g. ahead of memory profiling or graph capture, so that no later call grows it. Returns the buffer."""
-    scatter = scatter or scatter_mode()
+    scatter = resolve_scatter(scatter, tokens * topk)
     tr = rows_per_tile or tile_rows()
     thin = thin_tiles_enabled()
     sizing = _Carve()
@@ -186,11 +203,10 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     Restates kernel/exl3_grouped_runtime.py:50-83 with the route sort on the GPU (sort_routes).
     stage_events: if a list is given, a timing event recorded on the current stream after each stage is appended
     as (stage name, event), after a leading ("start", event).
-    scatter: "atomic" or "combine" (default: EXL3_GROUPED_SCATTER, else "atomic").
+    scatter: "atomic", "combine" or "auto" (default: EXL3_GROUPED_SCATTER, else "auto"; resolve_scatter).
     thin_tiles: run each expert's last tile of <= 64 rows on the thin GEMM kernel (default: EXL3_GROUPED_THIN, else
-    on; atomic scatter only). Same arithmetic per row, so the same result."""
+    on). Same arithmetic per row, so the same result."""
     gp = _load_ext()
-    scatter = scatter or scatter_mode()
 
     def mark(name):
         if stage_events is not None:
@@ -203,6 +219,7 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     T, K = x2d.shape
     topk = ids.shape[1]
     R = T * topk
+    scatter = resolve_scatter(scatter, R)
     E = int(layer.w13_trellis.shape[0])
     I = int(layer._exl3_intermediate_local)
     x16 = x2d.to(torch.float16).contiguous()

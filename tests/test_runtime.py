@@ -76,6 +76,24 @@ def test_patch_hook_is_idempotent(tmp_path):
     compile(text, str(target), "exec")
 
 
+def test_scatter_mode_resolution(monkeypatch):
+    """"auto" (the default) takes the deterministic combine method from COMBINE_MIN_ROUTES routes up, the atomic scatter
+    below; explicit modes pass through; anything else is rejected like the reference's checks."""
+    monkeypatch.delenv("EXL3_GROUPED_SCATTER", raising=False)
+    assert rt.scatter_mode() == "auto"
+    n = rt.COMBINE_MIN_ROUTES
+    assert rt.resolve_scatter(None, n) == "combine" and rt.resolve_scatter(None, n - 1) == "atomic"
+    assert rt.resolve_scatter("auto", 8192 * 8) == "combine" and rt.resolve_scatter("auto", 1024 * 8) == "atomic"
+    assert rt.resolve_scatter("atomic", 10 ** 6) == "atomic" and rt.resolve_scatter("combine", 8) == "combine"
+    monkeypatch.setenv("EXL3_GROUPED_SCATTER", "atomic")
+    assert rt.resolve_scatter(None, 10 ** 6) == "atomic"
+    monkeypatch.setenv("EXL3_GROUPED_SCATTER", "bogus")
+    with pytest.raises(RuntimeError, match="EXL3_GROUPED_SCATTER"):
+        rt.resolve_scatter(None, 8)
+    with pytest.raises(RuntimeError, match="scatter must be one of"):
+        rt.resolve_scatter("sum", 8)
+
+
 def test_generators_are_deterministic():
     a = synth.make_config("tiny", seed=3)
     b = synth.make_config("tiny", seed=3)
