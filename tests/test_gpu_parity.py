@@ -750,21 +750,22 @@ def test_prefill_workspace_reuse(dev, monkeypatch):
         assert ((g - ref).norm() / ref.norm()).item() < 1e-6, n
 
 
-def test_prefill_graph_capture_replays(dev):
+@pytest.mark.parametrize("scatter", ["atomic", "combine"])
+def test_prefill_graph_capture_replays(dev, scatter):
     """grouped_prefill captured in a HIP graph (the prefill workspace already sized; the output clear is a kernel, no
     memset node): replays with fresh inputs in the captured buffers match eager calls, with eager work between the
-    replays."""
+    replays, for both down-projection output methods."""
     L, x, ids, w, cfg = synth.make_config("tiny", seed=11)
     TL = synth.to_device(L, dev)
     xs, it, wt = t16(x, dev), t16(ids, dev), t16(w, dev)
-    rt.grouped_prefill(xs, it, wt, TL, LIMIT)
+    rt.grouped_prefill(xs, it, wt, TL, LIMIT, scatter=scatter)
     torch.cuda.synchronize()
     cap = torch.cuda.Stream()
     cap.wait_stream(torch.cuda.current_stream())
     g = torch.cuda.CUDAGraph()
     with torch.cuda.stream(cap):
         with torch.cuda.graph(g, stream=cap):
-            out = rt.grouped_prefill(xs, it, wt, TL, LIMIT)
+            out = rt.grouped_prefill(xs, it, wt, TL, LIMIT, scatter=scatter)
     torch.cuda.current_stream().wait_stream(cap)
     for seed in (1, 2, 3):
         ids2, w2 = synth.make_routing(cfg["routing"], cfg["T"], cfg["E"], cfg["topk"], seed=seed)
@@ -774,9 +775,11 @@ def test_prefill_graph_capture_replays(dev):
         g.replay()
         torch.cuda.synchronize()
         got = out.clone()
-        ref = rt.grouped_prefill(xs.clone(), it.clone(), wt.clone(), TL, LIMIT)
+        ref = rt.grouped_prefill(xs.clone(), it.clone(), wt.clone(), TL, LIMIT, scatter=scatter)
         torch.cuda.synchronize()
         assert ((got - ref).norm() / ref.norm()).item() < 1e-6, seed
+        if scatter == "combine":                                  # fixed summation order: bit-identical
+            assert torch.equal(got, ref), seed
 
 
 def test_install_engages_grouped_path(dev, monkeypatch):
