@@ -13,4 +13,4 @@ std::string& last_error()
 
 extern "C" const char* exl3_last_error(void) { return exl3::last_error().c_str(); }
 
-extern "C" int exl3_abi_version(void) { return 9; }
+extern "C" int exl3_abi_version(void) { return 10; }

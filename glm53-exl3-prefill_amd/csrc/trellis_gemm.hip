@@ -17,9 +17,31 @@ namespace {
 constexpr int COMBINE_THREADS = 256;
 constexpr int COMBINE_MAX_TOPK = 32;
 
-template <int TOPK>
+// fp32 -> bf16 bits, round to nearest even, every NaN -> 0x7FC0: torch's float -> bfloat16 conversion.
+__device__ __forceinline__ uint32_t f2bf(float f)
+{
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Four consecutive outputs (float4 index i4) in the output's dtype: fp32, or rounded once to bf16 / fp16 (RNE), which
+// is what casting the fp32 sums afterwards gives.
+template <int OUT>
+__device__ __forceinline__ void store_out4(void* out, int64_t i4, const float4& v)
+{
+    if constexpr (OUT == EXL3_DTYPE_F32)
+        reinterpret_cast<float4*>(out)[i4] = v;
+    else if constexpr (OUT == EXL3_DTYPE_BF16)
+        reinterpret_cast<uint2*>(out)[i4] = make_uint2(f2bf(v.x) | f2bf(v.y) << 16, f2bf(v.z) | f2bf(v.w) << 16);
+    else
+        reinterpret_cast<uint2*>(out)[i4] = make_uint2((uint32_t) f2h(v.x) | (uint32_t) f2h(v.y) << 16,
+                                                       (uint32_t) f2h(v.z) | (uint32_t) f2h(v.w) << 16);
+}
+
+template <int TOPK, int OUT>
 __global__ __launch_bounds__(COMBINE_THREADS)
-void combine_routes_kernel(const float4* __restrict__ partial, float4* __restrict__ out, const void* __restrict__ ids,
+void combine_routes_kernel(const float4* __restrict__ partial, void* __restrict__ out, const void* __restrict__ ids,
                            int ids_dtype, int n_experts, int64_t tokens, int topk_rt, int64_t n4)
 {
     const int topk = TOPK > 0 ? TOPK : topk_rt;
@@ -59,7 +81,7 @@ void combine_routes_kernel(const float4* __restrict__ partial, float4* __restric
                     const float4 v = rows[j * n4 + c];
                     acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
                 }
-            out[t * n4 + c] = acc;
+            store_out4<OUT>(out, t * n4 + c, acc);
         }
     }
 }
@@ -67,9 +89,9 @@ void combine_routes_kernel(const float4* __restrict__ partial, float4* __restric
 // The same sum for topk = TOPK when the row width is a multiple of COMBINE_THREADS float4s: one workgroup per (token,
 // COMBINE_THREADS float4 columns), so the token is uniform and its ids arrive through scalar loads issued after the
 // lane's TOPK row loads (rows read once: non-temporal). Grid = tokens x n4 / COMBINE_THREADS (fits 31 bits).
-template <int TOPK>
+template <int TOPK, int OUT>
 __global__ __launch_bounds__(COMBINE_THREADS)
-void combine_routes_cols_kernel(const float4* __restrict__ partial, float4* __restrict__ out,
+void combine_routes_cols_kernel(const float4* __restrict__ partial, void* __restrict__ out,
                                 const void* __restrict__ ids, int ids_dtype, int n_experts, int64_t n4)
 {
     typedef float fv4 __attribute__((ext_vector_type(4)));
@@ -104,7 +126,7 @@ void combine_routes_cols_kernel(const float4* __restrict__ partial, float4* __re
         acc.x += on ? v[j][0] : 0.f; acc.y += on ? v[j][1] : 0.f;
         acc.z += on ? v[j][2] : 0.f; acc.w += on ? v[j][3] : 0.f;
     }
-    out[t * n4 + c] = acc;
+    store_out4<OUT>(out, t * n4 + c, acc);
 }
 
 // ------------------------------------------------------------------------------------------- reconstruct
@@ -518,29 +540,53 @@ extern "C" int exl3_linear(const uint16_t* x, int64_t m, int k, const uint16_t* 
     return hip_status("linear");
 }
 
-extern "C" int exl3_combine_routes(const float* partial, float* out, const void* topk_ids, int ids_dtype, int n_experts,
-                                   int64_t tokens, int topk, int64_t n, void* stream)
+namespace exl3 {
+namespace {
+template <int OUT>
+void launch_combine(const float4* p4, void* out, const void* topk_ids, int ids_dtype, int n_experts, int64_t tokens,
+                    int topk, int64_t n4, hipStream_t s)
+{
+    const int64_t blocks = std::min<int64_t>(tokens, 65536), col_blocks = tokens * (n4 / COMBINE_THREADS);
+    if (topk == 8 && n4 % COMBINE_THREADS == 0 && col_blocks <= 0x7FFFFFFF)
+        combine_routes_cols_kernel<8, OUT><<<(unsigned) col_blocks, COMBINE_THREADS, 0, s>>>(
+            p4, out, topk_ids, ids_dtype, n_experts, n4);
+    else if (topk == 8)
+        combine_routes_kernel<8, OUT><<<(unsigned) blocks, COMBINE_THREADS, 0, s>>>(
+            p4, out, topk_ids, ids_dtype, n_experts, tokens, topk, n4);
+    else
+        combine_routes_kernel<0, OUT><<<(unsigned) blocks, COMBINE_THREADS, 0, s>>>(
+            p4, out, topk_ids, ids_dtype, n_experts, tokens, topk, n4);
+}
+}  // namespace
+}  // namespace exl3
+
+extern "C" int exl3_combine_routes_dt(const float* partial, void* out, int out_dtype, const void* topk_ids,
+                                      int ids_dtype, int n_experts, int64_t tokens, int topk, int64_t n, void* stream)
 {
     EXL3_CHECK(tokens >= 0 && topk > 0 && n > 0 && n % 4 == 0, "combine: bad shape");
     EXL3_CHECK(!topk_ids || ids_dtype == EXL3_DTYPE_I64 || ids_dtype == EXL3_DTYPE_I32, "topk_ids must be int64 or int32");
+    EXL3_CHECK(out_dtype == EXL3_DTYPE_F32 || out_dtype == EXL3_DTYPE_BF16 || out_dtype == EXL3_DTYPE_F16,
+               "combine: out must be fp32, bf16 or fp16");
     if (tokens == 0) return EXL3_OK;
     EXL3_CHECK(partial && out, "null pointer");
-    EXL3_CHECK(aligned16(partial) && aligned16(out), "partial/out must be 16-byte aligned");
+    EXL3_CHECK(aligned16(partial) && (reinterpret_cast<uintptr_t>(out) & (out_dtype == EXL3_DTYPE_F32 ? 15 : 7)) == 0,
+               "partial must be 16-byte aligned, out 16-byte (fp32) or 8-byte (bf16 / fp16) aligned");
     EXL3_CHECK(topk <= COMBINE_MAX_TOPK, "combine: topk above %d", COMBINE_MAX_TOPK);
-    const int64_t blocks = std::min<int64_t>(tokens, 65536);
     const auto* p4 = reinterpret_cast<const float4*>(partial);
-    auto* o4 = reinterpret_cast<float4*>(out);
-    const int64_t n4 = n / 4, col_blocks = tokens * (n4 / COMBINE_THREADS);
-    if (topk == 8 && n4 % COMBINE_THREADS == 0 && col_blocks <= 0x7FFFFFFF)
-        combine_routes_cols_kernel<8><<<(unsigned) col_blocks, COMBINE_THREADS, 0, as_stream(stream)>>>(
-            p4, o4, topk_ids, ids_dtype, n_experts, n4);
-    else if (topk == 8)
-        combine_routes_kernel<8><<<(unsigned) blocks, COMBINE_THREADS, 0, as_stream(stream)>>>(
-            p4, o4, topk_ids, ids_dtype, n_experts, tokens, topk, n / 4);
+    const hipStream_t s = as_stream(stream);
+    if (out_dtype == EXL3_DTYPE_F32)
+        launch_combine<EXL3_DTYPE_F32>(p4, out, topk_ids, ids_dtype, n_experts, tokens, topk, n / 4, s);
+    else if (out_dtype == EXL3_DTYPE_BF16)
+        launch_combine<EXL3_DTYPE_BF16>(p4, out, topk_ids, ids_dtype, n_experts, tokens, topk, n / 4, s);
     else
-        combine_routes_kernel<0><<<(unsigned) blocks, COMBINE_THREADS, 0, as_stream(stream)>>>(
-            p4, o4, topk_ids, ids_dtype, n_experts, tokens, topk, n / 4);
+        launch_combine<EXL3_DTYPE_F16>(p4, out, topk_ids, ids_dtype, n_experts, tokens, topk, n / 4, s);
     return hip_status("combine_routes");
+}
+
+extern "C" int exl3_combine_routes(const float* partial, float* out, const void* topk_ids, int ids_dtype, int n_experts,
+                                   int64_t tokens, int topk, int64_t n, void* stream)
+{
+    return exl3_combine_routes_dt(partial, out, EXL3_DTYPE_F32, topk_ids, ids_dtype, n_experts, tokens, topk, n, stream);
 }
 
 extern "C" int64_t exl3_smem_bytes(int64_t variant)

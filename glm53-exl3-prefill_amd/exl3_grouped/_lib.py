@@ -50,6 +50,7 @@ SIGNATURES = {
     "exl3_grouped_gemm_clear": (I32, [P, I64, I32, I32, P, P, I64, I32, I32, I32, P, P, I64, P, P, I32, I32, P, P,
                                       I32, P, P, P, P, I64, I32, I32, P, I64, P]),
     "exl3_combine_routes": (I32, [P, P, P, I32, I32, I64, I32, I64, P]),
+    "exl3_combine_routes_dt": (I32, [P, P, I32, P, I32, I32, I64, I32, I64, P]),
     "exl3_fat_gemm": (I32, [P, I64, I32, P, I32, I32, I32, P, I64, P, I64, I32, I32, I32, I32, P]),
     "exl3_fat_gemm_scatter": (I32, [P, I64, I32, P, I32, I32, I32, P, I64, P, I64, P, P, I32, I32, I32, I32, P]),
     "exl3_smem_bytes": (I64, [I64]),
@@ -67,7 +68,7 @@ SIGNATURES = {
                                       P, I64, P, I64, P, I64, F32, P, P]),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lib = None
 _path = None

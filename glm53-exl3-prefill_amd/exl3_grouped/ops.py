@@ -382,10 +382,12 @@ def grouped_gemm(a: torch.Tensor, packed_gate: torch.Tensor, packed_up: Optional
 def combine_routes(partial: torch.Tensor, out: torch.Tensor, topk: int, topk_ids: Optional[torch.Tensor] = None,
                    n_experts: int = 0) -> None:
     """out[t] = sum_j partial[t*topk + j] in order j = 0..topk-1 (new; pairs with grouped_gemm mode 2). Routes whose id
-    in topk_ids lies outside [0, n_experts) are skipped."""
+    in topk_ids lies outside [0, n_experts) are skipped. out fp32, or bf16 / fp16: each fp32 sum rounded once, as
+    casting the fp32 result would (the reference wrapper's out.to(x.dtype), kernel/exl3_grouped_runtime.py:107)."""
     T, n = out.shape
-    _check(partial.dtype == torch.float32 and out.dtype == torch.float32 and partial.is_contiguous() and
-           out.is_contiguous(), "combine: fp32 contiguous tensors")
+    _check(partial.dtype == torch.float32 and out.dtype in (torch.float32, torch.bfloat16, torch.float16) and
+           partial.is_contiguous() and out.is_contiguous(),
+           "combine: partial fp32, out fp32 / bf16 / fp16, contiguous")
     _check(partial.dim() == 2 and partial.size(0) == T * topk and partial.size(1) == n and n % 4 == 0,
            "combine: partial must be [T*topk, N], N % 4 == 0")
     _check(1 <= int(topk) <= 32, "combine: topk must be in [1, 32]")
@@ -394,7 +396,7 @@ def combine_routes(partial: torch.Tensor, out: torch.Tensor, topk: int, topk_ids
                topk_ids.numel() == T * topk and 0 < n_experts <= 1024, "combine: topk_ids [T, topk] int64/int32")
     dev = _require_cuda(partial, out, topk_ids)
     with _On(dev) as s:
-        _lib.call("exl3_combine_routes", _p(partial), _p(out), _p(topk_ids),
+        _lib.call("exl3_combine_routes_dt", _p(partial), _p(out), _DT[out.dtype], _p(topk_ids),
                   _DT[topk_ids.dtype] if topk_ids is not None else 0, int(n_experts), T, int(topk), n, s)
 
 

@@ -198,14 +198,17 @@ def _prefill_plan(gp, T: int, K: int, topk: int, E: int, I: int, tr: int, scatte
 
 def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, layer, limit: float,
                     stage_events: list | None = None, scatter: str | None = None,
-                    rows_per_tile: int | None = None, thin_tiles: bool | None = None) -> torch.Tensor:
+                    rows_per_tile: int | None = None, thin_tiles: bool | None = None,
+                    out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """x2d [T, K] (any float dtype), ids [T, topk] (int64 or int32), weights [T, topk] -> out [T, K] fp32.
     Restates kernel/exl3_grouped_runtime.py:50-83 with the route sort on the GPU (sort_routes).
     stage_events: if a list is given, a timing event recorded on the current stream after each stage is appended
     as (stage name, event), after a leading ("start", event).
     scatter: "atomic", "combine" or "auto" (default: EXL3_GROUPED_SCATTER, else "auto"; resolve_scatter).
     thin_tiles: run each expert's last tile of <= 64 rows on the thin GEMM kernel (default: EXL3_GROUPED_THIN, else
-    on). Same arithmetic per row, so the same result."""
+    on). Same arithmetic per row, so the same result.
+    out_dtype (new): return out in this dtype (bf16 or fp16), as out.to(out_dtype) of the fp32 result would; the combine
+    method writes it directly (no fp32 round trip through memory), the atomic scatter casts its fp32 target."""
     gp = _load_ext()
 
     def mark(name):
@@ -278,7 +281,7 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
                             thin_expert, thin_row0, counts, expert_row0, token_sorted, weight_sorted, out, 1,
                             tile_rows=THIN_ROWS, a_layout=1, a_rows=R)
         mark("gemm_down_scatter")
-        return out
+        return out if out_dtype is None else out.to(out_dtype)
     partial = B["partial"]
     gp.grouped_gemm(act, layer.w2_trellis, None, layer.w2_svh, None,
                     block_expert, block_row0, counts, expert_row0, None, weight_sorted, partial, 2,
@@ -288,10 +291,11 @@ def grouped_prefill(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
                         thin_expert, thin_row0, counts, expert_row0, None, weight_sorted, partial, 2,
                         route_index=route_index, tile_rows=THIN_ROWS, a_layout=1, a_rows=R)
     mark("gemm_down_routes")
-    out = torch.empty(T, K, dtype=torch.float32, device=dev)
+    direct = out_dtype in (torch.bfloat16, torch.float16)
+    out = torch.empty(T, K, dtype=out_dtype if direct else torch.float32, device=dev)
     gp.combine_routes(partial, out, topk, ids, E)
     mark("combine")
-    return out
+    return out if direct or out_dtype is None else out.to(out_dtype)
 
 
 def grouped_prefill_from_logits(x2d: torch.Tensor, router_logits: torch.Tensor, layer, limit: float,
@@ -376,7 +380,8 @@ def install(ov):
             out = moe_decode(x2d, ids, weights, layer, float(limit), cap=cap)
             layer._exl3_last_apply = "decode"
             return out.to(dtype=x.dtype)
-        out = grouped_prefill(x2d, ids, weights, layer, float(limit))
+        # the output in x.dtype straight from the combine pass where it runs (the same values as out.to(x.dtype))
+        out = grouped_prefill(x2d, ids, weights, layer, float(limit), out_dtype=x.dtype)
         layer._exl3_last_apply = "grouped"
         if not _logged:
             logger.info("EXL3 grouped prefill engaged (tokens=%d > cap=%d, experts=%d)", tokens, cap,

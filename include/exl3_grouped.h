@@ -261,6 +261,15 @@ int exl3_combine_routes(const float* partial, float* out, const void* topk_ids, 
                         int64_t tokens, int topk, int64_t n, void* stream);
 
 /*
+ * exl3_combine_routes with the sums written in out_dtype (new): EXL3_DTYPE_F32, or EXL3_DTYPE_BF16 / EXL3_DTYPE_F16,
+ * each fp32 sum rounded once to nearest even (every NaN -> bf16 0x7FC0) -- bit for bit the fp32 combine followed by
+ * the cast the reference's wrapper applies (kernel/exl3_grouped_runtime.py:107, out.to(x.dtype)), without the fp32
+ * round trip. out [tokens, n] of that dtype, 16-byte (fp32) or 8-byte aligned.
+ */
+int exl3_combine_routes_dt(const float* partial, void* out, int out_dtype, const void* topk_ids, int ids_dtype,
+                           int n_experts, int64_t tokens, int topk, int64_t n, void* stream);
+
+/*
  * Per-expert weight-stationary trellis GEMM, the exl3_fat_gemm drop-in (pybind ops fat_gemm_v2 /
  * fat_gemm_v2_scatter / smem_bytes, kernel/exl3_fat_gemm_v2.cu:236-333; PR77 signature
  * exl3_fat_gemm(a, packed, out, svh, K, mcg, mul1), kernel/test_fat_v2.py:122,134).

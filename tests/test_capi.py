@@ -82,6 +82,10 @@ def test_grouped_gemm_contract():
     assert "route_index" in _gemm(mode=2)[1]
     assert "combine" in rc_and_msg("exl3_combine_routes", FAKE, FAKE, None, 4, 8, 10, 8, 6, None)[1]
     assert "topk above 32" in rc_and_msg("exl3_combine_routes", FAKE, FAKE, None, 4, 8, 10, 33, 8, None)[1]
+    assert "fp32, bf16 or fp16" in rc_and_msg("exl3_combine_routes_dt", FAKE, FAKE, _lib.DTYPE_I32, None, 4, 8, 10, 8,
+                                              8, None)[1]
+    assert "aligned" in rc_and_msg("exl3_combine_routes_dt", FAKE, ctypes.c_void_p(0x1004), _lib.DTYPE_BF16, None, 4, 8, 10, 8, 8,
+                                   None)[1]
     a = dict(a=FAKE, a_rows=256, size_k=512, a_layout=0, pg=FAKE, pu=None, es=32 * 16 * 64, tk=32, tn=16, bits=4,
              sg=FAKE, su=None, ss=256, be=FAKE, br=FAKE, mb=10, tile_rows=96, counts=FAKE, row0=FAKE, E=8, tok=FAKE,
              rw=FAKE, ri=None, out=FAKE, out_rows=64, mode=1)

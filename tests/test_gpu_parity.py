@@ -557,6 +557,43 @@ def test_combine_order_is_route_order(dev, N):
     assert torch.equal(out.cpu(), ref)
 
 
+@pytest.mark.parametrize("N", [4096, 48])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_combine_into_half_dtypes_is_the_cast(dev, N, dtype):
+    """combine_routes writing bf16 / fp16 gives exactly the fp32 combine followed by torch's cast: one rounding to nearest
+    even, NaN and infinities, fp16 overflow to infinity, bf16 ties."""
+    T, k = 19, 8
+    rng = np.random.default_rng(N + 7)
+    partial = torch.from_numpy(rng.standard_normal((T * k, N)).astype(np.float32) * 300).to(dev)
+    partial[3, :8] = torch.tensor([float("nan"), float("inf"), -float("inf"), 7e4, -7e4, 1e-8, -0.0, 3.0], device=dev)
+    bf_tie = np.array([0x3F808000, 0x3F818000, 0xBF808000, 0x7F7FFFFF], dtype=np.uint32).view(np.float32)
+    partial[k * 5, :4] = torch.from_numpy(bf_tie).to(dev)         # token 5: ties and the largest finite fp32
+    partial[k * 5 + 1:k * 6, :4] = 0.0
+    ids = torch.from_numpy(rng.integers(-1, 9, (T, k))).to(dev)
+    ids[5] = torch.arange(k, device=dev)
+    ref32 = torch.empty(T, N, device=dev)
+    gp.combine_routes(partial, ref32, k, ids, 8)
+    out = torch.full((T, N), 1.0, dtype=dtype, device=dev)
+    gp.combine_routes(partial, out, k, ids, 8)
+    assert torch.equal(out.view(torch.int16), ref32.to(dtype).view(torch.int16))
+
+
+@pytest.mark.parametrize("scatter", ["atomic", "combine"])
+def test_prefill_out_dtype(dev, scatter):
+    """grouped_prefill(out_dtype=bf16) is grouped_prefill(...).to(bf16) bit for bit (the combine method writes it
+    directly; the atomic scatter casts its fp32 target)."""
+    L, x, ids, w, cfg = synth.make_config("tiny", seed=12)
+    TL = synth.to_device(L, dev)
+    args = (t16(x, dev).to(torch.bfloat16), t16(ids, dev), t16(w, dev), TL, LIMIT)
+    ref = rt.grouped_prefill(*args, scatter=scatter)
+    got = rt.grouped_prefill(*args, scatter=scatter, out_dtype=torch.bfloat16)
+    assert got.dtype == torch.bfloat16 and ref.dtype == torch.float32
+    if scatter == "combine":
+        assert torch.equal(got.view(torch.int16), ref.to(torch.bfloat16).view(torch.int16))
+    else:                                                          # atomic order may differ between the two calls
+        assert torch.allclose(got.float(), ref.to(torch.bfloat16).float(), rtol=1e-2, atol=1e-2)
+
+
 # ------------------------------------------------------------------------------------------- dense EXL3 linear
 @pytest.mark.parametrize("M,K,N,bits", [(1, 4096, 1536, 4), (300, 768, 4096, 4), (4096, 4096, 1536, 4),
                                         (200, 4096, 1536, 3), (70, 1024, 512, 2), (0, 512, 256, 4)])
