@@ -60,7 +60,7 @@ DOWN_STAGE_KERNELS = {
                                      "trellis_gemm_kernel<{bits}, 1, false, 1, 4>")},
     "combine": {"gemm_down_routes": ("trellis_gemm_kernel<{bits}, 3, false, 4, 4>",
                                      "trellis_gemm_kernel<{bits}, 3, false, 1, 4>"),
-                "combine": ("combine_routes_cols_kernel<8>",)},
+                "combine": ("combine_routes_cols_kernel<8, 0>",)},
 }
 
 
