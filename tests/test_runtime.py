@@ -94,6 +94,23 @@ def test_scatter_mode_resolution(monkeypatch):
         rt.resolve_scatter("sum", 8)
 
 
+def test_prefill_workspace_holds_the_combine_rows(monkeypatch):
+    """The prefill plan sized for a chunk that "auto" sends down the combine path holds the per-route fp32 rows
+    (routes x hidden) and the route index on top of what the atomic path needs; below the threshold it does not."""
+    monkeypatch.delenv("EXL3_GROUPED_SCATTER", raising=False)
+    gp = rt._load_ext()
+
+    def size(T, scatter):
+        c = rt._Carve()
+        rt._prefill_plan(gp, T, 4096, 8, 288, 768, 256, rt.resolve_scatter(scatter, T * 8), True)(c)
+        return c.off
+
+    T = rt.COMBINE_MIN_ROUTES // 8
+    extra = size(T, "auto") - size(T, "atomic")
+    assert T * 8 * 4096 * 4 + T * 8 * 4 <= extra <= T * 8 * 4096 * 4 + T * 8 * 4 + 2 * 256
+    assert size(T - 1, "auto") == size(T - 1, "atomic")
+
+
 def test_generators_are_deterministic():
     a = synth.make_config("tiny", seed=3)
     b = synth.make_config("tiny", seed=3)
