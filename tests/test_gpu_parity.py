@@ -726,6 +726,8 @@ def test_headline_sampled_tokens_and_properties(dev, scatter):
     perm = np.random.default_rng(1).permutation(cfg["T"])
     outp = run_layer(L, x[perm], ids[perm], w[perm], dev, scatter)
     assert (outp - out[torch.from_numpy(perm).to(dev)]).norm().item() <= 1e-6 * out.norm().item()
+    if scatter == "combine":      # every route's row is computed position-independently and summed in slot order
+        assert torch.equal(outp.view(torch.int32), out[torch.from_numpy(perm).to(dev)].view(torch.int32))
 
 
 @pytest.mark.parametrize("T", [1024, 2048, 4096])
