@@ -277,6 +277,18 @@ def test_prefill_thin_tiles_match_one_table(dev):
     assert ((c - b).norm() / b.norm()).item() < 1e-6
 
 
+def test_prefill_tile_heights_agree_bitwise(dev):
+    """128-, 256- and 512-row expert tiles (the 4-wave kernel, and the 8-wave kernel with its interleaved row groups)
+    give the same output bit for bit with the combine output: a row's sums over K run in the same order whatever the
+    tile height or the wave that multiplies it."""
+    L, x, ids, w, cfg = synth.make_config("headline", seed=5, T=2048)
+    TL = synth.to_device(L, dev)
+    args = (t16(x, dev), t16(ids, dev), t16(w, dev), TL, LIMIT)
+    outs = [rt.grouped_prefill(*args, scatter="combine", rows_per_tile=tr) for tr in (128, 256, 512)]
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int32), outs[0].view(torch.int32))
+
+
 def _margins(logits, bias, k):
     """Per token: is the chosen set unambiguous (k-th and (k+1)-th selection scores more than 1e-5 apart), and is the
     order too (every adjacent pair among the first k + 1 apart)? fp32 sigmoids may differ by an ulp between devices."""
