@@ -16,6 +16,7 @@ Env:
   EXL3_GROUPED_SCATTER=...   down-projection output: "atomic" (fp32 atomic scatter by token, the reference's
                              method), "combine" (per-route fp32 rows + a fixed-order sum per token: deterministic) or
                              "auto" (the default: combine for chunks of >= COMBINE_MIN_ROUTES routes, else atomic)
+  EXL3_GROUPED_COMBINE_MIN_ROUTES=<n>   the "auto" threshold in routes (tokens x topk; default 16384)
   EXL3_GROUPED_WORKSPACE=0   allocate the prefill intermediates per call (default: one reused buffer per device)
   EXL3_GROUPED_LIB=<path>    prebuilt libexl3_grouped.so (default: exl3_grouped/libexl3_grouped.so beside this file)
 """
@@ -73,7 +74,14 @@ def resolve_scatter(scatter: str | None, routes: int) -> str:
     if m not in SCATTER_MODES:
         raise RuntimeError(f"scatter must be one of {SCATTER_MODES}, got {m!r}")
     if m == "auto":
-        return "combine" if routes >= COMBINE_MIN_ROUTES else "atomic"
+        v = os.environ.get("EXL3_GROUPED_COMBINE_MIN_ROUTES")
+        try:
+            threshold = COMBINE_MIN_ROUTES if v is None else int(v)
+        except ValueError:
+            threshold = -1
+        if threshold < 0:
+            raise RuntimeError(f"EXL3_GROUPED_COMBINE_MIN_ROUTES must be a non-negative integer, got {v!r}")
+        return "combine" if routes >= threshold else "atomic"
     return m
 
 

@@ -92,6 +92,12 @@ def test_scatter_mode_resolution(monkeypatch):
         rt.resolve_scatter(None, 8)
     with pytest.raises(RuntimeError, match="scatter must be one of"):
         rt.resolve_scatter("sum", 8)
+    monkeypatch.setenv("EXL3_GROUPED_SCATTER", "auto")
+    monkeypatch.setenv("EXL3_GROUPED_COMBINE_MIN_ROUTES", "64")
+    assert rt.resolve_scatter(None, 64) == "combine" and rt.resolve_scatter(None, 63) == "atomic"
+    monkeypatch.setenv("EXL3_GROUPED_COMBINE_MIN_ROUTES", "-3")
+    with pytest.raises(RuntimeError, match="COMBINE_MIN_ROUTES"):
+        rt.resolve_scatter(None, 8)
 
 
 def test_prefill_workspace_holds_the_combine_rows(monkeypatch):
