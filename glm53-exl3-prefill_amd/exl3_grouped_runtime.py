@@ -103,7 +103,8 @@ def thin_tiles_enabled() -> bool:
 
 THIN_ROWS = 64
 
-# The prefill intermediates (sorted routes, tile tables, h13, gu, act: ~0.85 GB at 8192 tokens) live in one buffer per
+# The prefill intermediates (sorted routes, tile tables, h13, gu, act: ~0.85 GB at 8192 tokens; with the combine output
+# also the per-route fp32 rows, 1.07 GB more at H = 4096) live in one buffer per
 # device, reused by every call and grown (never shrunk) when a call needs more: steady-state calls allocate nothing but
 # their output, and the kernels keep working on memory they have touched before. Calls on one device must be ordered on
 # one stream (the model runner's); EXL3_GROUPED_WORKSPACE=0 allocates per call instead. A buffer that a larger call
