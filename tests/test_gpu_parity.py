@@ -217,15 +217,17 @@ def fused_prep(ids_t, w_t, E, tile_rows, fused, zero_n=0):
     return res
 
 
-@pytest.mark.parametrize("tile_rows", [256, 128, 512])
-@pytest.mark.parametrize("kind,T,E,k", ROUTINGS)
+# every routing at the default 256-row tiles; 128- and 512-row tiles on two of them
+SPLIT_TILE_CASES = ([r + (256,) for r in ROUTINGS] +
+                    [r + (tr,) for tr in (128, 512) for r in ROUTINGS if r[0] in ("zipf", "softmax")])
+
+
+@pytest.mark.parametrize("kind,T,E,k,tile_rows", SPLIT_TILE_CASES)
 def test_sort_routes_split_tiles_matches_two_ops(dev, kind, T, E, k, tile_rows):
     """The prefill path's two-launch preparation (histogram; scatter with per-workgroup cursors + tile tables +
     output clear) writes exactly what sort_routes followed by build_tiles_split writes (kernel/exl3_grouped_runtime.py
     :59-68, kernel/exl3_grouped_prefill.cu:63-96), bit for bit, with int64 and int32 ids; the clear covers exactly the
     given range."""
-    if tile_rows != 256 and kind not in ("zipf", "softmax"):
-        pytest.skip("other tile sizes: two routings suffice")
     ids, w = synth.make_routing(kind, T, E, k, seed=T + 9)
     wt = torch.from_numpy(w).to(dev)
     for ids_dt in (torch.int64, torch.int32):
