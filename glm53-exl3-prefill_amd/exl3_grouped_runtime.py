@@ -104,18 +104,26 @@ def thin_tiles_enabled() -> bool:
 THIN_ROWS = 64
 
 # The prefill intermediates (sorted routes, tile tables, h13, gu, act: ~0.85 GB at 8192 tokens; with the combine output
-# also the per-route fp32 rows, 1.07 GB more at H = 4096) live in one buffer per
-# device, reused by every call and grown (never shrunk) when a call needs more: steady-state calls allocate nothing but
-# their output, and the kernels keep working on memory they have touched before. Calls on one device must be ordered on
-# one stream (the model runner's); EXL3_GROUPED_WORKSPACE=0 allocates per call instead. A buffer that a larger call
-# outgrows is kept, not freed: a HIP graph captured over an earlier call still addresses it
-# (release_outgrown_prefill_workspaces frees them once no such graph is in use; reserve_prefill_workspace sizes the
-# buffer for the largest chunk up front so it never grows).
+# also the per-route fp32 rows, 1.07 GB more at H = 4096) live in one buffer per device, reused by every call: steady-state
+# calls allocate nothing but their output, and the kernels keep working on memory they have touched before. Calls on one
+# device must be ordered on one stream (the model runner's); EXL3_GROUPED_WORKSPACE=0 allocates per call instead.
+# When a call needs more, the buffer grows to at least WS_GROWTH times its old size (so rising chunk sizes re-allocate a
+# few times, not on every call) and the outgrown buffer is released: one live workspace per device. Graph capture is
+# the exception: a HIP graph captured over an earlier call still addresses the old buffer, so an outgrown buffer is kept
+# while the current stream is capturing or once the caller has asked for it (keep_outgrown_prefill_workspaces(True),
+# or reserve_prefill_workspace(..., keep_outgrown=True)); release_outgrown_prefill_workspaces frees those once no such
+# graph is replayed. The reference's prefill path is eager-only (kernel/exl3_grouped_runtime.py:4-5), so freeing is the
+# default.
+WS_GROWTH = 1.25
+WS_ALIGN = 2 << 20
 _prefill_ws: dict = {}
 _prefill_ws_outgrown: dict = {}
+_keep_outgrown = False
 
 
 def _device_index(dev: torch.device) -> int:
+    if dev.type != "cuda":
+        return -1                           # host buffers (CPU tests of the workspace policy)
     return dev.index if dev.index is not None else torch.cuda.current_device()
 
 
@@ -151,28 +159,55 @@ def _prefill_buffers(dev, plan):
     return plan(_Carve(_prefill_workspace(dev, sizing.off)))
 
 
+def _capturing(dev) -> bool:
+    return dev.type == "cuda" and torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+
+
 def _prefill_workspace(dev, nbytes: int) -> torch.Tensor:
     key = _device_index(dev)
     ws = _prefill_ws.get(key)
     if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 256)
         if ws is not None:
-            _prefill_ws_outgrown.setdefault(key, []).append(ws)
-        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+            size = max(size, int(ws.numel() * WS_GROWTH))
+            if _keep_outgrown or _capturing(dev):
+                _prefill_ws_outgrown.setdefault(key, []).append(ws)
+        size = (size + WS_ALIGN - 1) // WS_ALIGN * WS_ALIGN
+        _prefill_ws[key] = None
+        ws = None                           # the outgrown buffer returns to the allocator before the new one is taken
+        ws = torch.empty(size, dtype=torch.uint8, device=dev)
         _prefill_ws[key] = ws
     return ws
 
 
+def keep_outgrown_prefill_workspaces(keep: bool = True) -> None:
+    """Keep (True) or release (False, the default) a prefill workspace that a larger call outgrows. Keep them while HIP
+    graphs captured over earlier calls may still be replayed; outgrown buffers are always kept during a capture."""
+    global _keep_outgrown
+    _keep_outgrown = bool(keep)
+
+
+def live_prefill_workspaces(device=None) -> int:
+    """Prefill workspaces this module holds (current + outgrown kept), on every device or on one."""
+    keys = [_device_index(torch.device(device))] if device is not None else set(_prefill_ws) | set(_prefill_ws_outgrown)
+    return sum((_prefill_ws.get(k) is not None) + len(_prefill_ws_outgrown.get(k, [])) for k in keys)
+
+
 def release_outgrown_prefill_workspaces(device=None) -> None:
-    """Free the prefill workspaces that larger calls replaced (on every device, or one), once no HIP graph captured
-    over an earlier, smaller call is replayed any more."""
+    """Free the prefill workspaces that larger calls replaced and that were kept (on every device, or one), once no HIP
+    graph captured over an earlier, smaller call is replayed any more."""
     for key in ([_device_index(torch.device(device))] if device is not None else list(_prefill_ws_outgrown)):
         _prefill_ws_outgrown.pop(key, None)
 
 
 def reserve_prefill_workspace(device, tokens: int, topk: int, n_experts: int, hidden: int, inter: int,
-                              scatter: str | None = None, rows_per_tile: int | None = None) -> torch.Tensor:
+                              scatter: str | None = None, rows_per_tile: int | None = None,
+                              keep_outgrown: bool | None = None) -> torch.Tensor:
     """Size the device's prefill workspace for a chunk of `tokens` (the largest the scheduler sends) before the first
-    call, e.g. ahead of memory profiling or graph capture, so that no later call grows it. Returns the buffer."""
+    call, e.g. ahead of memory profiling or graph capture, so that no later call grows it. keep_outgrown (if given)
+    sets keep_outgrown_prefill_workspaces. Returns the buffer."""
+    if keep_outgrown is not None:
+        keep_outgrown_prefill_workspaces(keep_outgrown)
     scatter = resolve_scatter(scatter, tokens * topk)
     tr = rows_per_tile or tile_rows()
     thin = thin_tiles_enabled()

@@ -774,26 +774,32 @@ def test_thin_config_all_bits(dev, bits, svh_scale):
 
 def test_prefill_workspace_reuse(dev, monkeypatch):
     """The prefill intermediates come from one per-device buffer reused across calls of different sizes (grown when a
-    call needs more): results match the per-call-allocation path up to the atomic summation order."""
+    call needs more, the outgrown buffer released unless kept for captured graphs): results match the per-call-allocation
+    path up to the atomic summation order."""
     L, x, ids, w, cfg = synth.make_config("layer1k", seed=3, svh_scale=1 / 64)
     TL = synth.to_device(L, dev)
     xt, it, wt = t16(x, dev), t16(ids, dev), t16(w, dev)
     rt._prefill_ws.clear()
     rt._prefill_ws_outgrown.clear()
+    rt.keep_outgrown_prefill_workspaces(False)
     key = torch.cuda.current_device()
     sizes = (300, 1024, 300, 1024, 700)
     got = [rt.grouped_prefill(xt[:sizes[0]], it[:sizes[0]], wt[:sizes[0]], TL, LIMIT)]
-    first = rt._prefill_ws[key].data_ptr()
     for n in sizes[1:]:
         got.append(rt.grouped_prefill(xt[:n], it[:n], wt[:n], TL, LIMIT))
     ws = rt._prefill_ws[key]
-    assert [b.data_ptr() for b in rt._prefill_ws_outgrown[key]] == [first]     # outgrown, kept for captured graphs
+    assert not rt._prefill_ws_outgrown.get(key) and rt.live_prefill_workspaces(dev) == 1   # outgrown: released
     got.append(rt.grouped_prefill(xt[:500], it[:500], wt[:500], TL, LIMIT))
     assert rt._prefill_ws[key].data_ptr() == ws.data_ptr()                     # no growth for smaller calls
-    rt.release_outgrown_prefill_workspaces()
-    assert not rt._prefill_ws_outgrown
-    big = rt.reserve_prefill_workspace(dev, 2 * x.shape[0], cfg["topk"], cfg["E"], cfg["H"], cfg["I"])
+    # kept for captured graphs on request
+    big = rt.reserve_prefill_workspace(dev, 2 * x.shape[0], cfg["topk"], cfg["E"], cfg["H"], cfg["I"],
+                                       keep_outgrown=True)
     assert big.numel() > ws.numel() and rt._prefill_ws[key].data_ptr() == big.data_ptr()
+    assert [b.data_ptr() for b in rt._prefill_ws_outgrown[key]] == [ws.data_ptr()]
+    rt.release_outgrown_prefill_workspaces()
+    rt.keep_outgrown_prefill_workspaces(False)
+    assert not rt._prefill_ws_outgrown and rt.live_prefill_workspaces(dev) == 1
+    del ws
     rt.grouped_prefill(xt, it, wt, TL, LIMIT)
     assert rt._prefill_ws[key].data_ptr() == big.data_ptr()                    # reserved: the full chunk fits
     sizes = sizes + (500,)

@@ -117,6 +117,41 @@ def test_prefill_workspace_holds_the_combine_rows(monkeypatch):
     assert size(T - 1, "auto") == size(T - 1, "atomic")
 
 
+def test_prefill_workspace_is_bounded():
+    """Twenty calls of rising size leave one live workspace per device: each growth takes at least WS_GROWTH times the
+    old size and releases the outgrown buffer (kernel/exl3_grouped_runtime.py:69-80 allocates per call; the buffer here
+    is reused). Kept outgrown buffers (graph-capture safety, on request) are freed by
+    release_outgrown_prefill_workspaces."""
+    dev = torch.device("cpu")
+    rt._prefill_ws.clear()
+    rt._prefill_ws_outgrown.clear()
+    rt.keep_outgrown_prefill_workspaces(False)
+    try:
+        sizes = [int(1e6 * (1 + 0.1 * i)) for i in range(20)]
+        grows, last = 0, None
+        for n in sizes:
+            ws = rt._prefill_workspace(dev, n)
+            assert ws.numel() >= n and rt.live_prefill_workspaces(dev) == 1
+            if last is not None and ws.numel() != last:
+                assert ws.numel() >= rt.WS_GROWTH * last
+                grows += 1
+            last = ws.numel()
+            del ws
+        assert grows <= 6                     # 1e6 -> 2.9e6 in steps of >= 1.25x from a 2 MiB-aligned start
+        assert not rt._prefill_ws_outgrown
+        small = rt._prefill_workspace(dev, 1000)
+        assert small.numel() == last          # never shrinks
+        rt.keep_outgrown_prefill_workspaces(True)
+        big = rt._prefill_workspace(dev, 4 * last)
+        assert rt.live_prefill_workspaces(dev) == 2 and rt._prefill_ws_outgrown[-1][0] is small
+        rt.release_outgrown_prefill_workspaces()
+        assert rt.live_prefill_workspaces(dev) == 1 and rt._prefill_ws[-1] is big
+    finally:
+        rt.keep_outgrown_prefill_workspaces(False)
+        rt._prefill_ws.clear()
+        rt._prefill_ws_outgrown.clear()
+
+
 def test_generators_are_deterministic():
     a = synth.make_config("tiny", seed=3)
     b = synth.make_config("tiny", seed=3)
