@@ -448,8 +448,10 @@ struct Mma
 };
 
 // ------------------------------------------------------------------------------------------- epilogue
-// pa = {fp16(a0 * s0), fp16(a1 * s1)}, pb = {fp16(b0 * t0), fp16(b1 * t1)}: each product rounded once, straight to
-// fp16, packed in place. A high half is written two instructions after the low half it keeps (gfx950 forwards a
+// pa = {fp16(a0 * s0), fp16(a1 * s1)}, pb = {fp16(b0 * t0), fp16(b1 * t1)}: each exact product rounded once, straight
+// to fp16, packed in place. (The reference rounds the product in fp32 first and then to fp16,
+// kernel/exl3_grouped_prefill.cu:54-56,273: the two differ by one fp16 step where the fp32 rounding crosses an fp16
+// rounding boundary, about one element in 2^13.) A high half is written two instructions after the low half it keeps (gfx950 forwards a
 // partial register write stale to the next instruction), and an s_nop guards the last one for the code after.
 __device__ __forceinline__ void f16_products_4(float a0, float a1, float b0, float b1, float s0, float s1, float t0,
                                                float t1, uint32_t& pa, uint32_t& pb)
@@ -531,7 +533,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
                 uint16_t* o = reinterpret_cast<uint16_t*>(p.out) +
                               (p.out_t16 ? ((((orow >> 4) * (p.out_ld >> 3) + (c >> 3)) * 16 + (orow & 15)) * 8 + (c & 7))
                                          : orow * p.out_ld + c);
-                uint2 pk;                                       // fp16(x * svh / sqrt(128)), one rounding each
+                uint2 pk;                                       // fp16(x * svh / sqrt(128)), single-rounded
                 f16_products_4(x[4 * nb], x[4 * nb + 1], x[4 * nb + 2], x[4 * nb + 3], sv[4 * nb], sv[4 * nb + 1],
                                sv[4 * nb + 2], sv[4 * nb + 3], pk.x, pk.y);
                 *reinterpret_cast<uint2*>(o) = pk;
