@@ -194,8 +194,9 @@ def had128(x: np.ndarray, scale: float = HAD_SCALE) -> np.ndarray:
     x = np.asarray(x, dtype=np.float64)
     sh = x.shape
     assert sh[-1] % 128 == 0
-    y = x.reshape(-1, sh[-1] // 128, 128) @ _H128
-    return (y * scale).reshape(sh)
+    y = x.reshape(-1, 128) @ _H128          # one [n, 128] x [128, 128] product, not a batch of small ones
+    y *= scale
+    return y.reshape(sh)
 
 
 # ---------------------------------------------------------------------------------------------- layer
@@ -317,11 +318,15 @@ def grouped_prefill(x: np.ndarray, ids: np.ndarray, weights: np.ndarray, layer: 
 
 
 def expert_loop(x: np.ndarray, ids: np.ndarray, weights: np.ndarray, layer: Layer, limit: float,
-                cache: WeightCache | None = None, experts=None, dtype=np.float32) -> np.ndarray:
+                cache: WeightCache | None = None, experts=None, dtype=np.float32, round_h13: bool = False,
+                round_act: bool = False) -> np.ndarray:
     """The reference's per-expert loop (harness/proto_fp8.py:123-134) on the real-domain weights
     W = diag(suh) H W' H diag(svh) (:66-76), evaluated in factored form: x @ W = H((x*suh) H @ W') * svh.
     Rounding points: h = fp16 input rows, gate|up fp16, act fp16, route weight fp16; fp32 output.
-    `experts` restricts the loop to a subset (the CPU-baseline sample)."""
+    `experts` restricts the loop to a subset (the CPU-baseline sample).
+    round_h13 / round_act add the grouped path's two extra fp16 rounding points, the rotated input rows (row_had,
+    kernel/exl3_grouped_prefill.cu:101-115) and the rotated activation (act_had, :118-141); with both the loop computes
+    what the staged path does, so the two flags split the staged path's distance from the loop between them."""
     cache = cache or WeightCache(layer)
     T = x.shape[0]
     H = layer.hidden
@@ -335,15 +340,26 @@ def expert_loop(x: np.ndarray, ids: np.ndarray, weights: np.ndarray, layer: Laye
             continue
         h = x16[tok]
         hs = had128(h * layer.w13_suh[e, 0].astype(np.float32)).astype(dtype)
+        if round_h13:
+            hs = round_f16(hs).astype(dtype)
         gate = had128(hs @ cache.get(e, "gate").astype(dtype)) * layer.w13_svh[e, 0].astype(np.float32)
-        hs_u = had128(h * layer.w13_suh[e, 1].astype(np.float32)).astype(dtype)
+        same_suh = np.array_equal(layer.w13_suh[e, 0], layer.w13_suh[e, 1])
+        hs_u = hs if same_suh else had128(h * layer.w13_suh[e, 1].astype(np.float32)).astype(dtype)
+        if round_h13 and not same_suh:
+            hs_u = round_f16(hs_u).astype(dtype)
         up = had128(hs_u @ cache.get(e, "up").astype(dtype)) * layer.w13_svh[e, 1].astype(np.float32)
         gate = round_f16(gate)
         up = round_f16(up)
         act = round_f16(swiglu_clamped(gate, up, limit))
         a = had128(act * layer.w2_suh[e].astype(np.float32)).astype(dtype)
+        if round_act:
+            a = round_f16(a).astype(dtype)
         down = had128(a @ cache.get(e, "down").astype(dtype)) * layer.w2_svh[e].astype(np.float32)
-        np.add.at(out, tok, (down * w16[tok, kpos][:, None]).astype(np.float32))
+        v = (down * w16[tok, kpos][:, None]).astype(np.float32)
+        if np.unique(tok).size == tok.size:    # top-k ids are distinct per token: one add per output element
+            out[tok] += v
+        else:
+            np.add.at(out, tok, v)
     return out
 
 

@@ -699,7 +699,8 @@ class Fake:
     pass
 
 
-def run_layer(L, x, ids, w, dev, scatter="atomic"):
+def run_layer(L, x, ids, w, dev, scatter=None):
+    """One grouped_prefill call; scatter None is the shipped default (EXL3_GROUPED_SCATTER, else "auto")."""
     TL = synth.to_device(L, dev)
     out = rt.grouped_prefill(t16(x, dev), t16(ids, dev), t16(w, dev), TL, LIMIT, scatter=scatter)
     torch.cuda.synchronize()
@@ -744,14 +745,32 @@ def test_headline_sampled_tokens_and_properties(dev, scatter):
         assert torch.equal(outp.view(torch.int32), out[torch.from_numpy(perm).to(dev)].view(torch.int32))
 
 
+@pytest.mark.parametrize("scatter", [None, "atomic"])
 @pytest.mark.parametrize("T", [1024, 2048, 4096])
-def test_headline_routing_sweep_sampled_tokens(dev, T):
+def test_headline_routing_sweep_sampled_tokens(dev, T, scatter):
     """The headline layer and Zipf routing at the sweep's smaller chunks, sampled tokens
-    against the expert loop."""
+    against the expert loop, through the shipped output method (None: "auto", the combine from 16384 routes) and the
+    atomic scatter."""
     L, x, ids, w, cfg = synth.make_config("headline", seed=0, T=T)
-    out = run_layer(L, x, ids, w, dev).cpu().numpy()
+    out = run_layer(L, x, ids, w, dev, scatter).cpu().numpy()
     tokens = np.random.default_rng(T).choice(cfg["T"], 64, replace=False)
     assert O.rel_l2(out[tokens], sampled_loop(L, x, ids, w, tokens)) < 1e-3
+
+
+@pytest.mark.parametrize("name,T", [("headline", 2048), ("headline", 8192), ("repro", 256), ("repro", 2048)])
+def test_full_output_vs_expert_loop(dev, name, T):
+    """Every token of the output through the shipped output method (scatter None: "auto") against the expert loop,
+    as the reference checks its grouped path (kernel/test_grouped.py:148-155: the whole output at 256 and 2048 tokens,
+    skewed routing, which the repro config restates): the headline layer and Zipf routing at 2048 tokens and at the
+    full 8192-token chunk, and the reference's own shape (I = 1024, skewed routing)."""
+    L, x, ids, w, cfg = synth.make_config(name, seed=0, T=T)
+    out = run_layer(L, x, ids, w, dev).cpu().numpy()
+    ref = O.expert_loop(x, ids, w, to_np_layer(L), LIMIT)
+    err = O.rel_l2(out, ref)
+    print(f"{name} T={T} scatter={rt.resolve_scatter(None, T * cfg['topk'])}: rel L2 vs expert loop {err:.3e} "
+          f"over {T} tokens", flush=True)
+    assert np.isfinite(out).all()
+    assert err < 1e-3
 
 
 def test_repro_config_sampled_tokens(dev):
@@ -763,11 +782,12 @@ def test_repro_config_sampled_tokens(dev):
     assert O.rel_l2(out[tokens], sampled_loop(L, x, ids, w, tokens)) < 1e-3
 
 
+@pytest.mark.parametrize("scatter", [None, "atomic"])       # None: the shipped "auto" (combine at 57344 routes)
 @pytest.mark.parametrize("svh_scale", [1.0, 1 / 64])          # 1/64: pre-activations inside the clamp (SiLU region)
 @pytest.mark.parametrize("bits", [4, 3, 2])
-def test_thin_config_all_bits(dev, bits, svh_scale):
+def test_thin_config_all_bits(dev, bits, svh_scale, scatter):
     L, x, ids, w, cfg = synth.make_config("thin", seed=0, bits=bits, svh_scale=svh_scale)
-    out = run_layer(L, x, ids, w, dev).cpu().numpy()
+    out = run_layer(L, x, ids, w, dev, scatter).cpu().numpy()
     tokens = np.random.default_rng(bits).choice(cfg["T"], 16, replace=False)
     assert O.rel_l2(out[tokens], sampled_loop(L, x, ids, w, tokens)) < 1e-3
 

@@ -256,6 +256,26 @@ def test_staged_oracle_tracks_expert_loop(svh_scale):
     assert O.rel_l2(staged, loop) < 1e-3
 
 
+@pytest.mark.parametrize("svh_scale", [1.0, 1.0 / 64])
+def test_staged_distance_from_loop_is_its_two_rounding_points(svh_scale):
+    """The staged path (the grouped kernels' stages) differs from the real-domain loop only by its two extra fp16
+    rounding points, the rotated input rows and the rotated activation: the loop with both added equals the staged
+    oracle (both with fp64 GEMMs), and the rotated input's rounding carries most of the distance."""
+    from exl3_grouped import synth
+    L, x, ids, w, cfg = synth.make_config("tiny", seed=0, svh_scale=svh_scale)
+    layer = O.Layer(L.w13_trellis, L.w13_suh, L.w13_svh, L.w2_trellis, L.w2_suh, L.w2_svh)
+    cache = O.WeightCache(layer)
+    loop = O.expert_loop(x, ids, w, layer, 10.0, cache=cache)
+    both = O.expert_loop(x, ids, w, layer, 10.0, cache=cache, dtype=np.float64, round_h13=True, round_act=True)
+    h13 = O.expert_loop(x, ids, w, layer, 10.0, cache=cache, round_h13=True)
+    act = O.expert_loop(x, ids, w, layer, 10.0, cache=cache, round_act=True)
+    staged = O.grouped_prefill(x, ids, w, layer, 10.0)
+    assert O.rel_l2(both, staged) < 1e-6
+    d = O.rel_l2(staged, loop)
+    assert 2e-4 < d < 1e-3
+    assert O.rel_l2(h13, loop) > 0.8 * d > O.rel_l2(act, loop)
+
+
 def test_gemm_stage_commutes_with_real_domain_weight():
     """mode-0 stage on H(x*suh) equals x @ W_real before rounding: pins the Hadamard side and the svh axis."""
     layer, x, ids, w = _micro(3)
