@@ -36,7 +36,7 @@ constexpr uint32_t MCG_MASK = 0x8FFF8FFFu;
         "v_mul_lo_u16_sdwa %1, %5, %6 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:" S1 " src1_sel:DWORD\n\t"       \
         "v_mad_u32_u16 %2, %4, %7, %0" OP0 "\n\t"                                                                    \
         "v_mad_u32_u16 %3, %5, %7, %1" OP1                                                                          \
-        : "=&v"(t0), "=&v"(t1), "=&v"(x0), "=&v"(x1) : "v"(ra), "v"(rb), "v"(chi), "v"(clo))
+        : "=&v"(t0), "=&v"(t1), "=&v"(x0), "=&v"(x1) : "v"(ra), "v"(rb), "s"(chi), "s"(clo))
 template <int SEL0, int SEL1>
 __device__ __forceinline__ void mcg_mul2(uint32_t ra, uint32_t rb, uint32_t& x0, uint32_t& x1)
 {

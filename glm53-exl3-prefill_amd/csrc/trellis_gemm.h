@@ -112,6 +112,18 @@ struct GemmParams
     int64_t zero4;
 };
 
+// A wave's epilogue inputs, staged in LDS while its main loop's pipeline fills (their global loads then overlap the
+// first trellis and activation loads instead of each opening a step of the epilogue): the svh of the tile's 128 output
+// columns and, for the route modes, every row slot's route weight and destination row (slot 16 mb + tok of the wave's
+// group mb; rows past the tile's last clamped to it, as the epilogue clamps them).
+struct EpiLds
+{
+    uint32_t svh[64];              // 128 fp16
+    float rw[64];
+    int64_t dest[64];
+};
+constexpr bool route_mode(int mode) { return mode == MODE_SCATTER_F32 || mode == MODE_STORE_ROUTE_F32; }
+
 // In-place Walsh-Hadamard transform of 32 values (Sylvester order over the index bits).
 __device__ __forceinline__ void fwht32(float (&x)[32])
 {
@@ -471,9 +483,10 @@ __device__ __forceinline__ void f16_products_4(float a0, float a1, float b0, flo
 // one output row.
 // GSTRIDE > 0: the wave's groups are interleaved over the tile (group mb of wave mw is the tile's 16-row group
 // mw + GSTRIDE mb); 0: they are contiguous (rows 16 MBN mw + 16 mb ..).
+// epi: the wave's inputs staged in LDS (EpiLds), or null to read them from global memory here.
 template <int MODE, int MBN, int GSTRIDE = 0>
 __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int mw, int lane, floatx4 (&acc)[MBN][8],
-                                         float* stage)
+                                         float* stage, const EpiLds* epi = nullptr)
 {
     const int tok = lane & 15, kq = lane >> 4;
     auto group_row0 = [&](int mb) { return GSTRIDE ? 16 * (mw + GSTRIDE * mb) : 16 * MBN * mw + 16 * mb; };
@@ -482,7 +495,8 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
     #pragma unroll
     for (int nb = 0; nb < 8; ++nb)
     {
-        const uint2 v = *reinterpret_cast<const uint2*>(t.svh + 16 * nb + 4 * kq);
+        const uint2 v = epi ? *reinterpret_cast<const uint2*>(epi->svh + 8 * nb + 2 * kq)
+                            : *reinterpret_cast<const uint2*>(t.svh + 16 * nb + 4 * kq);
         sv[4 * nb + 0] = h2f(v.x & 0xFFFF) * HAD_SCALE;
         sv[4 * nb + 1] = h2f(v.x >> 16) * HAD_SCALE;
         sv[4 * nb + 2] = h2f(v.y & 0xFFFF) * HAD_SCALE;
@@ -509,10 +523,18 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
         const int64_t srow = (int64_t) t.row0 + min(r_local, t.rows_valid - 1);
         float rw = 1.0f;
         int64_t orow = srow;
-        if constexpr (MODE == MODE_SCATTER_F32 || MODE == MODE_STORE_ROUTE_F32)
+        if constexpr (route_mode(MODE))
         {
-            rw = h2f(p.route_weight[srow]);
-            orow = (MODE == MODE_SCATTER_F32) ? p.token[srow] : (int64_t) p.route_index[srow];
+            if (epi)
+            {
+                rw = epi->rw[16 * mb + tok];
+                orow = epi->dest[16 * mb + tok];
+            }
+            else
+            {
+                rw = h2f(p.route_weight[srow]);
+                orow = (MODE == MODE_SCATTER_F32) ? p.token[srow] : (int64_t) p.route_index[srow];
+            }
         }
         #pragma unroll
         for (int nb = 0; nb < 8; ++nb)
@@ -689,10 +711,12 @@ __device__ __forceinline__ void thin_tile(const GemmParams& p, const Tile& t, in
     if (wave == 0) epilogue<MODE, 1, 0>(p, t, 0, lane, full, stage);
 }
 
-// 128-, 256- and 512-row tiles: the waves share each decoded stage (a barrier per stage), each multiplying its own rows.
+// The main loop of a 128-, 256- or 512-row tile: the waves share each decoded stage (a barrier per stage), each
+// multiplying its own rows into acc. epi (may be null): where the wave stages its epilogue inputs. Returns the number
+// of 16-row groups the wave multiplied (uniform over the wave).
 template <int BITS, int MODE, int MBN, int WAVES>
-__device__ __forceinline__ void shared_tile(const GemmParams& p, const Tile& t, int group, int wave, int lane,
-                                            unsigned char* lds_raw)
+__device__ __forceinline__ int tile_mainloop(const GemmParams& p, const Tile& t, int wave, int lane,
+                                             unsigned char* lds_raw, EpiLds* epi, floatx4 (&acc)[MBN][8])
 {
     uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
     const int num_kb = t.num_kb;
@@ -707,7 +731,6 @@ __device__ __forceinline__ void shared_tile(const GemmParams& p, const Tile& t, 
     const int n_w = GSTRIDE ? (n_groups > wave ? (n_groups - wave + GSTRIDE - 1) / GSTRIDE : 0)
                             : min(MBN, max(0, n_groups - MBN * wave));          // this wave's groups (uniform)
 
-    floatx4 acc[MBN][8];
     #pragma unroll
     for (int mb = 0; mb < MBN; ++mb)
         #pragma unroll
@@ -716,17 +739,45 @@ __device__ __forceinline__ void shared_tile(const GemmParams& p, const Tile& t, 
     // Main loop, specialised on the number of 16-row groups a wave multiplies (MBA: 0 = decode only, 1 for a wave with
     // <= 16 valid rows, else MBN). Every variant runs the same barriers. Loads past the last stage are clamped to it, so
     // every path keeps the same loads in flight.
+    // The epilogue's inputs: loaded before the pipeline's first loads, written to LDS after them (so the write waits
+    // only for these), read back by the epilogue.
+    uint32_t ep_svh;
+    float ep_rw = 0.f;
+    int64_t ep_dest = 0;
+    auto epi_load = [&]() {
+        ep_svh = reinterpret_cast<const uint32_t*>(t.svh)[lane];
+        if constexpr (route_mode(MODE))
+            if (lane < 16 * MBN)
+            {
+                const int mb = lane >> 4;
+                const int r_local = (GSTRIDE ? 16 * (wave + GSTRIDE * mb) : 16 * MBN * wave + 16 * mb) + (lane & 15);
+                const int64_t srow = (int64_t) t.row0 + min(r_local, t.rows_valid - 1);
+                ep_rw = h2f(p.route_weight[srow]);
+                ep_dest = (MODE == MODE_SCATTER_F32) ? p.token[srow] : (int64_t) p.route_index[srow];
+            }
+    };
+    auto epi_store = [&]() {
+        epi->svh[lane] = ep_svh;
+        if constexpr (route_mode(MODE))
+            if (lane < 16 * MBN)
+            {
+                epi->rw[lane] = ep_rw;
+                epi->dest[lane] = ep_dest;
+            }
+    };
     auto mainloop = [&](auto mba_tag) {
         constexpr int MBA = decltype(mba_tag)::value;
         uint32_t raw[RAW_DEPTH][NR];
         half8_t act[ACT_DEPTH][MBN];
         {
             uint32_t r0[NR];
+            if (MBA > 0 && epi) epi_load();
             dec.load(0, r0);
             #pragma unroll
             for (int s = 1; s <= RAW_DEPTH; ++s) dec.load(s, raw[s % RAW_DEPTH]);
             #pragma unroll
             for (int s = 0; s < ACT_DEPTH; ++s) mm.load_act<MBA>(s, act[s]);
+            if (MBA > 0 && epi) epi_store();
             typename Dec::Out o;
             dec.decode(r0, o);
             dec.store(o, lds_b);
@@ -779,6 +830,17 @@ __device__ __forceinline__ void shared_tile(const GemmParams& p, const Tile& t, 
     else if (MBN > 1 && n_w > 1) mainloop(std::integral_constant<int, MBN>{});
     else if (n_w > 0) mainloop(std::integral_constant<int, 1>{});
     else mainloop(std::integral_constant<int, 0>{});
+    return n_w;
+}
+
+// 128-, 256- and 512-row tiles: the shared main loop, then every wave's epilogue over its rows.
+template <int BITS, int MODE, int MBN, int WAVES>
+__device__ __forceinline__ void shared_tile(const GemmParams& p, const Tile& t, int group, int wave, int lane,
+                                            unsigned char* lds_raw, EpiLds* epi)
+{
+    constexpr int GSTRIDE = WAVES == 8 ? 8 : 0;
+    floatx4 acc[MBN][8];
+    const int n_w = tile_mainloop<BITS, MODE, MBN, WAVES>(p, t, wave, lane, lds_raw, epi, acc);
 
     if constexpr (atomic_mode(MODE)) __syncthreads();            // decoded tiles are dead; LDS becomes staging
     float* const stage = reinterpret_cast<float*>(lds_raw) + wave * (16 * SC_ROW);
@@ -786,13 +848,13 @@ __device__ __forceinline__ void shared_tile(const GemmParams& p, const Tile& t, 
     {
         if (p.act_arrive)                                        // every wave goes on to the arrival barrier
         {
-            if (n_w > 0) epilogue<MODE, MBN, GSTRIDE>(p, t, wave, lane, acc, stage);
+            if (n_w > 0) epilogue<MODE, MBN, GSTRIDE>(p, t, wave, lane, acc, stage, epi);
             act_after_last_slice(p, t, group, wave, lane);
             return;
         }
     }
     if (n_w == 0) return;
-    epilogue<MODE, MBN, GSTRIDE>(p, t, wave, lane, acc, stage);
+    epilogue<MODE, MBN, GSTRIDE>(p, t, wave, lane, acc, stage, epi);
 }
 
 // ------------------------------------------------------------------------------------------- kernel
@@ -815,6 +877,7 @@ void trellis_gemm_kernel(const GemmParams p)
     constexpr int SCB = lds_scatter_bytes<WAVES>();
     constexpr int LDS_BYTES = (atomic_mode(MODE) && SCB > LDS_MAIN_BYTES) ? SCB : LDS_MAIN_BYTES;
     __shared__ __align__(16) unsigned char lds_raw[LDS_BYTES];
+    __shared__ EpiLds lds_epi[WAVES];
 
     if (p.zero4 > 0)                    // every workgroup, tile or not, clears its grid-strided share up front; the
     {                                   // stores drain while the tile computes
@@ -832,7 +895,69 @@ void trellis_gemm_kernel(const GemmParams p)
     if (MBN == 1 && t.rows_valid <= 16)                           // uniform over the workgroup
         thin_tile<BITS, MODE>(p, t, group, wave, lane, lds_raw);
     else
-        shared_tile<BITS, MODE, MBN, WAVES>(p, t, group, wave, lane, lds_raw);
+        shared_tile<BITS, MODE, MBN, WAVES>(p, t, group, wave, lane, lds_raw, lds_epi + wave);
+}
+
+// A dense GEMM whose 256-row tiles would leave CUs idle (long K, few rows): the two K halves of one tile run in one
+// workgroup of 8 waves, waves 0-3 over the first half and 4-7 over the second, each half the 4-wave main loop over its
+// own double-buffered stage tiles (the barriers are shared: both halves run the same number of stages). The second
+// half's accumulators are then added to the first's through LDS, one 16-row group at a time, and the first half's
+// waves run the epilogue: twice the waves per tile with plain stores -- no zeroed output, no atomics, and the same
+// summation order on every run (the sum over K: first half + second half, each in stage order).
+constexpr int KPAIR_LDS_BYTES = 2 * LDS_MAIN_BYTES;
+static_assert(KPAIR_LDS_BYTES >= 4 * 8 * 64 * 16, "one row group of four waves' accumulators");
+
+template <int BITS, int MODE, bool DENSE>
+__global__ __launch_bounds__(512, 2)
+void trellis_gemm_kpair_kernel(const GemmParams p)
+{
+    static_assert(MODE == MODE_STORE_F32 || MODE == MODE_STORE_F16, "plain-store modes");
+    __shared__ __align__(16) unsigned char lds_raw[KPAIR_LDS_BYTES];
+    __shared__ EpiLds lds_epi[4];
+    int group, slot;
+    xcd_group_slot((int) blockIdx.x, p.n_slots, group, slot);
+    Tile t;
+    if (!resolve_tile<DENSE>(p, group, slot, t)) return;          // uniform over the workgroup
+    const int lane = threadIdx.x & 63;
+    const int wave8 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int half = wave8 >> 2, wave = wave8 & 3;
+    Tile th = t;
+    th.num_kb = t.num_kb / 2;                                      // even: the host requires K % 128 == 0
+    th.kb0 = t.kb0 + half * th.num_kb;
+    floatx4 acc[4][8];
+    const int n_w = tile_mainloop<BITS, MODE, 4, 4>(p, th, wave, lane, lds_raw + half * LDS_MAIN_BYTES,
+                                                    half ? nullptr : lds_epi + wave, acc);
+    floatx4* xs = reinterpret_cast<floatx4*>(lds_raw) + wave * 8 * 64 + lane;
+    #pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+    {
+        __syncthreads();                            // mb = 0: both main loops are done with the stage tiles
+        if (half == 1 && mb < n_w)
+            #pragma unroll
+            for (int nb = 0; nb < 8; ++nb) xs[nb * 64] = acc[mb][nb];
+        __syncthreads();
+        if (half == 0 && mb < n_w)
+            #pragma unroll
+            for (int nb = 0; nb < 8; ++nb) acc[mb][nb] += xs[nb * 64];
+    }
+    if (half == 0 && n_w > 0) epilogue<MODE, 4, 0>(p, t, wave, lane, acc, nullptr, lds_epi + wave);
+}
+
+// The K-pair schedule for a dense store: 256-row tiles, one 8-wave workgroup per (tile, 128-column block).
+template <int BITS, int MODE, bool DENSE>
+int launch_gemm_kpair(const GemmParams& p, hipStream_t s)
+{
+    if constexpr (MODE == MODE_STORE_F32 || MODE == MODE_STORE_F16)
+    {
+        if (p.tile_rows != 256 || (p.size_k / TILE_K) % 4 != 0 || p.k_split > 1)
+            return fail("internal: K-pair launch needs 256-row tiles and K %% 128 == 0");
+        const int64_t grid = (int64_t) (p.n_groups + 7) / 8 * 8 * p.n_slots;
+        if (grid == 0) return EXL3_OK;
+        if (grid > 0x7FFFFFFF) return fail("grid too large");
+        trellis_gemm_kpair_kernel<BITS, MODE, DENSE><<<(unsigned) grid, 512, 0, s>>>(p);
+        return EXL3_OK;
+    }
+    return fail("internal: K-pair launch for mode %d", MODE);
 }
 
 // 512-row tiles run the 8-wave variant, 128- and 256-row tiles the 4-wave kernel (the only one built for ATOMIC_F32,
@@ -868,5 +993,8 @@ int launch_gemm_b2(int mode, bool dense, const GemmParams& p, hipStream_t s);
 int launch_gemm_b3(int mode, bool dense, const GemmParams& p, hipStream_t s);
 int launch_gemm_b4g(int mode, const GemmParams& p, hipStream_t s);
 int launch_gemm_b4d(int mode, const GemmParams& p, hipStream_t s);
+int launch_gemm_kpair_b2(int mode, const GemmParams& p, hipStream_t s);
+int launch_gemm_kpair_b3(int mode, const GemmParams& p, hipStream_t s);
+int launch_gemm_kpair_b4(int mode, const GemmParams& p, hipStream_t s);
 
 }  // namespace exl3

@@ -190,6 +190,23 @@ int launch_bits(int bits, const GemmParams& p, hipStream_t s)
     }
 }
 
+// The K-pair schedule (trellis_gemm_kpair_kernel): a dense store on 256-row tiles with both K halves of a tile in one
+// 8-wave workgroup.
+template <int MODE>
+int launch_kpair_bits(int bits, GemmParams p, hipStream_t s)
+{
+    p.tile_rows = 256;
+    p.n_groups = (int) ((p.m + 255) / 256);
+    p.k_split = 0;
+    switch (bits)
+    {
+        case 2: return launch_gemm_kpair_b2(MODE, p, s);
+        case 3: return launch_gemm_kpair_b3(MODE, p, s);
+        case 4: return launch_gemm_kpair_b4(MODE, p, s);
+        default: return fail("unsupported bits %d (2, 3 or 4)", bits);
+    }
+}
+
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 }  // namespace
@@ -398,8 +415,9 @@ int dense_tile_rows(int64_t m, int size_k)
 // The fat GEMM's `variant` (the reference's four smem/pipeline variants, kernel/exl3_fat_gemm_v2.cu:285-295) selects
 // the row-tile schedule here: 1 (the reference's production variant, K64 / 2 stages) the shape-tuned policy above,
 // 0 64-row tiles on the thin kernel, 2 256-row tiles on the 4-wave kernel, 3 512-row tiles on the 8-wave kernel. A
-// long-K store that would leave CUs idle runs as two K slices under every variant (dense_split_pays), so all four give
-// bit-identical results: each row's sum over K runs in the same order whatever the tile height.
+// long-K store that would leave CUs idle runs as two K slices, or on the K-pair schedule, under every variant
+// (dense_split_pays, dense_kpair_pays), so all four give bit-identical results: each row's sum over K runs in the same
+// order whatever the tile height.
 int variant_tile_rows(int variant, int64_t m, int size_k)
 {
     switch (variant)
@@ -441,6 +459,15 @@ bool dense_split_pays(int64_t m, int n_slots, int size_k)
     return (m + 255) / 256 * n_slots <= device_cus() && size_k >= 2048;
 }
 
+// Such a GEMM whose 256-row tiles still cover at least 70% of the CUs runs the K-pair schedule instead: both K halves
+// of a tile in one 8-wave workgroup, deterministic plain stores (no zero fill, no atomics). Config 2 (4096 x 4096 x
+// 1536, 192 tiles): 0.086 vs 0.107 ms for the two slices; at 128 tiles (2048 x 4096 x 2048) the slices stay ahead
+// (0.073 vs 0.080 ms): the K-pair workgroups leave half the CUs idle.
+bool dense_kpair_pays(int64_t m, int n_slots, int size_k)
+{
+    return dense_split_pays(m, n_slots, size_k) && (m + 255) / 256 * n_slots * 10 >= 7 * device_cus();
+}
+
 template <int MODE>
 int launch_dense_split2(GemmParams p, int bits, float* out, int64_t out_floats, hipStream_t s, int variant = 1)
 {
@@ -475,9 +502,12 @@ extern "C" int exl3_fat_gemm(const uint16_t* a, int64_t m, int size_k, const uin
     p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
     p.n_tiles_each = (int) (svh_len / TILE_N);
     p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = svh_len;
-    rc = dense_split_pays(m, p.n_slots, size_k)
-             ? launch_dense_split2<MODE_ATOMIC_F32>(p, bits, out, m * svh_len, as_stream(stream), variant)
-             : launch_bits<MODE_STORE_F32, true>(bits, p, as_stream(stream));
+    if (dense_kpair_pays(m, p.n_slots, size_k))
+        rc = launch_kpair_bits<MODE_STORE_F32>(bits, p, as_stream(stream));
+    else
+        rc = dense_split_pays(m, p.n_slots, size_k)
+                 ? launch_dense_split2<MODE_ATOMIC_F32>(p, bits, out, m * svh_len, as_stream(stream), variant)
+                 : launch_bits<MODE_STORE_F32, true>(bits, p, as_stream(stream));
     if (rc) return rc;
     return hip_status("fat_gemm_v2");
 }
@@ -531,7 +561,10 @@ extern "C" int exl3_linear(const uint16_t* x, int64_t m, int k, const uint16_t* 
     p.a = work; p.a_rows = m; p.a_t16 = 1; p.size_k = k; p.packed0 = packed; p.tiles_n = tiles_n;
     p.svh0 = svh; p.tile_rows = dense_tile_rows(m, k); p.n_groups = (int) ((m + p.tile_rows - 1) / p.tile_rows);
     p.n_tiles_each = n / TILE_N; p.n_slots = p.n_tiles_each; p.m = m; p.out = out; p.out_ld = n;
-    if (out_dtype == EXL3_DTYPE_F32 && dense_split_pays(m, p.n_slots, k))
+    if (dense_kpair_pays(m, p.n_slots, k))
+        rc = out_dtype == EXL3_DTYPE_F32 ? launch_kpair_bits<MODE_STORE_F32>(bits, p, s)
+                                         : launch_kpair_bits<MODE_STORE_F16>(bits, p, s);
+    else if (out_dtype == EXL3_DTYPE_F32 && dense_split_pays(m, p.n_slots, k))
         rc = launch_dense_split2<MODE_ATOMIC_F32>(p, bits, reinterpret_cast<float*>(out), m * n, s);
     else
         rc = out_dtype == EXL3_DTYPE_F32 ? launch_bits<MODE_STORE_F32, true>(bits, p, s)

@@ -15,4 +15,15 @@ int launch_gemm_b4d(int mode, const GemmParams& p, hipStream_t s)
     }
     return fail("internal: no kernel for mode %d", mode);
 }
+
+int launch_gemm_kpair_b4(int mode, const GemmParams& p, hipStream_t s)
+{
+    switch (mode)
+    {
+        case MODE_STORE_F16: return launch_gemm_kpair<4, MODE_STORE_F16, true>(p, s);
+        case MODE_STORE_F32: return launch_gemm_kpair<4, MODE_STORE_F32, true>(p, s);
+        default: break;
+    }
+    return fail("internal: no K-pair kernel for mode %d", mode);
+}
 }  // namespace exl3

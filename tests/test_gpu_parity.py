@@ -610,7 +610,8 @@ def test_prefill_out_dtype(dev, scatter):
 
 # ------------------------------------------------------------------------------------------- dense EXL3 linear
 @pytest.mark.parametrize("M,K,N,bits", [(1, 4096, 1536, 4), (300, 768, 4096, 4), (4096, 4096, 1536, 4),
-                                        (200, 4096, 1536, 3), (70, 1024, 512, 2), (0, 512, 256, 4)])
+                                        (200, 4096, 1536, 3), (70, 1024, 512, 2), (0, 512, 256, 4),
+                                        (4096, 2048, 1536, 3), (3072, 4096, 2048, 2)])     # the last two: K-pair
 def test_linear_exl3(dev, M, K, N, bits):
     rng = np.random.default_rng(M + K + bits)
     x = rng.standard_normal((M, K)).astype(np.float16)
@@ -626,6 +627,8 @@ def test_linear_exl3(dev, M, K, N, bits):
     got = y32.cpu().numpy()
     assert O.rel_l2(got, ref) < 1e-4
     assert within_f16_steps(y16.cpu().numpy(), got.astype(np.float16))      # fp16 store = rounded fp32 result
+    again = gp.linear_exl3(t16(x, dev), t16(packed, dev), t16(suh, dev), t16(svh, dev), bits, out_dtype=torch.float32)
+    assert torch.equal(again, y32)                                          # the same summation order every run
 
 
 # ------------------------------------------------------------------------------------------- fat GEMM (config 2)
