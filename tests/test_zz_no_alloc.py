@@ -38,7 +38,7 @@ def test_noalloc_matches_workspace_entry_point(dev):
     L, x_all, _, _, cfg = synth.make_config("layer1k", seed=0, T=1, svh_scale=1 / 64)
     TL = synth.to_device(L, dev)
     layer = O.Layer(L.w13_trellis, L.w13_suh, L.w13_svh, L.w2_trellis, L.w2_suh, L.w2_svh)
-    for T, seed in ((96, 11), (5, 12)):                 # the second call is smaller than the first
+    for T, seed in ((96, 11), (5, 12), (2, 13)):         # each call smaller than the one before
         print(f"noalloc decode: T={T} seed={seed}", flush=True)
         x = synth.make_x(T, cfg["H"], seed)
         ids, w = synth.make_routing("softmax", T, cfg["E"], cfg["topk"], seed=seed)
@@ -48,8 +48,10 @@ def test_noalloc_matches_workspace_entry_point(dev):
         out = torch.full((T, cfg["H"]), float("nan"), dtype=torch.float32, device=dev)
         rc = noalloc(xt, it, wt, TL, out)
         assert rc == 0, _lib.load().exl3_last_error()
+        ws = torch.empty(gp.moe_decode_workspace_bytes(T, cfg["topk"], cfg["E"], cfg["H"], cfg["I"]),
+                         dtype=torch.uint8, device=dev)          # exl3_moe_decode: any workspace contents
         ref = gp.moe_decode(xt, it, wt, TL.w13_trellis, TL.w13_suh, TL.w13_svh, TL.w2_trellis, TL.w2_suh, TL.w2_svh,
-                            LIMIT)
+                            LIMIT, workspace=ws)
         torch.cuda.synchronize()
         got = out.cpu().numpy()
         assert np.isfinite(got).all()
