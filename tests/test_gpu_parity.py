@@ -760,18 +760,20 @@ def test_headline_routing_sweep_sampled_tokens(dev, T, scatter):
     assert O.rel_l2(out[tokens], sampled_loop(L, x, ids, w, tokens)) < 1e-3
 
 
-@pytest.mark.parametrize("name,T", [("headline", 2048), ("headline", 8192), ("repro", 256), ("repro", 2048)])
-def test_full_output_vs_expert_loop(dev, name, T):
+@pytest.mark.parametrize("name,T,bits", [("headline", 2048, None), ("headline", 8192, None), ("repro", 256, None),
+                                         ("repro", 2048, None), ("headline", 2048, 3), ("headline", 2048, 2)])
+def test_full_output_vs_expert_loop(dev, name, T, bits):
     """Every token of the output through the shipped output method (scatter None: "auto") against the expert loop,
     as the reference checks its grouped path (kernel/test_grouped.py:148-155: the whole output at 256 and 2048 tokens,
     skewed routing, which the repro config restates): the headline layer and Zipf routing at 2048 tokens and at the
-    full 8192-token chunk, and the reference's own shape (I = 1024, skewed routing)."""
-    L, x, ids, w, cfg = synth.make_config(name, seed=0, T=T)
+    full 8192-token chunk, the reference's own shape (I = 1024, skewed routing), and the
+    headline layer with 3- and 2-bit trellis codes (configs[4] repeats the hot path at those widths)."""
+    L, x, ids, w, cfg = synth.make_config(name, seed=0, T=T, bits=bits)
     out = run_layer(L, x, ids, w, dev).cpu().numpy()
     ref = O.expert_loop(x, ids, w, to_np_layer(L), LIMIT)
     err = O.rel_l2(out, ref)
-    print(f"{name} T={T} scatter={rt.resolve_scatter(None, T * cfg['topk'])}: rel L2 vs expert loop {err:.3e} "
-          f"over {T} tokens", flush=True)
+    print(f"{name} T={T} bits={cfg['bits']} scatter={rt.resolve_scatter(None, T * cfg['topk'])}: rel L2 vs expert "
+          f"loop {err:.3e} over {T} tokens", flush=True)
     assert np.isfinite(out).all()
     assert err < 1e-3
 
