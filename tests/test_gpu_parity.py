@@ -653,6 +653,24 @@ def test_fat_gemm_config2(dev, M):
     assert np.array_equal(alias.cpu().numpy(), outs[1])
 
 
+@pytest.mark.parametrize("M,bits", [(4090, 4), (4090, 3), (3600, 2)])
+def test_fat_gemm_kpair_shapes(dev, M, bits):
+    """The K-pair schedule (192 or more 256-row tiles x 128 columns at K = 4096, both K halves in one workgroup) on
+    row counts that are not a multiple of 16 (a partial last row group) and 2/3/4-bit tiles, against the oracle, with
+    every variant bit-identical and every output written."""
+    a, packed, svh = synth.make_fat(5, M=M, K=4096, N=1536, bits=bits)
+    ref = O.fat_gemm(a, packed, svh, dtype=np.float32)
+    outs = []
+    for v in range(4):
+        out = torch.full((M, 1536), float("nan"), dtype=torch.float32, device=dev)
+        gp.fat_gemm_v2(t16(a, dev), t16(packed, dev), out, t16(svh, dev), bits, True, False, v)
+        outs.append(out.cpu().numpy())
+    assert np.isfinite(outs[0]).all()
+    assert O.rel_l2(outs[0], ref) < 1e-5
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+
+
 def test_fat_gemm_scatter(dev):
     M, T = 300, 4096
     a, packed, svh = synth.make_fat(1, M=M, K=1024, N=4096)
