@@ -453,9 +453,14 @@ def fat_bench(args):
         line("down, I = 1024", M, 1024, 4096, dn_ms)
 
 
+GRAPH_CALLS = 10          # decode-path calls captured in one graph for graph_in_step_us
+
+
 def decode_bench(args):
     """moe_decode on the config-3 layer (E=288, H=4096, I=768) at small batches with softmax top-8 routing: HIP-event
-    time per call, eager and replayed from a captured graph, beside the prefill path at the same batch. Its bound is
+    time per call, eager, replayed from a captured graph of one call (graph_us), and per call from a graph of
+    GRAPH_CALLS calls (graph_in_step_us: a decode step's graph holds every layer, so its launch is paid once per
+    step), beside the prefill path at the same batch. Its bound is
     the trellis stream of the active experts (HBM) and their decode (VALU): bytes = active experts x 3 H I bits / 8
     plus their sign / scale vectors, x and out."""
     import numpy as np
@@ -504,12 +509,20 @@ def decode_bench(args):
         with torch.cuda.graph(g):
             call()
         graph_us = timed(g.replay, n)
+        # A decode step's graph holds every layer's call, so the graph launch is paid once per step, not per layer:
+        # GRAPH_CALLS back-to-back calls in one graph, time per call.
+        g_n = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_n):
+            for _ in range(GRAPH_CALLS):
+                call()
+        graph_step_us = timed(g_n.replay, max(n // GRAPH_CALLS, 4)) / GRAPH_CALLS
         prefill_us = None if args.decode_no_compare else round(timed(lambda: rt.grouped_prefill(x, ids, w, TL, 10.0),
                                                                          n), 2)
         active = int(np.unique(ids_np).size)
         nbytes = active * (3 * H * I * bits // 8 + (H + 2 * I + I + H) * 2) + T * H * 2 + T * H * 4
         print(json.dumps({"metric": "decode-path MoE us per layer", "tokens": T, "topk": k, "active_experts": active,
                           "eager_us": round(eager_us, 2), "graph_us": round(graph_us, 2),
+                          "graph_in_step_us": round(graph_step_us, 2), "graph_calls_per_step": GRAPH_CALLS,
                           "prefill_path_us": prefill_us, "bytes": nbytes,
                           "hbm_frac_graph": round(nbytes / (graph_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
                           "config": {"workload": f"layer1k weights: E={E} H={H} I={I} {bits}bpw top{k} softmax"}}),
