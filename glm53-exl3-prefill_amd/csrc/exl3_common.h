@@ -62,6 +62,9 @@ inline int device_cus()
 // The decode path's activation pass fused into its split-K gate|up GEMM (ATOMIC_F32 over both tensors, 64-row tiles;
 // trellis_gemm.h, act_after_last_slice): arrive is int32 [max_blocks * N / 128], zero before the call; act is fp16
 // T16 [a_rows rounded up to 16, N]; suh is suh_down with row e at suh + e * suh_stride (16-byte aligned).
+// K stages of act a down workgroup with the activation pass inside holds in LDS (12 KB; trellis_gemm_actin_kernel).
+constexpr int ACTIN_MAX_KB = 12;
+
 struct ActFuse
 {
     int* arrive;
@@ -69,6 +72,9 @@ struct ActFuse
     const uint16_t* suh;
     int64_t suh_stride;
     float limit;
+    // not null: the pass runs inside the down GEMM instead (mode 1 on tiles of at most 16 rows), which reads these fp32
+    // gate|up sums [rows, 2 I] and still stores act; arrive is then unused
+    const float* gu_in = nullptr;
 };
 
 // exl3_grouped_gemm_split, plus the fused activation pass when `act` is not null and the clear of zero[0 ..

@@ -89,6 +89,28 @@ __device__ __forceinline__ uint4 pack8_scaled(const float* x)
     return r;
 }
 
+// H128 over 8 values per lane x 16 lanes (index = 8 (lane & 15) + i), scaled by 1/sqrt(128): the row-major passes'
+// mapping. Its stages run in the same column-bit order as the T16 ones (bits 0-2 in registers, 3-6 across lanes), so
+// both round identically.
+__device__ __forceinline__ void had128_lane8(float (&x)[8], int lane)
+{
+    #pragma unroll
+    for (int len = 1; len < 8; len <<= 1)
+        #pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (!(i & len)) { const float a = x[i], b = x[i + len]; x[i] = a + b; x[i + len] = a - b; }
+    #pragma unroll
+    for (int i = 0; i < 8; ++i)
+    {
+        float v = x[i];
+        v = lane_butterfly<1>(v, lane);
+        v = lane_butterfly<2>(v, lane);
+        v = lane_butterfly<4>(v, lane);
+        v = lane_butterfly<8>(v, lane);
+        x[i] = v * HAD_SCALE;
+    }
+}
+
 __device__ __forceinline__ void had128_t16(float (&x)[32])
 {
     fwht_regs<1, 2>(x);

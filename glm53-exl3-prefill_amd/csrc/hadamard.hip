@@ -13,26 +13,6 @@ namespace {
 constexpr int HAD_THREADS = 256;
 constexpr int PAIRS_PER_WG = HAD_THREADS / 16;
 
-// H128 over 8 values per lane x 16 lanes (index = 8 (lane & 15) + i), scaled by 1/sqrt(128).
-__device__ __forceinline__ void had128_lane8(float (&x)[8], int lane)
-{
-    #pragma unroll
-    for (int len = 1; len < 8; len <<= 1)
-        #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (!(i & len)) { const float a = x[i], b = x[i + len]; x[i] = a + b; x[i + len] = a - b; }
-    #pragma unroll
-    for (int i = 0; i < 8; ++i)
-    {
-        float v = x[i];
-        v = lane_butterfly<1>(v, lane);
-        v = lane_butterfly<2>(v, lane);
-        v = lane_butterfly<4>(v, lane);
-        v = lane_butterfly<8>(v, lane);
-        x[i] = v * HAD_SCALE;
-    }
-}
-
 template <bool GATHER>
 __global__ __launch_bounds__(HAD_THREADS)
 void row_had_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, const int64_t* __restrict__ token_sorted,

@@ -119,6 +119,34 @@ int k_split_for(int64_t wgs, int stages, int target)
     return best;
 }
 
+// K slices for the down launch with the activation pass inside (trellis_gemm_actin_kernel): equal slices of whole
+// 128-column act blocks, at most ACTIN_MAX_KB stages each, with the cost rule of k_split_for but the fewest
+// workgroups among equals (at one token 2 slices of 12 stages ran 30.3-30.5 us per call in a step's graph, 3 slices
+// of 8 stages 30.6-30.8: each slice adds its partial rows into the same output row, and the act work per slice is
+// spread over the waves either way); 0 when no such split fits one round of `target` workgroups (the gate|up launch
+// then keeps the pass).
+int k_split_actin(int64_t wgs, int stages, int target)
+{
+    if (wgs <= 0 || stages % 4 != 0) return 0;
+    const int64_t cus = device_cus();
+    int best = 0;
+    int64_t best_cost = -1;
+    for (int per = 4; per <= ACTIN_MAX_KB && per <= stages; per += 4)
+    {
+        if (stages % per != 0) continue;
+        const int s = stages / per;
+        const int64_t n = wgs * s;
+        if (n > target) continue;
+        const int64_t cost = (n + cus - 1) / cus * per;
+        if (best_cost < 0 || cost <= best_cost)            // per rises: the last of equals has the fewest workgroups
+        {
+            best_cost = cost;
+            best = s;
+        }
+    }
+    return best;
+}
+
 // This device's address of `scratch`, looked up once per device with that device current. In host code the array's
 // name is not a device address: every host use of the scratch (kernel arguments, fills, copies) takes this pointer.
 int decode_scratch(void** ptr)
@@ -408,14 +436,27 @@ extern "C" int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, co
     }
     const int target = target_workgroups();
     const int gu_split = k_split_for((int64_t) L.max_blocks * 2 * (inter / 128), hidden / 32, target);
-    // gate|up slices add into the fp32 gu; the last workgroup of each (row tile, 128-column block) computes that block
-    // of act from the finished sums (the activation pass, without a launch of its own)
+    // With at most 16 routes every tile holds at most 16 rows (whatever the ids), and where the down launch can take K
+    // slices of whole act blocks the activation pass runs inside it (each down workgroup computes its own slice of act
+    // from the gate|up sums, behind its first trellis loads); otherwise the last gate|up workgroup of each (row tile,
+    // 128-column block) computes that block of act from the finished sums. Either way the pass needs no launch of its
+    // own.
+    const int actin_split = R <= 16 ? k_split_actin((int64_t) L.max_blocks * (hidden / 128), inter / 32, target) : 0;
     const ActFuse fuse{act_arrive, act, suh_down, suh2_stride, limit};
     rc = grouped_gemm_split(h13, R, hidden, EXL3_LAYOUT_T16, packed_gate, packed_up, w13_expert_stride_words,
                             hidden / 16, inter / 16, bits, svh_gate, svh_up, svh13_stride, block_expert, block_row0,
                             L.max_blocks, DECODE_TILE_ROWS, counts, expert_row0, n_experts, token_sorted, weight_sorted,
-                            nullptr, gu, R, EXL3_GEMM_ATOMIC_F32, gu_split, &fuse, s);
+                            nullptr, gu, R, EXL3_GEMM_ATOMIC_F32, gu_split, actin_split ? nullptr : &fuse, s);
     if (rc) return rc;
+    if (actin_split)
+    {
+        const ActFuse in{nullptr, act, suh_down, suh2_stride, limit, gu};
+        return grouped_gemm_split(act, R, inter, EXL3_LAYOUT_T16, packed_down, nullptr, w2_expert_stride_words,
+                                  inter / 16, hidden / 16, bits, svh_down, nullptr, svh2_stride, block_expert,
+                                  block_row0, L.max_blocks, DECODE_TILE_ROWS, counts, expert_row0, n_experts,
+                                  token_sorted, weight_sorted, nullptr, out, tokens, EXL3_GEMM_SCATTER_F32, actin_split,
+                                  &in, s);
+    }
     const int down_split = k_split_for((int64_t) L.max_blocks * (hidden / 128), inter / 32, target);
     return exl3_grouped_gemm_split(act, R, inter, EXL3_LAYOUT_T16, packed_down, nullptr, w2_expert_stride_words,
                                    inter / 16, hidden / 16, bits, svh_down, nullptr, svh2_stride, block_expert,

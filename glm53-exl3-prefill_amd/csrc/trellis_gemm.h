@@ -107,6 +107,9 @@ struct GemmParams
     const uint16_t* act_suh;       // suh_down, row e at act_suh + e * act_suh_stride
     int64_t act_suh_stride;
     float act_limit;
+    // SCATTER_F32 thin tiles of the decode path (trellis_gemm_actin_kernel): the fp32 gate|up sums [rows, 2 I] from
+    // which each workgroup computes its own K slice of act into LDS (act_suh / act_suh_stride / act_limit as above)
+    const float* act_gu;
     // a side job of the launch: clear zero[0 .. zero4) (float4s), a buffer a later launch accumulates into
     float4* zero;
     int64_t zero4;
@@ -627,6 +630,137 @@ __device__ __forceinline__ void act_after_last_slice(const GemmParams& p, const 
     }
 }
 
+// The activation pass for one thin tile's rows over its K slice (whole 128-column blocks of act, at most
+// ACTIN_MAX_KB / 4 = 3, one per wave), into LDS as the T16 blocks the main loop multiplies: stage s of the slice is
+// 1 KB at dst + s KB, lane l's 16 bytes = row l & 15, k chunk l >> 4 (the layout of one T16 activation load). Each row
+// gets the separate pass's arithmetic (clamped SwiGLU rounded to fp16, x suh_down, H128, x 1/sqrt(128), fp16), so the
+// slice holds exactly the act that pass would store. The workgroups of the first output column block also store their
+// slice's valid rows to act_out (T16), one writer per element, so the act of the call stays in the workspace as the
+// other placement leaves it. Two phases, so that the thin tile's first trellis loads go out between them: act_load
+// issues the gate|up sum and suh_down loads, act_store computes and writes.
+// One row (every tile of a one-token call with distinct experts): lane l takes columns 2 l and 2 l + 1 of the wave's
+// block. Up to 4 rows: lane l takes row l >> 4 and the 8 consecutive columns 8 (l & 15) ..
+// of the wave's block (the row-major pass's mapping, had128_lane8: a quarter of the work per row of the 16-row
+// mapping, the same rounding); rows 4-15 of the slice stay unwritten, and only rows past the tile's last multiply
+// them. Taller tiles take the 16-row T16 mapping (act_had_row), loading and computing in the second phase.
+static_assert(ACTIN_MAX_KB <= 16, "one act block per wave");
+struct ActIn
+{
+    float g[8], u[8];
+    uint4 s;
+};
+__device__ __forceinline__ void act_load(const GemmParams& p, const Tile& t, int wave, int lane, ActIn& a)
+{
+    if (t.rows_valid > 4 || wave >= t.num_kb / 4) return;
+    const int I = p.size_k;
+    if (t.rows_valid == 1)
+    {
+        // one row: lane l takes columns 2 l and 2 l + 1 of the wave's block
+        const int64_t r = t.row0;
+        const int c = (t.kb0 / 4 + wave) * 128 + 2 * lane;
+        const float2 g = *reinterpret_cast<const float2*>(p.act_gu + r * 2 * (int64_t) I + c);
+        const float2 u = *reinterpret_cast<const float2*>(p.act_gu + r * 2 * (int64_t) I + I + c);
+        a.g[0] = h2f(f2h(g.x)); a.g[1] = h2f(f2h(g.y));        // the sums as the fp16 gate|up of the reference
+        a.u[0] = h2f(f2h(u.x)); a.u[1] = h2f(f2h(u.y));
+        a.s.x = *reinterpret_cast<const uint32_t*>(p.act_suh + (int64_t) t.e * p.act_suh_stride + c);
+        return;
+    }
+    const int q = lane >> 4, c16 = lane & 15;
+    const int64_t r = (int64_t) t.row0 + min(q, t.rows_valid - 1);
+    const int c = (t.kb0 / 4 + wave) * 128 + 8 * c16;
+    load_gu8<true, false>(p.act_gu, r * 2 * (int64_t) I + c, a.g);
+    load_gu8<true, false>(p.act_gu, r * 2 * (int64_t) I + I + c, a.u);
+    a.s = *reinterpret_cast<const uint4*>(p.act_suh + (int64_t) t.e * p.act_suh_stride + c);
+}
+__device__ __forceinline__ void act_store(const GemmParams& p, const Tile& t, int wave, int lane, const ActIn& a,
+                                          unsigned char* dst)
+{
+    if (wave >= t.num_kb / 4) return;
+    const int I = p.size_k;
+    const int blk = t.kb0 / 4 + wave;
+    uint4* o = reinterpret_cast<uint4*>(dst);
+    if (t.rows_valid == 1)
+    {
+        // one row, columns 2 l and 2 l + 1 on lane l: column bit 0 in registers, bits 1-4 across lanes l ^ 1 .. l ^ 8,
+        // bits 5 and 6 across l ^ 16 and l ^ 32 -- the same stage order as the other mappings, so the same rounding
+        float x[2];
+        #pragma unroll
+        for (int j = 0; j < 2; ++j)
+        {
+            const float gc = fminf(a.g[j], p.act_limit);
+            const float uc = fminf(fmaxf(a.u[j], -p.act_limit), p.act_limit);
+            x[j] = h2f(f2h(silu_mul(gc, uc))) * h2f((uint16_t) (a.s.x >> (16 * j)));   // fp16 rounding point
+        }
+        {
+            const float s0 = x[0] + x[1], d0 = x[0] - x[1];
+            x[0] = s0;
+            x[1] = d0;
+        }
+        #pragma unroll
+        for (int j = 0; j < 2; ++j)
+        {
+            x[j] = lane_butterfly<1>(x[j], lane);
+            x[j] = lane_butterfly<2>(x[j], lane);
+            x[j] = lane_butterfly<4>(x[j], lane);
+            x[j] = lane_butterfly<8>(x[j], lane);
+        }
+        pair_butterfly16(x[0], x[1]);
+        pair_butterfly32(x[0], x[1]);
+        const uint32_t pk = (uint32_t) f2h(x[0] * HAD_SCALE) | ((uint32_t) f2h(x[1] * HAD_SCALE) << 16);
+        // T16: stage lane / 16 of the block, k chunk (lane / 4) % 4, row 0, values 2 (lane % 4) ..
+        reinterpret_cast<uint32_t*>(dst)[((4 * wave + (lane >> 4)) * 64 + ((lane >> 2) & 3) * 16) * 4 + (lane & 3)] = pk;
+        if (t.nt == 0)
+        {
+            const int64_t r = t.row0;
+            const int64_t chunk = (r >> 4) * (I / 8) + blk * 16 + (lane >> 2);
+            reinterpret_cast<uint32_t*>(p.act_out + chunk * 128 + (r & 15) * 8)[lane & 3] = pk;
+        }
+        return;
+    }
+    if (t.rows_valid <= 4)
+    {
+        const int q = lane >> 4, c16 = lane & 15;
+        const int64_t r = (int64_t) t.row0 + min(q, t.rows_valid - 1);
+        float ss[8], x[8];
+        unpack8(a.s, ss);
+        #pragma unroll
+        for (int j = 0; j < 8; ++j)
+        {
+            const float gc = fminf(a.g[j], p.act_limit);
+            const float uc = fminf(fmaxf(a.u[j], -p.act_limit), p.act_limit);
+            x[j] = h2f(f2h(silu_mul(gc, uc))) * ss[j];              // fp16 rounding point of the reference
+        }
+        had128_lane8(x, lane);
+        const uint4 pk = pack8(x);
+        o[(4 * wave + (c16 >> 2)) * 64 + (c16 & 3) * 16 + q] = pk;
+        if (t.nt == 0 && q < t.rows_valid)
+        {
+            const int64_t chunk = (r >> 4) * (I / 8) + blk * 16 + c16;
+            *reinterpret_cast<uint4*>(p.act_out + chunk * 128 + (r & 15) * 8) = pk;
+        }
+        return;
+    }
+    const int rl = lane & 15, cq = lane >> 4;
+    const int64_t r = (int64_t) t.row0 + min(rl, t.rows_valid - 1);
+    float x[32];
+    act_had_row<true, false, false>(p.act_gu, r, blk, cq, I, p.act_suh + (int64_t) t.e * p.act_suh_stride,
+                                    p.act_limit, x);
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        float v[8];
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = x[8 * i + j];
+        const uint4 pk = pack8(v);
+        o[(4 * wave + i) * 64 + cq * 16 + rl] = pk;
+        if (t.nt == 0 && rl < t.rows_valid)
+        {
+            const int64_t chunk = (r >> 4) * (I / 8) + blk * 16 + 4 * i + cq;
+            *reinterpret_cast<uint4*>(p.act_out + chunk * 128 + (r & 15) * 8) = pk;
+        }
+    }
+}
+
 // Thin tiles of at most 16 rows (one row group; the MBN == 1 kernels, which run most of the decode path's tiles): every
 // wave decodes the weights of its own 32 output columns (Decoder cols) into its part of the double-buffered stage tile
 // and multiplies the row group by them, so no wave reads weights another wave decoded and the stages need no barrier
@@ -634,7 +768,9 @@ __device__ __forceinline__ void act_after_last_slice(const GemmParams& p, const 
 // shared-tile loop does, so the results are its results bit for bit. Afterwards the accumulators go through LDS so that
 // wave 0 holds the group over all 128 columns, the layout of the shared epilogue. (Taller thin tiles keep the shared
 // loop: there every wave would load all of the tile's activation rows, and a 1024-token layer ran 3.5% slower.)
-template <int BITS, int MODE>
+// ACT_IN: the activation operand is computed by the workgroup itself (act_load / act_store around the first
+// trellis loads) and read from LDS instead of loaded.
+template <int BITS, int MODE, bool ACT_IN = false>
 __device__ __forceinline__ void thin_tile(const GemmParams& p, const Tile& t, int group, int wave, int lane,
                                           unsigned char* lds_raw)
 {
@@ -644,6 +780,11 @@ __device__ __forceinline__ void thin_tile(const GemmParams& p, const Tile& t, in
     constexpr int NR = Dec::NR;
     const Dec dec(p, t, wave, lane, num_kb, true);
     const Mma mm(p, t, 0, lane, num_kb, 64);                       // the A operand of row group 0
+    // ACT_IN: stage s's activation fragment from the slice in LDS (stages past the last clamped, like the loads)
+    auto act_from_lds = [&](int s) {
+        const uint4* a = reinterpret_cast<const uint4*>(lds_raw + LDS_MAIN_BYTES);
+        return __builtin_bit_cast(half8_t, a[min(s, num_kb - 1) * 64 + lane]);
+    };
     floatx4 acc[4][2];
     #pragma unroll
     for (int nb = 0; nb < 2; ++nb) acc[0][nb] = {};
@@ -652,11 +793,21 @@ __device__ __forceinline__ void thin_tile(const GemmParams& p, const Tile& t, in
         half8_t act[ACT_DEPTH][4];
         {
             uint32_t r0[NR];
+            ActIn ain;
+            if constexpr (ACT_IN) act_load(p, t, wave, lane, ain);
             dec.load(0, r0);
             #pragma unroll
             for (int s = 1; s <= RAW_DEPTH; ++s) dec.load(s, raw[s % RAW_DEPTH]);
-            #pragma unroll
-            for (int s = 0; s < ACT_DEPTH; ++s) mm.load_act<1>(s, act[s]);
+            if constexpr (ACT_IN)
+            {
+                act_store(p, t, wave, lane, ain, lds_raw + LDS_MAIN_BYTES);
+                __syncthreads();
+                #pragma unroll
+                for (int s = 0; s < ACT_DEPTH; ++s) act[s][0] = act_from_lds(s);
+            }
+            else
+                #pragma unroll
+                for (int s = 0; s < ACT_DEPTH; ++s) mm.load_act<1>(s, act[s]);
             typename Dec::Out o;
             dec.decode(r0, o);
             dec.store(o, lds_b);
@@ -674,7 +825,8 @@ __device__ __forceinline__ void thin_tile(const GemmParams& p, const Tile& t, in
                 Mma::mfma2<1>(f, act[u % ACT_DEPTH], acc);
                 dec.store(o, lds_b + ((u + 1) & 1) * LDS_TILE);
                 dec.load(s + 1 + RAW_DEPTH, raw[(u + 1) % RAW_DEPTH]);
-                mm.load_act<1>(s + ACT_DEPTH, act[u % ACT_DEPTH]);
+                if constexpr (ACT_IN) act[u % ACT_DEPTH][0] = act_from_lds(s + ACT_DEPTH);
+                else mm.load_act<1>(s + ACT_DEPTH, act[u % ACT_DEPTH]);
             }
         };
         using full_trip = std::integral_constant<int, UNROLL>;
@@ -898,6 +1050,38 @@ void trellis_gemm_kernel(const GemmParams p)
         shared_tile<BITS, MODE, MBN, WAVES>(p, t, group, wave, lane, lds_raw, lds_epi + wave);
 }
 
+// The decode path's down GEMM with the activation pass inside (SCATTER_F32 on 64-row tiles of at most 16 rows): each
+// workgroup computes the act of its tile's rows over its K slice from the fp32 gate|up sums (act_load, act_store) while
+// its first trellis loads are in flight and multiplies it from LDS, so the gate|up launch ends without the pass. The
+// host sends it only calls of at most 16 routes (so no tile holds more than 16 rows) and K slices of whole 128-column
+// act blocks, at most ACTIN_MAX_KB stages each.
+template <int BITS>
+__global__ __launch_bounds__(256, 4)
+void trellis_gemm_actin_kernel(const GemmParams p)
+{
+    constexpr int SCB = lds_scatter_bytes<4>();
+    constexpr int ACT_END = LDS_MAIN_BYTES + ACTIN_MAX_KB * 1024;
+    __shared__ __align__(16) unsigned char lds_raw[SCB > ACT_END ? SCB : ACT_END];
+    int group, slot;
+    xcd_group_slot((int) blockIdx.x, p.k_split > 1 ? p.n_slots * p.k_split : p.n_slots, group, slot);
+    Tile t;
+    if (!resolve_tile<false>(p, group, slot, t)) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    thin_tile<BITS, MODE_SCATTER_F32, true>(p, t, group, wave, lane, lds_raw);
+}
+
+template <int BITS>
+int launch_gemm_actin(const GemmParams& p, hipStream_t s)
+{
+    const int groups8 = (p.n_groups + 7) / 8 * 8;
+    const int64_t grid = (int64_t) groups8 * p.n_slots * (p.k_split > 1 ? p.k_split : 1);
+    if (grid == 0) return EXL3_OK;
+    if (grid > 0x7FFFFFFF) return fail("grid too large");
+    trellis_gemm_actin_kernel<BITS><<<(unsigned) grid, 256, 0, s>>>(p);
+    return EXL3_OK;
+}
+
 // A dense GEMM whose 256-row tiles would leave CUs idle (long K, few rows): the two K halves of one tile run in one
 // workgroup of 8 waves, waves 0-3 over the first half and 4-7 over the second, each half the 4-wave main loop over its
 // own double-buffered stage tiles (the barriers are shared: both halves run the same number of stages). The second
@@ -996,5 +1180,8 @@ int launch_gemm_b4d(int mode, const GemmParams& p, hipStream_t s);
 int launch_gemm_kpair_b2(int mode, const GemmParams& p, hipStream_t s);
 int launch_gemm_kpair_b3(int mode, const GemmParams& p, hipStream_t s);
 int launch_gemm_kpair_b4(int mode, const GemmParams& p, hipStream_t s);
+int launch_gemm_actin_b2(const GemmParams& p, hipStream_t s);
+int launch_gemm_actin_b3(const GemmParams& p, hipStream_t s);
+int launch_gemm_actin_b4(const GemmParams& p, hipStream_t s);
 
 }  // namespace exl3

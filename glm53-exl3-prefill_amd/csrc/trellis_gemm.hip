@@ -190,6 +190,17 @@ int launch_bits(int bits, const GemmParams& p, hipStream_t s)
     }
 }
 
+int launch_actin_bits(int bits, const GemmParams& p, hipStream_t s)
+{
+    switch (bits)
+    {
+        case 2: return launch_gemm_actin_b2(p, s);
+        case 3: return launch_gemm_actin_b3(p, s);
+        case 4: return launch_gemm_actin_b4(p, s);
+        default: return fail("unsupported bits %d (2, 3 or 4)", bits);
+    }
+}
+
 // The K-pair schedule (trellis_gemm_kpair_kernel): a dense store on 256-row tiles with both K halves of a tile in one
 // 8-wave workgroup.
 template <int MODE>
@@ -264,7 +275,22 @@ int grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layo
     EXL3_CHECK(zero_floats == 0 || max_blocks > 0, "the clear runs on the GEMM's workgroups: max_blocks must be > 0");
     p.zero = reinterpret_cast<float4*>(zero);
     p.zero4 = zero_floats / 4;
-    if (act)
+    if (act && act->gu_in)
+    {
+        EXL3_CHECK(mode == EXL3_GEMM_SCATTER_F32 && n_tensors == 1 && tile_rows == 64 && a_layout == EXL3_LAYOUT_T16,
+                   "internal: the activation pass inside the down GEMM runs on mode 1 with 64-row tiles");
+        EXL3_CHECK(total_kb % 4 == 0 && p.kb_per_split % 4 == 0 && p.kb_per_split <= ACTIN_MAX_KB,
+                   "internal: the down GEMM's K slices must be whole 128-column act blocks of at most %d stages",
+                   ACTIN_MAX_KB);
+        EXL3_CHECK(act->suh && act->act && aligned16(act->suh) && act->suh_stride % 8 == 0 && aligned16(act->gu_in) &&
+                   aligned16(act->act), "suh_down, act and the gate|up sums must be 16-byte aligned");
+        p.act_gu = act->gu_in;
+        p.act_out = act->act;
+        p.act_suh = act->suh;
+        p.act_suh_stride = act->suh_stride;
+        p.act_limit = act->limit;
+    }
+    else if (act)
     {
         EXL3_CHECK(mode == EXL3_GEMM_ATOMIC_F32 && n_tensors == 2 && tile_rows == 64,
                    "internal: the fused activation pass runs on mode 3 over gate|up with 64-row tiles");
@@ -292,7 +318,7 @@ int grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layo
         EXL3_CHECK(n_tensors == 1, "mode 1: out fp32 [T, N], single tensor");
         EXL3_CHECK(token_sorted && route_weight, "routing dtypes");
         p.out_ld = size_n_each;
-        rc = launch_bits<MODE_SCATTER_F32, false>(bits, p, s);
+        rc = p.act_gu ? launch_actin_bits(bits, p, s) : launch_bits<MODE_SCATTER_F32, false>(bits, p, s);
     }
     else if (mode == EXL3_GEMM_STORE_ROUTE_F32)
     {

@@ -36,4 +36,6 @@ int launch_gemm_kpair_b3(int mode, const GemmParams& p, hipStream_t s)
     }
     return fail("internal: no K-pair kernel for mode %d", mode);
 }
+
+int launch_gemm_actin_b3(const GemmParams& p, hipStream_t s) { return launch_gemm_actin<3>(p, s); }
 }  // namespace exl3

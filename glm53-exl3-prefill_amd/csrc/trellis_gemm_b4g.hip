@@ -15,4 +15,6 @@ int launch_gemm_b4g(int mode, const GemmParams& p, hipStream_t s)
     }
     return fail("internal: no kernel for mode %d", mode);
 }
+
+int launch_gemm_actin_b4(const GemmParams& p, hipStream_t s) { return launch_gemm_actin<4>(p, s); }
 }  // namespace exl3

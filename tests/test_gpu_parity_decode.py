@@ -200,11 +200,12 @@ def test_decode_fused_prep_matches_separate_launches(dev, name, T, drop):
 @pytest.mark.parametrize("name,T,drop", [("layer1k", 1, False), ("layer1k", 3, True), ("layer1k", 16, False),
                                          ("layer1k", 40, False), ("tiny", 1, False), ("tiny", 63, True)])
 def test_decode_fused_act_matches_act_had(dev, name, T, drop):
-    """The decode op has no activation launch: the gate|up workgroup that adds the last K slice of a (row tile,
-    128-column block) computes that block of act from the finished fp32 sums. It must equal the activation pass
-    (kernel/exl3_grouped_prefill.cu:118-141, here act_had over the same fp32 gu) bit for bit on every routed row --
-    with K split into slices (1 and 3 tokens: up to 10 slices on layer1k) and unsplit (16 and 40 tokens), dropped
-    routes, and the tiny layer's 2 column blocks."""
+    """The decode op has no activation launch. With at most 16 routes (one token) every down workgroup computes the
+    act of its K slice itself from the fp32 gate|up sums (the first column block's workgroups also store it);
+    otherwise the gate|up workgroup that adds the last K slice of a (row tile, 128-column block) computes that block
+    of act from the finished sums. Either way the act must equal the activation pass (kernel/exl3_grouped_prefill.cu:
+    118-141, here act_had over the same fp32 gu) bit for bit on every routed row -- with K split into slices (1 and 3
+    tokens) and unsplit (16 and 40 tokens), dropped routes, and the tiny layer's 2 column blocks."""
     L, cfg = layer_case(name, svh_scale=1 / 64)
     TL = device_layer(name, svh_scale=1 / 64)
     E, H, I, k = cfg["E"], cfg["H"], cfg["I"], cfg["topk"]
@@ -339,11 +340,14 @@ def test_decode_vs_expert_loop_tiny(dev, T, svh_scale):
     assert O.rel_l2(got, ref) < 1e-3
 
 
+@pytest.mark.parametrize("T", [1, 4])
 @pytest.mark.parametrize("bits", [3, 2])
-def test_decode_low_bits(dev, bits):
+def test_decode_low_bits(dev, bits, T):
+    """2/3-bit trellis through both placements of the activation pass: inside the down launch (one token, 8 routes)
+    and at the end of the gate|up launch (four tokens, 32 routes)."""
     L, cfg = layer_case("layer1k", bits=bits, svh_scale=1 / 64)
     TL = device_layer("layer1k", bits=bits, svh_scale=1 / 64)
-    x, ids, w = inputs(cfg, 4, 20 + bits)
+    x, ids, w = inputs(cfg, T, 20 + bits)
     got = decode(TL, x, ids, w, dev).cpu().numpy()
     assert O.rel_l2(got, O.expert_loop(x, ids, w, to_np_layer(L), LIMIT)) < 1e-3
 
