@@ -591,6 +591,54 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
     }
 }
 
+// The act of one row's columns 2 l, 2 l + 1 of a 128-column block on lane l, from its fp16-rounded gate / up sums and
+// suh_down pair: column bit 0 in registers, bits 1-4 across lanes l ^ 1 .. l ^ 8, bits 5 and 6 across l ^ 16 and
+// l ^ 32 -- the stage order of the other mappings, so the same rounding. Packed fp16 pair.
+__device__ __forceinline__ uint32_t act_pair(const float* g, const float* u, uint32_t s, float limit, int lane)
+{
+    float x[2];
+    #pragma unroll
+    for (int j = 0; j < 2; ++j)
+    {
+        const float gc = fminf(g[j], limit);
+        const float uc = fminf(fmaxf(u[j], -limit), limit);
+        x[j] = h2f(f2h(silu_mul(gc, uc))) * h2f((uint16_t) (s >> (16 * j)));   // fp16 rounding point of the reference
+    }
+    {
+        const float s0 = x[0] + x[1], d0 = x[0] - x[1];
+        x[0] = s0;
+        x[1] = d0;
+    }
+    #pragma unroll
+    for (int j = 0; j < 2; ++j)
+    {
+        x[j] = lane_butterfly<1>(x[j], lane);
+        x[j] = lane_butterfly<2>(x[j], lane);
+        x[j] = lane_butterfly<4>(x[j], lane);
+        x[j] = lane_butterfly<8>(x[j], lane);
+    }
+    pair_butterfly16(x[0], x[1]);
+    pair_butterfly32(x[0], x[1]);
+    return (uint32_t) f2h(x[0] * HAD_SCALE) | ((uint32_t) f2h(x[1] * HAD_SCALE) << 16);
+}
+
+// The act of 8 consecutive columns 8 (l & 15) .. of a 128-column block for the row lane l holds (the row-major pass's
+// mapping, 4 rows per wave, had128_lane8), from fp16-rounded sums and suh_down. Packed fp16.
+__device__ __forceinline__ uint4 act_oct(const float (&g)[8], const float (&u)[8], uint4 s, float limit, int lane)
+{
+    float ss[8], x[8];
+    unpack8(s, ss);
+    #pragma unroll
+    for (int j = 0; j < 8; ++j)
+    {
+        const float gc = fminf(g[j], limit);
+        const float uc = fminf(fmaxf(u[j], -limit), limit);
+        x[j] = h2f(f2h(silu_mul(gc, uc))) * ss[j];                          // fp16 rounding point of the reference
+    }
+    had128_lane8(x, lane);
+    return pack8(x);
+}
+
 // act_had fused into the split-K gate|up GEMM of 64-row tiles (ATOMIC_F32 into fp32 gu, both tensors). Every
 // workgroup of a (row tile, column block nt) pair -- gate and up, each K slice -- counts its arrival after its adds;
 // the one that arrives last (2 k_split arrivals) computes act for the tile's rows over block nt with the activation
@@ -612,6 +660,44 @@ __device__ __forceinline__ void act_after_last_slice(const GemmParams& p, const 
     __syncthreads();
     if (!last) return;                                  // uniform over the workgroup
     const int I = p.n_tiles_each * TILE_N;
+    const int64_t W = 2 * (int64_t) I;
+    const float* gu = reinterpret_cast<const float*>(p.out);
+    const uint16_t* suh_e = p.act_suh + (int64_t) t.e * p.act_suh_stride;
+    if (t.rows_valid <= 4)
+    {
+        // small tiles (the common case of a few tokens): wave 0 alone, with the one-row or four-row mapping, a
+        // sixteenth or a quarter of the 16-row mapping's work, the same rounding
+        if (wave != 0) return;
+        if (t.rows_valid == 1)
+        {
+            const int64_t r = t.row0;
+            const int c = t.nt * TILE_N + 2 * lane;
+            float g[2], u[2];
+            #pragma unroll
+            for (int j = 0; j < 2; ++j)
+            {
+                g[j] = h2f(f2h(__hip_atomic_load(gu + r * W + c + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+                u[j] = h2f(f2h(__hip_atomic_load(gu + r * W + I + c + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+            }
+            const uint32_t pk = act_pair(g, u, *reinterpret_cast<const uint32_t*>(suh_e + c), p.act_limit, lane);
+            const int64_t chunk = (r >> 4) * (I / 8) + t.nt * 16 + (lane >> 2);
+            reinterpret_cast<uint32_t*>(p.act_out + chunk * 128 + (r & 15) * 8)[lane & 3] = pk;
+            return;
+        }
+        const int q = lane >> 4, c16 = lane & 15;
+        const int64_t r = (int64_t) t.row0 + min(q, t.rows_valid - 1);
+        const int c = t.nt * TILE_N + 8 * c16;
+        float g[8], u[8];
+        load_gu8<true, true>(gu, r * W + c, g);
+        load_gu8<true, true>(gu, r * W + I + c, u);
+        const uint4 pk = act_oct(g, u, *reinterpret_cast<const uint4*>(suh_e + c), p.act_limit, lane);
+        if (q < t.rows_valid)
+        {
+            const int64_t chunk = (r >> 4) * (I / 8) + t.nt * 16 + c16;
+            *reinterpret_cast<uint4*>(p.act_out + chunk * 128 + (r & 15) * 8) = pk;
+        }
+        return;
+    }
     const int rl = lane & 15, cq = lane >> 4;
     const int g0 = 16 * wave;
     if (g0 >= t.rows_valid) return;
@@ -644,6 +730,7 @@ __device__ __forceinline__ void act_after_last_slice(const GemmParams& p, const 
 // mapping, the same rounding); rows 4-15 of the slice stay unwritten, and only rows past the tile's last multiply
 // them. Taller tiles take the 16-row T16 mapping (act_had_row), loading and computing in the second phase.
 static_assert(ACTIN_MAX_KB <= 16, "one act block per wave");
+
 struct ActIn
 {
     float g[8], u[8];
@@ -681,32 +768,7 @@ __device__ __forceinline__ void act_store(const GemmParams& p, const Tile& t, in
     uint4* o = reinterpret_cast<uint4*>(dst);
     if (t.rows_valid == 1)
     {
-        // one row, columns 2 l and 2 l + 1 on lane l: column bit 0 in registers, bits 1-4 across lanes l ^ 1 .. l ^ 8,
-        // bits 5 and 6 across l ^ 16 and l ^ 32 -- the same stage order as the other mappings, so the same rounding
-        float x[2];
-        #pragma unroll
-        for (int j = 0; j < 2; ++j)
-        {
-            const float gc = fminf(a.g[j], p.act_limit);
-            const float uc = fminf(fmaxf(a.u[j], -p.act_limit), p.act_limit);
-            x[j] = h2f(f2h(silu_mul(gc, uc))) * h2f((uint16_t) (a.s.x >> (16 * j)));   // fp16 rounding point
-        }
-        {
-            const float s0 = x[0] + x[1], d0 = x[0] - x[1];
-            x[0] = s0;
-            x[1] = d0;
-        }
-        #pragma unroll
-        for (int j = 0; j < 2; ++j)
-        {
-            x[j] = lane_butterfly<1>(x[j], lane);
-            x[j] = lane_butterfly<2>(x[j], lane);
-            x[j] = lane_butterfly<4>(x[j], lane);
-            x[j] = lane_butterfly<8>(x[j], lane);
-        }
-        pair_butterfly16(x[0], x[1]);
-        pair_butterfly32(x[0], x[1]);
-        const uint32_t pk = (uint32_t) f2h(x[0] * HAD_SCALE) | ((uint32_t) f2h(x[1] * HAD_SCALE) << 16);
+        const uint32_t pk = act_pair(a.g, a.u, a.s.x, p.act_limit, lane);
         // T16: stage lane / 16 of the block, k chunk (lane / 4) % 4, row 0, values 2 (lane % 4) ..
         reinterpret_cast<uint32_t*>(dst)[((4 * wave + (lane >> 4)) * 64 + ((lane >> 2) & 3) * 16) * 4 + (lane & 3)] = pk;
         if (t.nt == 0)
@@ -721,17 +783,7 @@ __device__ __forceinline__ void act_store(const GemmParams& p, const Tile& t, in
     {
         const int q = lane >> 4, c16 = lane & 15;
         const int64_t r = (int64_t) t.row0 + min(q, t.rows_valid - 1);
-        float ss[8], x[8];
-        unpack8(a.s, ss);
-        #pragma unroll
-        for (int j = 0; j < 8; ++j)
-        {
-            const float gc = fminf(a.g[j], p.act_limit);
-            const float uc = fminf(fmaxf(a.u[j], -p.act_limit), p.act_limit);
-            x[j] = h2f(f2h(silu_mul(gc, uc))) * ss[j];              // fp16 rounding point of the reference
-        }
-        had128_lane8(x, lane);
-        const uint4 pk = pack8(x);
+        const uint4 pk = act_oct(a.g, a.u, a.s, p.act_limit, lane);
         o[(4 * wave + (c16 >> 2)) * 64 + (c16 & 3) * 16 + q] = pk;
         if (t.nt == 0 && q < t.rows_valid)
         {
