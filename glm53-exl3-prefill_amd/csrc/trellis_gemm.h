@@ -591,6 +591,63 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const Tile& t, int
     }
 }
 
+// Epilogue inputs of a one-row tile in the atomic modes, loaded before the main loop: lane l's svh of columns l and
+// l + 64 (scaled by 1 / sqrt(128)), the row's route weight and destination row (uniform).
+struct OneRow
+{
+    float sv0, sv1, rw;
+    int64_t dest;
+};
+
+template <int MODE>
+__device__ __forceinline__ OneRow one_row_inputs(const GemmParams& p, const Tile& t, int lane)
+{
+    OneRow o;
+    o.sv0 = h2f(t.svh[lane]) * HAD_SCALE;
+    o.sv1 = h2f(t.svh[lane + 64]) * HAD_SCALE;
+    o.rw = 1.0f;
+    o.dest = t.row0;
+    if constexpr (MODE == MODE_SCATTER_F32)
+    {
+        o.rw = h2f(p.route_weight[t.row0]);
+        o.dest = p.token[t.row0];
+    }
+    return o;
+}
+
+// The epilogue of a tile whose only row is row 0 (atomic modes), run by one wave: the row's 128 sums, as the waves left
+// their column blocks in LDS (xs: block b's floatx4 of lane 16 kq + row at b * 64 + lane, columns 16 b + 4 kq + r), are
+// gathered as columns l and l + 64 on lane l, so one H128 over 64 lanes replaces sixteen rows' worth of it. The
+// butterfly stages run in the general epilogue's order over the column bits (0, 1, 4, 5, 6, then 2 and 3, each stage's
+// sums a + b and differences a - b of the same operands), and the scaling multiplies in its order (x * svh / sqrt(128),
+// then the route weight), so each output is the general epilogue's bit for bit.
+template <int MODE>
+__device__ __forceinline__ void one_row_epilogue(const GemmParams& p, const Tile& t, int lane, const float* xs,
+                                                 const OneRow& in)
+{
+    auto at = [&](int c) { return xs[(c >> 4) * 256 + ((c >> 2) & 3) * 64 + (c & 3)]; };
+    float x0 = at(lane), x1 = at(lane + 64);
+    x0 = lane_butterfly<1>(x0, lane);                   // column bit 0
+    x1 = lane_butterfly<1>(x1, lane);
+    x0 = lane_butterfly<2>(x0, lane);                   // bit 1
+    x1 = lane_butterfly<2>(x1, lane);
+    pair_butterfly16(x0, x1);                           // bit 4
+    pair_butterfly32(x0, x1);                           // bit 5
+    {
+        const float s = x0 + x1, d = x0 - x1;           // bit 6
+        x0 = s;
+        x1 = d;
+    }
+    x0 = lane_butterfly<4>(x0, lane);                   // bit 2
+    x1 = lane_butterfly<4>(x1, lane);
+    x0 = lane_butterfly<8>(x0, lane);                   // bit 3
+    x1 = lane_butterfly<8>(x1, lane);
+    float* o = reinterpret_cast<float*>(p.out) + in.dest * p.out_ld + t.which * p.n_tiles_each * TILE_N +
+               t.nt * TILE_N + lane;
+    unsafeAtomicAdd(o, x0 * in.sv0 * in.rw);
+    unsafeAtomicAdd(o + 64, x1 * in.sv1 * in.rw);
+}
+
 // The act of one row's columns 2 l, 2 l + 1 of a 128-column block on lane l, from its fp16-rounded gate / up sums and
 // suh_down pair: column bit 0 in registers, bits 1-4 across lanes l ^ 1 .. l ^ 8, bits 5 and 6 across l ^ 16 and
 // l ^ 32 -- the stage order of the other mappings, so the same rounding. Packed fp16 pair.
@@ -840,6 +897,9 @@ __device__ __forceinline__ void thin_tile(const GemmParams& p, const Tile& t, in
     floatx4 acc[4][2];
     #pragma unroll
     for (int nb = 0; nb < 2; ++nb) acc[0][nb] = {};
+    const bool one_row = atomic_mode(MODE) && t.rows_valid == 1;   // uniform
+    OneRow one{};
+    if (one_row) one = one_row_inputs<MODE>(p, t, lane);           // in flight with the pipeline's first loads
     {
         uint32_t raw[RAW_DEPTH][NR];
         half8_t act[ACT_DEPTH][4];
@@ -898,6 +958,14 @@ __device__ __forceinline__ void thin_tile(const GemmParams& p, const Tile& t, in
     xs[(2 * wave) * 64 + lane] = acc[0][0];
     xs[(2 * wave + 1) * 64 + lane] = acc[0][1];
     __syncthreads();
+    if constexpr (atomic_mode(MODE))
+        if (one_row)
+        {
+            if (wave == 0) one_row_epilogue<MODE>(p, t, lane, reinterpret_cast<const float*>(lds_raw), one);
+            if constexpr (MODE == MODE_ATOMIC_F32)
+                if (p.act_arrive) act_after_last_slice(p, t, group, wave, lane);   // every wave arrives
+            return;
+        }
     if (wave == 0)
         #pragma unroll
         for (int nb = 0; nb < 8; ++nb) full[0][nb] = xs[nb * 64 + lane];

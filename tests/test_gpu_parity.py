@@ -706,6 +706,34 @@ def test_fat_gemm_short_k(dev, M, K, bits):
     assert O.rel_l2(out.cpu().numpy(), ref) < 1e-5
 
 
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_one_row_tile_epilogue_bit_identical(dev, bits):
+    """A tile holding one row takes its own epilogue in the fp32 atomic modes (one H128 over 64 lanes instead of
+    sixteen rows' worth), whose output must be the general epilogue's bit for bit: row 0 of one-row calls against row
+    0 of the same calls with a second row (which take the general epilogue), for the K-split atomic store at K = 4096
+    and the routed scatter, and against the oracle."""
+    a, packed, svh = synth.make_fat(7, M=2, K=4096, N=512, bits=bits)
+    ref = O.fat_gemm(a[:1], packed, svh, dtype=np.float32)
+    rows = []
+    for m in (1, 2):
+        out = torch.full((m, 512), float("nan"), dtype=torch.float32, device=dev)
+        gp.fat_gemm_v2(t16(a[:m], dev), t16(packed, dev), out, t16(svh, dev), bits, True, False, 1)
+        rows.append(out[0].cpu().numpy())
+    assert O.rel_l2(rows[0][None], ref) < 1e-5
+    assert np.array_equal(rows[0], rows[1])
+    tok = np.array([5, 9], np.int64)
+    rw = np.array([0.625, 0.375], np.float16)
+    scat = []
+    for m in (1, 2):
+        out = torch.zeros(12, 512, dtype=torch.float32, device=dev)
+        gp.fat_gemm_v2_scatter(t16(a[:m], dev), t16(packed, dev), out, t16(svh, dev), t16(tok[:m], dev),
+                               t16(rw[:m], dev), bits, True, False, 1)
+        scat.append(out.cpu().numpy())
+    assert np.array_equal(scat[0][5], scat[1][5])
+    assert O.rel_l2(scat[0][5][None], ref * np.float32(rw[0])) < 1e-5
+    assert not scat[0][9].any()
+
+
 @pytest.mark.parametrize("bits", [2, 3])
 def test_fat_gemm_low_bits(dev, bits):
     a, packed, svh = synth.make_fat(2, M=200, K=1024, N=768, bits=bits)
