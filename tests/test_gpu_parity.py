@@ -707,31 +707,62 @@ def test_fat_gemm_short_k(dev, M, K, bits):
 
 
 @pytest.mark.parametrize("bits", [4, 3, 2])
-def test_one_row_tile_epilogue_bit_identical(dev, bits):
-    """A tile holding one row takes its own epilogue in the fp32 atomic modes (one H128 over 64 lanes instead of
-    sixteen rows' worth), whose output must be the general epilogue's bit for bit: row 0 of one-row calls against row
-    0 of the same calls with a second row (which take the general epilogue), for the K-split atomic store at K = 4096
-    and the routed scatter, and against the oracle."""
-    a, packed, svh = synth.make_fat(7, M=2, K=4096, N=512, bits=bits)
-    ref = O.fat_gemm(a[:1], packed, svh, dtype=np.float32)
-    rows = []
-    for m in (1, 2):
-        out = torch.full((m, 512), float("nan"), dtype=torch.float32, device=dev)
-        gp.fat_gemm_v2(t16(a[:m], dev), t16(packed, dev), out, t16(svh, dev), bits, True, False, 1)
-        rows.append(out[0].cpu().numpy())
-    assert O.rel_l2(rows[0][None], ref) < 1e-5
-    assert np.array_equal(rows[0], rows[1])
-    tok = np.array([5, 9], np.int64)
-    rw = np.array([0.625, 0.375], np.float16)
-    scat = []
-    for m in (1, 2):
-        out = torch.zeros(12, 512, dtype=torch.float32, device=dev)
-        gp.fat_gemm_v2_scatter(t16(a[:m], dev), t16(packed, dev), out, t16(svh, dev), t16(tok[:m], dev),
-                               t16(rw[:m], dev), bits, True, False, 1)
-        scat.append(out.cpu().numpy())
-    assert np.array_equal(scat[0][5], scat[1][5])
-    assert O.rel_l2(scat[0][5][None], ref * np.float32(rw[0])) < 1e-5
-    assert not scat[0][9].any()
+def test_thin_tile_epilogues_bit_identical(dev, bits):
+    """Thin tiles of at most 16 rows (the column-split loop, its results gathered in LDS for wave 0's epilogue; one-row
+    tiles in the fp32 atomic modes take a one-row epilogue, two columns per lane) must give the shared loop's outputs
+    bit for bit. Dense calls of 1, 2, 5 and 16 rows (thin tiles) against the same rows of a 20-row call (the shared
+    loop), for the fp32 store (K = 1024), the K-split fp32 atomic store (K = 4096: two slices added onto zero) and the
+    routed scatter (one add per token), and against the oracle."""
+    M = 20
+    tok = np.random.default_rng(bits).permutation(40)[:M].astype(np.int64)
+    rw = (np.random.default_rng(bits + 1).random(M) * 0.5 + 0.25).astype(np.float16)
+    for K in (1024, 4096):
+        a, packed, svh = synth.make_fat(7 + K, M=M, K=K, N=256, bits=bits)
+        ref = O.fat_gemm(a, packed, svh, dtype=np.float32)
+        outs, scat = {}, {}
+        for m in (1, 2, 5, 16, M):
+            out = torch.full((m, 256), float("nan"), dtype=torch.float32, device=dev)
+            gp.fat_gemm_v2(t16(a[:m], dev), t16(packed, dev), out, t16(svh, dev), bits, True, False, 1)
+            outs[m] = out.cpu().numpy()
+            sc = torch.zeros(40, 256, dtype=torch.float32, device=dev)
+            gp.fat_gemm_v2_scatter(t16(a[:m], dev), t16(packed, dev), sc, t16(svh, dev), t16(tok[:m], dev),
+                                   t16(rw[:m], dev), bits, True, False, 1)
+            scat[m] = sc.cpu().numpy()
+        assert O.rel_l2(outs[M], ref) < 1e-5
+        assert O.rel_l2(scat[M][tok], ref * rw[:, None].astype(np.float32)) < 1e-5
+        for m in (1, 2, 5, 16):
+            assert np.array_equal(outs[m].view(np.uint32), outs[M][:m].view(np.uint32)), (K, m)
+            assert np.array_equal(scat[m][tok[:m]].view(np.uint32), scat[M][tok[:m]].view(np.uint32)), (K, m)
+            assert not np.delete(scat[m], tok[:m], axis=0).any()
+
+
+def test_thin_tile_epilogue_grouped_bit_identical(dev):
+    """The grouped GEMM's thin tiles (64-row tables: the thin kernel, experts of 1-16 rows on the column-split loop)
+    against the same rows on 256-row tiles (the shared loop): the fp16 gate|up rows and the down projection's per-route
+    fp32 rows bit for bit, at the headline routing over 256 tokens."""
+    L, x, ids, w, cfg = synth.make_config("headline", seed=4, T=256)
+    E, H, I = cfg["E"], cfg["H"], cfg["I"]
+    ts, ws, eor, counts, row0 = O.sort_routes(ids, w, E)
+    R = ids.size
+    assert ((counts >= 2) & (counts <= 16)).any() and (counts == 1).any()
+    TL = synth.to_device(L, dev)
+    rng = np.random.default_rng(3)
+    h13 = t16(to_t16(rng.standard_normal((R, H)).astype(np.float16)), dev)
+    act = t16(to_t16(rng.standard_normal((R, I)).astype(np.float16)), dev)
+    ri = torch.from_numpy(np.argsort(ids.reshape(-1), kind="stable").astype(np.int32)).to(dev)
+    res = {}
+    for tr in (64, 256):
+        be, br = gpu_blocks(counts, R, E, dev, tr)
+        gu = torch.full((R, 2 * I), float("nan"), dtype=torch.float16, device=dev)
+        gp.grouped_gemm(h13, TL.w13_trellis[:, 0], TL.w13_trellis[:, 1], TL.w13_svh[:, 0], TL.w13_svh[:, 1], be, br,
+                        t16(counts, dev), t16(row0, dev), None, None, gu, 0, tile_rows=tr, a_layout=1, a_rows=R)
+        part = torch.full((R, H), float("nan"), dtype=torch.float32, device=dev)
+        gp.grouped_gemm(act, TL.w2_trellis, None, TL.w2_svh, None, be, br, t16(counts, dev), t16(row0, dev), None,
+                        t16(ws, dev), part, 2, route_index=ri, tile_rows=tr, a_layout=1, a_rows=R)
+        res[tr] = (gu.cpu().numpy().view(np.uint16), part.cpu().numpy().view(np.uint32))
+    assert not np.isnan(res[64][1].view(np.float32)).any()
+    assert np.array_equal(res[64][0], res[256][0])
+    assert np.array_equal(res[64][1], res[256][1])
 
 
 @pytest.mark.parametrize("bits", [2, 3])
