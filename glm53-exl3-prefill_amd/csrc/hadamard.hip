@@ -11,6 +11,14 @@ namespace exl3 {
 namespace {
 
 constexpr int HAD_THREADS = 256;
+
+// A 16-byte streaming store: the T16 outputs are written once and read by the next launch in another order, long
+// after a cache would have kept them; non-temporal stores keep them from evicting the gathered source rows.
+__device__ __forceinline__ void store_nt(uint16_t* p, const uint4 v)
+{
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(u4{v.x, v.y, v.z, v.w}, reinterpret_cast<u4*>(p));
+}
 constexpr int PAIRS_PER_WG = HAD_THREADS / 16;
 
 template <bool GATHER>
@@ -121,7 +129,7 @@ void row_had_t16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__
             for (int i = 0; i < 4; ++i)
             {
                 const int64_t chunk = g * (K / 8) + blk * 16 + 4 * i + cq;
-                *reinterpret_cast<uint4*>(dst + chunk * 128 + rl * 8) = pack8_scaled(x + 8 * i);
+                store_nt(dst + chunk * 128 + rl * 8, pack8_scaled(x + 8 * i));
             }
     }
 }
@@ -154,7 +162,7 @@ void act_had_t16_kernel(const void* __restrict__ gu, uint16_t* __restrict__ act,
                 #pragma unroll
                 for (int j = 0; j < 8; ++j) o[j] = x[8 * i + j];
                 const int64_t chunk = g * (I / 8) + blk * 16 + 4 * i + cq;
-                *reinterpret_cast<uint4*>(act + chunk * 128 + rl * 8) = pack8(o);
+                store_nt(act + chunk * 128 + rl * 8, pack8(o));
             }
     }
 }
