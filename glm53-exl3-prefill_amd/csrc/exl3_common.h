@@ -86,7 +86,7 @@ int grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layo
                        const int32_t* counts, const int32_t* expert_row0, int n_experts, const int64_t* token_sorted,
                        const uint16_t* route_weight, const int32_t* route_index, void* out, int64_t out_rows, int mode,
                        int k_split, const ActFuse* act, hipStream_t s, float* zero = nullptr,
-                       int64_t zero_floats = 0);
+                       int64_t zero_floats = 0, bool weights_nt = false);
 
 // ------------------------------------------------------------------------------------------- device helpers
 constexpr float HAD_SCALE = 0.088388347648f;     // 1/sqrt(128)

@@ -125,6 +125,13 @@ int k_split_for(int64_t wgs, int stages, int target)
 // of 8 stages 30.6-30.8: each slice adds its partial rows into the same output row, and the act work per slice is
 // spread over the waves either way); 0 when no such split fits one round of `target` workgroups (the gate|up launch
 // then keeps the pass).
+// Whether the gate|up launch and the down launch with the activation pass inside load the trellis words
+// non-temporal (each call reads each active expert's weights once). Measured per call in a step's graph (two
+// alternating runs): one token 25.6-26.0 vs 26.7-26.8 us, 16 tokens 172-177 vs 183-184, 32 tokens 262-266 vs 276-277,
+// 64 tokens 400 vs 403-405; at 2 and 4 tokens the non-temporal loads measured 2.8-3 us slower, at 8 and 128 even. The
+// down launch after a separate activation pass (more than 16 routes) measured slower with them at every size.
+bool decode_weights_nt(int64_t routes) { return routes <= 8 || routes >= 64; }
+
 int k_split_actin(int64_t wgs, int stages, int target)
 {
     if (wgs <= 0 || stages % 4 != 0) return 0;
@@ -442,11 +449,13 @@ extern "C" int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, co
     // 128-column block) computes that block of act from the finished sums. Either way the pass needs no launch of its
     // own.
     const int actin_split = R <= 16 ? k_split_actin((int64_t) L.max_blocks * (hidden / 128), inter / 32, target) : 0;
+    const bool nt = decode_weights_nt(R);
     const ActFuse fuse{act_arrive, act, suh_down, suh2_stride, limit};
     rc = grouped_gemm_split(h13, R, hidden, EXL3_LAYOUT_T16, packed_gate, packed_up, w13_expert_stride_words,
                             hidden / 16, inter / 16, bits, svh_gate, svh_up, svh13_stride, block_expert, block_row0,
                             L.max_blocks, DECODE_TILE_ROWS, counts, expert_row0, n_experts, token_sorted, weight_sorted,
-                            nullptr, gu, R, EXL3_GEMM_ATOMIC_F32, gu_split, actin_split ? nullptr : &fuse, s);
+                            nullptr, gu, R, EXL3_GEMM_ATOMIC_F32, gu_split, actin_split ? nullptr : &fuse, s, nullptr, 0,
+                            nt);
     if (rc) return rc;
     if (actin_split)
     {
@@ -455,7 +464,7 @@ extern "C" int exl3_moe_decode(const uint16_t* x, int64_t tokens, int hidden, co
                                   inter / 16, hidden / 16, bits, svh_down, nullptr, svh2_stride, block_expert,
                                   block_row0, L.max_blocks, DECODE_TILE_ROWS, counts, expert_row0, n_experts,
                                   token_sorted, weight_sorted, nullptr, out, tokens, EXL3_GEMM_SCATTER_F32, actin_split,
-                                  &in, s);
+                                  &in, s, nullptr, 0, nt);
     }
     const int down_split = k_split_for((int64_t) L.max_blocks * (hidden / 128), inter / 32, target);
     return exl3_grouped_gemm_split(act, R, inter, EXL3_LAYOUT_T16, packed_down, nullptr, w2_expert_stride_words,

@@ -110,6 +110,9 @@ struct GemmParams
     // SCATTER_F32 thin tiles of the decode path (trellis_gemm_actin_kernel): the fp32 gate|up sums [rows, 2 I] from
     // which each workgroup computes its own K slice of act into LDS (act_suh / act_suh_stride / act_limit as above)
     const float* act_gu;
+    // the decode path's thin tiles (fp32 atomic modes, grouped) load the trellis words non-temporal: each call reads
+    // each active expert's weights once
+    int weights_nt;
     // a side job of the launch: clear zero[0 .. zero4) (float4s), a buffer a later launch accumulates into
     float4* zero;
     int64_t zero4;
@@ -229,9 +232,11 @@ __device__ __forceinline__ bool resolve_tile(const GemmParams& p, int group, int
 // a = j16 >> 1 and a + 8, rows 4 b .. 4 b + 3 and 8 + 4 b .. with b = j16 & 1.
 template <int N> struct Chunks { Chunk4 c[N]; };
 
-template <int BITS>
+// NT: the raw words are loaded non-temporal (the decode path, whose workgroups read each weight once).
+template <int BITS, bool NT = false>
 struct Decoder
 {
+    static constexpr int AUX = NT ? 2 : 0;                // buffer-load cache policy: 2 = non-temporal
     static constexpr int NDW = 8 * BITS;                  // dwords per tile
     static constexpr int NR = raw_words<BITS>();
     using Out = Chunks<2>;
@@ -275,14 +280,14 @@ struct Decoder
         const int so = min(kb, last_kb) * stage_bytes;
         if constexpr (BITS == 4)
         {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b64(raw, off[0], so, 0);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(raw, off[0], so, AUX);
             r[0] = v[0];
             r[1] = v[1];
         }
         else
         {
             #pragma unroll
-            for (int i = 0; i < NR; ++i) r[i] = __builtin_amdgcn_raw_buffer_load_b32(raw, off[i], so, 0);
+            for (int i = 0; i < NR; ++i) r[i] = __builtin_amdgcn_raw_buffer_load_b32(raw, off[i], so, AUX);
         }
     }
     __device__ __forceinline__ void decode(const uint32_t (&r)[NR], Out& o) const
@@ -879,13 +884,14 @@ __device__ __forceinline__ void act_store(const GemmParams& p, const Tile& t, in
 // loop: there every wave would load all of the tile's activation rows, and a 1024-token layer ran 3.5% slower.)
 // ACT_IN: the activation operand is computed by the workgroup itself (act_load / act_store around the first
 // trellis loads) and read from LDS instead of loaded.
-template <int BITS, int MODE, bool ACT_IN = false>
+// NT: the trellis words are loaded non-temporal (the decode path's kernels, which read each weight once).
+template <int BITS, int MODE, bool ACT_IN = false, bool NT = false>
 __device__ __forceinline__ void thin_tile(const GemmParams& p, const Tile& t, int group, int wave, int lane,
                                           unsigned char* lds_raw)
 {
     uint16_t* lds_b = reinterpret_cast<uint16_t*>(lds_raw);
     const int num_kb = t.num_kb;
-    using Dec = Decoder<BITS>;
+    using Dec = Decoder<BITS, NT>;
     constexpr int NR = Dec::NR;
     const Dec dec(p, t, wave, lane, num_kb, true);
     const Mma mm(p, t, 0, lane, num_kb, 64);                       // the A operand of row group 0
@@ -1140,7 +1146,7 @@ template <int WAVES> constexpr int lds_scatter_bytes() { return WAVES * 16 * SC_
 // workgroups share a CU.
 // WAVES = 8: 512-row tiles, one workgroup per CU; each wave decodes half as much of every stage (one chunk per lane),
 // so a decoded weight feeds twice the rows for the same VALU work per wave.
-template <int BITS, int MODE, bool DENSE, int MBN = 4, int WAVES = 4>
+template <int BITS, int MODE, bool DENSE, int MBN = 4, int WAVES = 4, bool NT = false>
 // (HIP's second launch bound is the minimum number of waves per SIMD: 2 leaves 256 VGPRs per wave, 4 leaves 128.)
 __global__ __launch_bounds__(64 * WAVES, MBN == 4 ? 2 : 4)
 void trellis_gemm_kernel(const GemmParams p)
@@ -1165,7 +1171,7 @@ void trellis_gemm_kernel(const GemmParams p)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (MBN == 1 && t.rows_valid <= 16)                           // uniform over the workgroup
-        thin_tile<BITS, MODE>(p, t, group, wave, lane, lds_raw);
+        thin_tile<BITS, MODE, false, NT>(p, t, group, wave, lane, lds_raw);
     else
         shared_tile<BITS, MODE, MBN, WAVES>(p, t, group, wave, lane, lds_raw, lds_epi + wave);
 }
@@ -1175,7 +1181,7 @@ void trellis_gemm_kernel(const GemmParams p)
 // its first trellis loads are in flight and multiplies it from LDS, so the gate|up launch ends without the pass. The
 // host sends it only calls of at most 16 routes (so no tile holds more than 16 rows) and K slices of whole 128-column
 // act blocks, at most ACTIN_MAX_KB stages each.
-template <int BITS>
+template <int BITS, bool NT>
 __global__ __launch_bounds__(256, 4)
 void trellis_gemm_actin_kernel(const GemmParams p)
 {
@@ -1188,7 +1194,7 @@ void trellis_gemm_actin_kernel(const GemmParams p)
     if (!resolve_tile<false>(p, group, slot, t)) return;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    thin_tile<BITS, MODE_SCATTER_F32, true>(p, t, group, wave, lane, lds_raw);
+    thin_tile<BITS, MODE_SCATTER_F32, true, NT>(p, t, group, wave, lane, lds_raw);
 }
 
 template <int BITS>
@@ -1198,7 +1204,8 @@ int launch_gemm_actin(const GemmParams& p, hipStream_t s)
     const int64_t grid = (int64_t) groups8 * p.n_slots * (p.k_split > 1 ? p.k_split : 1);
     if (grid == 0) return EXL3_OK;
     if (grid > 0x7FFFFFFF) return fail("grid too large");
-    trellis_gemm_actin_kernel<BITS><<<(unsigned) grid, 256, 0, s>>>(p);
+    if (p.weights_nt) trellis_gemm_actin_kernel<BITS, true><<<(unsigned) grid, 256, 0, s>>>(p);
+    else trellis_gemm_actin_kernel<BITS, false><<<(unsigned) grid, 256, 0, s>>>(p);
     return EXL3_OK;
 }
 
@@ -1275,6 +1282,12 @@ int launch_gemm(const GemmParams& p, hipStream_t s)
     if (grid > 0x7FFFFFFF) return fail("grid too large");
     if (p.tile_rows == 64)
     {
+        if constexpr (atomic_mode(MODE) && !DENSE)
+            if (p.weights_nt)
+            {
+                trellis_gemm_kernel<BITS, MODE, DENSE, 1, 4, true><<<(unsigned) grid, 256, 0, s>>>(p);
+                return EXL3_OK;
+            }
         trellis_gemm_kernel<BITS, MODE, DENSE, 1><<<(unsigned) grid, 256, 0, s>>>(p);
         return EXL3_OK;
     }

@@ -232,7 +232,8 @@ int grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layo
                        const int32_t* block_expert, const int32_t* block_row0, int max_blocks, int tile_rows,
                        const int32_t* counts, const int32_t* expert_row0, int n_experts, const int64_t* token_sorted,
                        const uint16_t* route_weight, const int32_t* route_index, void* out, int64_t out_rows, int mode,
-                       int k_split, const ActFuse* act, hipStream_t s, float* zero, int64_t zero_floats)
+                       int k_split, const ActFuse* act, hipStream_t s, float* zero, int64_t zero_floats,
+                       bool weights_nt)
 {
     EXL3_CHECK(tile_rows == 64 || tile_rows == 128 || tile_rows == 256 || tile_rows == 512,
                "tile_rows must be 64, 128, 256 or 512");
@@ -275,6 +276,7 @@ int grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layo
     EXL3_CHECK(zero_floats == 0 || max_blocks > 0, "the clear runs on the GEMM's workgroups: max_blocks must be > 0");
     p.zero = reinterpret_cast<float4*>(zero);
     p.zero4 = zero_floats / 4;
+    p.weights_nt = weights_nt ? 1 : 0;
     if (act && act->gu_in)
     {
         EXL3_CHECK(mode == EXL3_GEMM_SCATTER_F32 && n_tensors == 1 && tile_rows == 64 && a_layout == EXL3_LAYOUT_T16,
