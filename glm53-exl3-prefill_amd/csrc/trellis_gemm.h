@@ -110,8 +110,8 @@ struct GemmParams
     // SCATTER_F32 thin tiles of the decode path (trellis_gemm_actin_kernel): the fp32 gate|up sums [rows, 2 I] from
     // which each workgroup computes its own K slice of act into LDS (act_suh / act_suh_stride / act_limit as above)
     const float* act_gu;
-    // the decode path's thin tiles (fp32 atomic modes, grouped) load the trellis words non-temporal: each call reads
-    // each active expert's weights once
+    // grouped 64-row tiles that read each expert's weights once (the prefill's thin launches, the decode path) load the
+    // trellis words non-temporal
     int weights_nt;
     // a side job of the launch: clear zero[0 .. zero4) (float4s), a buffer a later launch accumulates into
     float4* zero;
@@ -1282,7 +1282,7 @@ int launch_gemm(const GemmParams& p, hipStream_t s)
     if (grid > 0x7FFFFFFF) return fail("grid too large");
     if (p.tile_rows == 64)
     {
-        if constexpr (atomic_mode(MODE) && !DENSE)
+        if constexpr (!DENSE)
             if (p.weights_nt)
             {
                 trellis_gemm_kernel<BITS, MODE, DENSE, 1, 4, true><<<(unsigned) grid, 256, 0, s>>>(p);

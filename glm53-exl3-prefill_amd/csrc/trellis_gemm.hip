@@ -276,7 +276,12 @@ int grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layo
     EXL3_CHECK(zero_floats == 0 || max_blocks > 0, "the clear runs on the GEMM's workgroups: max_blocks must be > 0");
     p.zero = reinterpret_cast<float4*>(zero);
     p.zero4 = zero_floats / 4;
-    p.weights_nt = weights_nt ? 1 : 0;
+    // Thin tables (64-row tiles: each expert's small last tile) in the store modes, the prefill's thin launches, read
+    // each tail expert's weights once: loaded non-temporal, they leave the caches to the data that is read again
+    // (headline 2.083-2.096 vs 2.097-2.108 ms per layer over six alternating runs, most of it in the combine that
+    // follows). The decode path chooses per call (weights_nt).
+    p.weights_nt = (weights_nt || (tile_rows == 64 && (mode == EXL3_GEMM_STORE_F16 || mode == EXL3_GEMM_STORE_F16_T16 ||
+                                                       mode == EXL3_GEMM_STORE_ROUTE_F32))) ? 1 : 0;
     if (act && act->gu_in)
     {
         EXL3_CHECK(mode == EXL3_GEMM_SCATTER_F32 && n_tensors == 1 && tile_rows == 64 && a_layout == EXL3_LAYOUT_T16,
