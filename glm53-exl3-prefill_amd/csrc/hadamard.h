@@ -156,7 +156,12 @@ __device__ __forceinline__ void load_gu8(const void* gu, int64_t idx, float (&x)
         for (int j = 0; j < 8; ++j) x[j] = h2f(f2h(v[j]));
     }
     else
-        unpack8(*reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(gu) + idx), x);
+    {
+        // fp16 gate|up rows are read once here: non-temporal (act_had at the headline 0.058-0.059 vs 0.061 ms)
+        typedef unsigned u4 __attribute__((ext_vector_type(4)));
+        const u4 v = __builtin_nontemporal_load(reinterpret_cast<const u4*>(reinterpret_cast<const uint16_t*>(gu) + idx));
+        unpack8(make_uint4(v[0], v[1], v[2], v[3]), x);
+    }
 }
 
 // Element offset of (r, c) in a T16 [*, W] matrix (c a multiple of 8 here).
