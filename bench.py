@@ -50,16 +50,16 @@ HBM_PEAK_GBS = 8000.0
 STAGE_KERNELS = {
     "sort_routes": ("sort_hist_kernel", "sort_scatter_tiles_kernel"),         # + the tile tables
     "row_had": ("row_had_t16_kernel<true>",),
-    "gemm_gate_up": ("trellis_gemm_kernel<{bits}, 0, false, 4, 4>", "trellis_gemm_kernel<{bits}, 0, false, 1, 4>"),
+    "gemm_gate_up": ("trellis_gemm_kernel<{bits}, 0, false, 4, 4, false>", "trellis_gemm_kernel<{bits}, 0, false, 1, 4, true>"),
     "act_had": ("act_had_t16_kernel<false, true>",),
 }
 # The down projection's stages by output method: the fp32 atomic scatter by token (mode 1), or per-route fp32 rows
 # (mode 2) and their fixed-order sum per token.
 DOWN_STAGE_KERNELS = {
-    "atomic": {"gemm_down_scatter": ("trellis_gemm_kernel<{bits}, 1, false, 4, 4>",
-                                     "trellis_gemm_kernel<{bits}, 1, false, 1, 4>")},
-    "combine": {"gemm_down_routes": ("trellis_gemm_kernel<{bits}, 3, false, 4, 4>",
-                                     "trellis_gemm_kernel<{bits}, 3, false, 1, 4>"),
+    "atomic": {"gemm_down_scatter": ("trellis_gemm_kernel<{bits}, 1, false, 4, 4, false>",
+                                     "trellis_gemm_kernel<{bits}, 1, false, 1, 4, false>")},
+    "combine": {"gemm_down_routes": ("trellis_gemm_kernel<{bits}, 3, false, 4, 4, false>",
+                                     "trellis_gemm_kernel<{bits}, 3, false, 1, 4, true>"),
                 "combine": ("combine_routes_cols_kernel<8, 0>",)},
 }
 
