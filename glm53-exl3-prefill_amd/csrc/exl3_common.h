@@ -78,7 +78,8 @@ struct ActFuse
 };
 
 // exl3_grouped_gemm_split, plus the fused activation pass when `act` is not null and the clear of zero[0 ..
-// zero_floats) as a side job of the same launch (trellis_gemm.hip).
+// zero_floats) as a side job of the same launch (trellis_gemm.hip). weights_nt: 64-row tiles load their trellis words
+// non-temporal (the store modes' 64-row tables always do).
 int grouped_gemm_split(const uint16_t* a, int64_t a_rows, int size_k, int a_layout, const uint16_t* packed_gate,
                        const uint16_t* packed_up, int64_t expert_stride_words, int tiles_k, int tiles_n, int bits,
                        const uint16_t* svh_gate, const uint16_t* svh_up, int64_t svh_stride,
