@@ -232,7 +232,8 @@ __device__ __forceinline__ bool resolve_tile(const GemmParams& p, int group, int
 // a = j16 >> 1 and a + 8, rows 4 b .. 4 b + 3 and 8 + 4 b .. with b = j16 & 1.
 template <int N> struct Chunks { Chunk4 c[N]; };
 
-// NT: the raw words are loaded non-temporal (the decode path, whose workgroups read each weight once).
+// NT: the raw words are loaded non-temporal (64-row tiles that read each weight once: the prefill's thin launches and
+// the decode path).
 template <int BITS, bool NT = false>
 struct Decoder
 {
@@ -884,7 +885,7 @@ __device__ __forceinline__ void act_store(const GemmParams& p, const Tile& t, in
 // loop: there every wave would load all of the tile's activation rows, and a 1024-token layer ran 3.5% slower.)
 // ACT_IN: the activation operand is computed by the workgroup itself (act_load / act_store around the first
 // trellis loads) and read from LDS instead of loaded.
-// NT: the trellis words are loaded non-temporal (the decode path's kernels, which read each weight once).
+// NT: the trellis words are loaded non-temporal (set where each weight is read once; GemmParams::weights_nt).
 template <int BITS, int MODE, bool ACT_IN = false, bool NT = false>
 __device__ __forceinline__ void thin_tile(const GemmParams& p, const Tile& t, int group, int wave, int lane,
                                           unsigned char* lds_raw)
