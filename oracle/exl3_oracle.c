@@ -15,6 +15,10 @@
  *     exllamav3's dq_dispatch<4,1> (kernel/exl3_grouped_prefill.cu:237) and reconstruct
  *     (kernel/test_fat_v2.py:91-94); exllamav3 @ c5d9c657 is not vendored, so the bit order within the
  *     stream is this build's own written spec (stated below).  -> parity unpinned against exllamav3.
+ *     The reference's exllamav3 overlay (kernel/tuned-fused-kernel-patch/exl3patch/exllamav3/exllamav3_ext/
+ *     quant/exl3_gemm_inner.cuh:9,280) includes exl3_dq.cuh and calls dq_dispatch<bits, cb>(shb, lane_id << 3,
+ *     ...), which fixes the eight consecutive positions per lane used below; exl3_dq.cuh itself, where the
+ *     codebook constants and the window extraction live, is not part of the overlay.
  *   - IEEE fp16 <-> fp32 conversion with round-to-nearest-even (the __float2half of the reference's stores).
  *
  * Trellis spec (K = bits per weight, 1 <= K <= 8; the kernels support K in {2, 3, 4}):
